@@ -1,0 +1,205 @@
+// One (64 queries, head, key range) tile of the attention, as a device function: the body of the
+// per-layer `attention_kernel` and a task of the persistent layer kernel, which pass their own
+// LDS. See attention.hip for the design.
+#pragma once
+
+#include "device.h"
+
+namespace jh {
+
+constexpr int ATT_PART = 18;  // f32 per thread in a key-range partial: 16 outputs, max, sum
+
+// LDS f16 attention_tile needs: the K tile [64 keys][72] and the V^T tile [64 d][68].
+constexpr int ATT_LDS_F16 = 64 * 72 + 64 * 68;
+
+// Tile (query block qb, head h), key range `chunk` of p.chunks. Every thread of the block calls
+// it; `lds` holds ATT_LDS_F16 f16 (16-byte aligned). It ends with a block barrier, so the
+// caller may reuse lds right after.
+__device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int h, int chunk,
+                                               f16* lds, uint32_t* s_last) {
+    f16 (*ks)[72] = (f16 (*)[72])lds;              // [key][d], rows of 144 B
+    f16 (*vt)[68] = (f16 (*)[68])(lds + 64 * 72);  // [d][key], rows of 136 B
+    const int n = p.n, d = p.d, ld = 3 * d, heads = d >> 6;
+    const int q0 = qb * 64;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g = l >> 4;
+
+    // Key blocks this tile needs, then this chunk's range of them (possibly empty).
+    const int nb = (n + 63) >> 6;
+    int kb0 = 0, kb1 = nb;
+    if (p.window > 0) {
+        kb0 = max(q0 - p.window, 0) >> 6;
+        kb1 = (min(q0 + 63 + p.window, n - 1) >> 6) + 1;
+    }
+    const int nkb = kb1 - kb0;
+    const int c0 = kb0 + chunk * nkb / p.chunks, c1 = kb0 + (chunk + 1) * nkb / p.chunks;
+
+    // This wave's 16 queries as B operands (two K steps over d = 64).
+    const int qi = q0 + 16 * w + r16;
+    half8 qf[2];
+    {
+        const f16* qp = (const f16*)p.qkv + (size_t)min(qi, n - 1) * ld + h * 64 + 8 * g;
+        qf[0] = *(const half8*)qp;
+        qf[1] = *(const half8*)(qp + 32);
+        if (qi >= n) qf[0] = qf[1] = half8{};
+    }
+
+    // Staging of one key block: thread t loads K chunk (key t / 8, d chunk t % 8) and (t + 256),
+    // and V chunks keyed the other way round (key t % 64, d chunk t / 64 and + 4) so that its
+    // transposed LDS writes are consecutive in the key. Keys past n are zero.
+    half8 kr[2], vr[2];
+    auto gload = [&](int kb) {
+        const int base = kb * 64;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int ck = tid + 256 * u;
+            const int key = base + (ck >> 3);
+            kr[u] = key < n ? *(const half8*)((const f16*)p.qkv + (size_t)key * ld + d + h * 64 + (ck & 7) * 8)
+                            : half8{};
+            const int vkey = base + (tid & 63), vch = (tid >> 6) + 4 * u;
+            vr[u] = vkey < n ? *(const half8*)((const f16*)p.qkv + (size_t)vkey * ld + 2 * d + h * 64 + vch * 8)
+                             : half8{};
+        }
+    };
+    auto lstore = [&]() {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int ck = tid + 256 * u;
+            *(half8*)&ks[ck >> 3][(ck & 7) * 8] = kr[u];
+            const int vkey = tid & 63, vch = (tid >> 6) + 4 * u;
+#pragma unroll
+            for (int e = 0; e < 8; e++) vt[vch * 8 + e][vkey] = vr[u][e];
+        }
+    };
+
+    const float scale = 1.4426950408889634f / 8.0f;  // log2(e) / sqrt(64)
+    float mx = -INFINITY, lsum = 0.0f;
+    floatx4 oacc[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) oacc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    if (c0 < c1) gload(c0);
+    for (int kb = c0; kb < c1; kb++) {
+        __syncthreads();  // the previous block's tiles are no longer read
+        lstore();
+        __syncthreads();
+        if (kb + 1 < c1) gload(kb + 1);
+        const int kbase = kb * 64;
+
+        // S^T for keys 16 t + 4 g + e of this block, query qi.
+        floatx4 s[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            s[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int ks_ = 0; ks_ < 2; ks_++) {
+                const half8 kf = *(const half8*)&ks[16 * t + r16][32 * ks_ + 8 * g];
+                s[t] = mfma16(kf, qf[ks_], s[t]);
+            }
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int key = kbase + 16 * t + 4 * g + e;
+                const int dist = qi > key ? qi - key : key - qi;
+                const bool ok = key < n && (p.window == 0 || dist <= p.window);
+                s[t][e] = ok ? s[t][e] * scale : -INFINITY;
+                bm = fmaxf(bm, s[t][e]);
+            }
+        bm = fmaxf(bm, __shfl_xor(bm, 16));
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        const float mnew = fmaxf(mx, bm);
+        const float base = mnew == -INFINITY ? 0.0f : mnew;  // no valid key yet: exp2(-inf) = 0
+        const float alpha = exp2f(mx - base);
+        mx = mnew;
+        float rs = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                s[t][e] = exp2f(s[t][e] - base);
+                rs += s[t][e];
+            }
+        lsum = lsum * alpha + rs;
+#pragma unroll
+        for (int t = 0; t < 4; t++) oacc[t] *= alpha;
+
+        // O^T += V^T . P^T: K step k2 covers keys 32 k2 .. 32 k2 + 31; lane group g holds keys
+        // 32 k2 + 4 g + (0..3) and 32 k2 + 16 + 4 g + (0..3) (its S^T values of tiles 2 k2 and
+        // 2 k2 + 1), and reads the same keys of V^T.
+#pragma unroll
+        for (int k2 = 0; k2 < 2; k2++) {
+            half8 pf;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                pf[e] = (f16)s[2 * k2][e];
+                pf[4 + e] = (f16)s[2 * k2 + 1][e];
+            }
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                const half4 a = *(const half4*)&vt[16 * dt + r16][32 * k2 + 4 * g];
+                const half4 b = *(const half4*)&vt[16 * dt + r16][32 * k2 + 16 + 4 * g];
+                const half8 vf = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+                oacc[dt] = mfma16(vf, pf, oacc[dt]);
+            }
+        }
+    }
+
+    if (p.chunks > 1) {
+        const int tile = qb * heads + h;
+        float* slots = p.ws + (size_t)tile * p.chunks * ATT_PART * 256;
+        float* mine = slots + (size_t)chunk * ATT_PART * 256 + tid;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) mine[(dt * 4 + e) * 256] = oacc[dt][e];
+        mine[16 * 256] = mx;
+        mine[17 * 256] = lsum;
+        fence_agent();
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t old = atomic_add_agent(p.counters + tile, 1u);
+            const uint32_t last = old == (uint32_t)(p.chunks - 1);
+            if (last) atomic_store_agent(p.counters + tile, 0u);
+            *s_last = last;
+        }
+        __syncthreads();
+        const uint32_t last = *s_last;
+        __syncthreads();  // every thread has read s_last (and is done with the tiles)
+        if (last == 0) return;
+        fence_agent();
+        float m = -INFINITY;
+        for (int z = 0; z < p.chunks; z++) m = fmaxf(m, slots[(size_t)z * ATT_PART * 256 + 16 * 256 + tid]);
+        const float base = m == -INFINITY ? 0.0f : m;
+        lsum = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) oacc[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int z = 0; z < p.chunks; z++) {
+            const float* src = slots + (size_t)z * ATT_PART * 256 + tid;
+            const float f = exp2f(src[16 * 256] - base);
+            lsum += src[17 * 256] * f;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) oacc[dt][e] += src[(dt * 4 + e) * 256] * f;
+        }
+    }
+
+    float tot = lsum + __shfl_xor(lsum, 16);
+    tot += __shfl_xor(tot, 32);
+    const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+    if (qi < n) {
+        f16* op = (f16*)p.o + (size_t)qi * d + h * 64 + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            half4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = (f16)(oacc[dt][e] * inv);
+            *(half4*)(op + 16 * dt) = o;
+        }
+    }
+    __syncthreads();  // the tiles are free again
+}
+
+}  // namespace jh

@@ -1,0 +1,190 @@
+// Device-side building blocks shared by the gfx950 kernels: f16 vector types, the MFMA
+// 16x16x32 f16 step, wave64 reductions, the GELU of the reference and the GEMM epilogue.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.h"
+
+typedef _Float16 f16;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+namespace jh {
+
+// D = A . B + C for a 16 x 16 output, K = 32. Lane l holds row/column (l % 16) of A/B and
+// eight K values (the lane group l / 16 picks which eight; A and B use the same map, so any
+// consistent permutation of K between the two operands gives the same result). The result
+// lane l holds D[4 (l / 16) + i][l % 16], i = 0..3.
+__device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// The sum over each group of `W` consecutive lanes (W a power of two <= 64), to every lane.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int m = W / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// GELU(x) = x Phi(x), with erf(x / sqrt 2) from Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7),
+// the approximation the reference uses (kernels/src/gemm.rs:139-150): t = 1 / (1 + p |x| / sqrt 2)
+// with p = 0.3275911, and 1 - Phi(|x|) = poly(t) exp(-x^2 / 2) / 2.
+__device__ __forceinline__ float gelu(float x) {
+    const float p = 0.3275911f * 0.70710678118654752f;
+    float t = 1.0f / (1.0f + p * fabsf(x));
+    float poly = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t +
+                  0.254829592f) * t;
+    float q = 0.5f * poly * __expf(-0.5f * x * x);
+    return x * (x >= 0.0f ? 1.0f - q : q);
+}
+
+__device__ __forceinline__ float ld_f32(const float* p) { return *p; }
+
+// Agent-scope release/acquire around the cross-block hand-offs (split-K partials, key-range
+// partials, grid barriers): the partial writers' L2 lines reach memory before the arrival is
+// counted, and the last arriver's caches are invalidated before it reads them, which matters on
+// a GPU whose eight XCDs each have their own L2.
+__device__ __forceinline__ void fence_agent() { __threadfence(); }
+
+__device__ __forceinline__ uint32_t atomic_add_agent(uint32_t* p, uint32_t v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void atomic_store_agent(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint32_t atomic_load_agent(const uint32_t* p) {
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Blocks are dispatched to the XCDs round-robin (block b to XCD b % 8). This maps block b to a
+// task index so that each XCD gets one contiguous run of the T tasks: consecutive tasks share a
+// weight tile, so each weight tile is fetched into (mostly) one XCD's L2.
+__device__ __forceinline__ int xcd_task(int b, int T) {
+    const int x = b & 7, j = b >> 3, q = T >> 3, r = T & 7;
+    return x * q + (x < r ? x : r) + j;
+}
+
+// ---- the GEMM epilogue ------------------------------------------------------------------------
+// One thread's share of an output tile: 8 values of row `row`, columns gcol + c0 + e (lo) and
+// gcol + 32 + c0 + e (hi), e < 4, where gcol is a multiple of 64 (the tile's 64-column group
+// `grp`) and c0 a multiple of 4 below 32. The 8 threads sharing a row are 8 consecutive lanes
+// (lane % 8 = c0 / 4), which the statistics reduce over. `valid` is row < m; every thread calls
+// this (the reduction needs the whole group).
+//
+// Order as the reference's gemm_tile (kernels/src/main.rs:931-1038): LayerNorm from the input
+// statistics, bias, ReLU, GELU, RoPE, then GeGLU or the store with the residual and the output
+// statistics of the stored f16 values.
+template <int EPI>
+__device__ __forceinline__ void epilogue(const GemmParams& p, int row, int grp, int c0, float* v,
+                                         bool valid) {
+    const int gcol = grp * 64;
+    if (EPI & EPI_LN) {
+        if (valid) {
+            const int slots = p.k >> 6;
+            const float* st = p.stats_in + (size_t)row * slots * 2;
+            float S = 0.0f, Q = 0.0f;
+            for (int s = 0; s < slots; s++) {
+                S += st[2 * s];
+                Q += st[2 * s + 1];
+            }
+            const float mean = S / (float)p.k;
+            const float var = fmaxf(Q / (float)p.k - mean * mean, 0.0f);
+            const float rs = 1.0f / sqrtf(var + p.eps);
+            const float4 a = *(const float4*)(p.colsum + gcol + c0);
+            const float4 b = *(const float4*)(p.colsum + gcol + 32 + c0);
+            const float cs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = rs * (v[e] - mean * cs[e]);
+        }
+    }
+    if (EPI & EPI_BIAS) {
+        const float4 a = *(const float4*)(p.bias + gcol + c0);
+        const float4 b = *(const float4*)(p.bias + gcol + 32 + c0);
+        const float bs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] += bs[e];
+    }
+    if (EPI & EPI_RELU) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = fmaxf(v[e], 0.0f);
+    }
+    if (EPI & EPI_GELU) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = gelu(v[e]);
+    }
+    if (EPI & EPI_ROPE) {
+        // q and k heads: columns i and i + 32 of a head are the rotate-half pair of dimension i.
+        if (valid && gcol < p.rope_cols) {
+            const int pos = p.pos ? p.pos[row] : row;
+            const float4* t = (const float4*)(p.rope + ((size_t)pos * 32 + c0) * 2);
+            const float4 t0 = t[0], t1 = t[1];
+            const float cs[4] = {t0.x, t0.z, t1.x, t1.z}, sn[4] = {t0.y, t0.w, t1.y, t1.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float x1 = v[e], x2 = v[4 + e];
+                v[e] = x1 * cs[e] - x2 * sn[e];
+                v[4 + e] = x2 * cs[e] + x1 * sn[e];
+            }
+        }
+    }
+    if (EPI & EPI_GEGLU) {
+        // Packed rows 64 grp + e are the input of output column 32 grp + e, + 32 its gate.
+        if (valid) {
+            half4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = (f16)(gelu(v[e]) * v[4 + e]);
+            *(half4*)((f16*)p.c + (size_t)row * (p.n >> 1) + grp * 32 + c0) = o;
+        }
+    } else {
+        half4 lo, hi;
+        f16* out = (f16*)p.c + (size_t)row * p.n + gcol + c0;
+        if (valid) {
+            if (EPI & EPI_RES) {
+                const half4 rl = *(const half4*)out, rh = *(const half4*)(out + 32);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    v[e] += (float)rl[e];
+                    v[4 + e] += (float)rh[e];
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                lo[e] = (f16)v[e];
+                hi[e] = (f16)v[4 + e];
+            }
+            *(half4*)out = lo;
+            *(half4*)(out + 32) = hi;
+        }
+        if (EPI & EPI_STATS) {
+            float s = 0.0f, q = 0.0f;
+            if (valid) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float a = (float)lo[e], b = (float)hi[e];
+                    s += a + b;
+                    q += a * a + b * b;
+                }
+            }
+            s = group_sum<8>(s);
+            q = group_sum<8>(q);
+            if (valid && (threadIdx.x & 7) == 0) {
+                float2* so = (float2*)(p.stats_out + ((size_t)row * (p.n >> 6) + grp) * 2);
+                *so = make_float2(s, q);
+            }
+        }
+    }
+}
+
+}  // namespace jh

@@ -1,0 +1,729 @@
+// The engine and the C ABI (host only). Engine mirrors the reference's src/engine.rs (the model
+// on GPU 0, one stream, weights, scratch; `launch` queues one request, `run` queues 16 and waits
+// once), Encoder/Head mirror src/forward.rs's GpuEncoder and GpuHead, and the extern "C"
+// functions mirror src/capi.rs. Unlike the reference, the activation buffers are allocated once
+// at load for max_length rows (no allocation per request), and the row statistics are per
+// 64-column partial sums (deterministic; no clearing between GEMMs).
+#include <hip/hip_runtime_api.h>
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../include/julia_hip.h"
+#include "kernels.h"
+#include "layer.h"
+#include "weights.h"
+
+using namespace jh;
+
+namespace {
+
+void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+template <typename T>
+T* dalloc(size_t count, const char* what) {
+    void* p = nullptr;
+    hip_check(hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(T)), what);
+    return (T*)p;
+}
+
+constexpr int QUEUE = 16;  // requests queued before waiting (src/engine.rs:26)
+
+}  // namespace
+
+struct Engine {
+    int device = 0, cus = 256;
+    std::string name;
+    hipStream_t stream = nullptr;
+    ModelConfig cfg;
+    Layout layout;
+    jh_half* w16 = nullptr;
+    float* w32 = nullptr;
+    size_t n16 = 0, n32 = 0;
+    int max_length = 0;
+    // Activations for max_length rows.
+    jh_half *x = nullptr, *qkv = nullptr, *o = nullptr, *mid = nullptr, *hx = nullptr;
+    float *stats_a = nullptr, *stats_b = nullptr;
+    // Per queued request: ids, markers and logits on the device and in pinned host memory.
+    uint32_t *ids_d = nullptr, *markers_d = nullptr, *ids_h = nullptr, *markers_h = nullptr;
+    float *logits_d = nullptr, *logits_h = nullptr;
+    hipEvent_t ev_start[QUEUE] = {}, ev_end[QUEUE] = {};
+    Scratch scratch{};
+    LayerKernel layer_kernel;
+
+    const jh_half* h(const Span& s) const { return s.present ? w16 + s.start : nullptr; }
+    const float* f(const Span& s) const { return s.present ? w32 + s.start : nullptr; }
+
+    ~Engine() {
+        if (device >= 0) hipSetDevice(device);
+        if (stream) hipStreamSynchronize(stream);
+        for (int i = 0; i < QUEUE; i++) {
+            if (ev_start[i]) hipEventDestroy(ev_start[i]);
+            if (ev_end[i]) hipEventDestroy(ev_end[i]);
+        }
+        for (void* p : {(void*)w16, (void*)w32, (void*)x, (void*)qkv, (void*)o, (void*)mid,
+                        (void*)hx, (void*)stats_a, (void*)stats_b, (void*)ids_d,
+                        (void*)markers_d, (void*)logits_d, (void*)scratch.ws,
+                        (void*)scratch.counters})
+            if (p) hipFree(p);
+        if (ids_h) hipHostFree(ids_h);
+        if (markers_h) hipHostFree(markers_h);
+        if (logits_h) hipHostFree(logits_h);
+        if (stream) hipStreamDestroy(stream);
+    }
+
+    // ---- the encoder (src/forward.rs GpuEncoder) -------------------------------------------
+    void gemm(int epi, const jh_half* a, const jh_half* w, jh_half* c, int m, int n, int k,
+              const float* stats_in, const float* colsum, float eps, const float* bias,
+              const float* rope, float* stats_out) {
+        Gemm g{};
+        g.epi = epi, g.a = a, g.w = w, g.c = c, g.m = m, g.n = n, g.k = k;
+        g.stats_in = stats_in, g.colsum = colsum, g.eps = eps, g.bias = bias;
+        g.rope = rope, g.pos = nullptr, g.rope_rows = cfg.max_positions, g.stats_out = stats_out;
+        gemm_launch(g, gemm_choose(m, n, k, cus), scratch, stream);
+    }
+
+    // Layer l's five steps as five launches (src/forward.rs:105-165, 361-424): qkv (RoPE; the
+    // LayerNorm folded in from layer 1, from the statistics wo_mlp left in stats_b), attention,
+    // wo (+ residual, statistics into stats_a), wi (LayerNorm from stats_a, GeGLU), wo_mlp
+    // (+ residual, statistics into stats_b).
+    void launch_layer(int l, int n) {
+        const EncoderLayer& L = layout.layers[l];
+        const int d = cfg.d, I = cfg.inter;
+        const float* rope = f(L.global ? layout.rope_global : layout.rope_local);
+        if (L.qkv_colsum.present)
+            gemm(EPI_K_LNROPE, x, h(L.wqkv), qkv, n, 3 * d, d, stats_b, f(L.qkv_colsum),
+                 cfg.norm_eps, nullptr, rope, nullptr);
+        else
+            gemm(EPI_K_ROPE, x, h(L.wqkv), qkv, n, 3 * d, d, nullptr, nullptr, 0.0f, nullptr, rope,
+                 nullptr);
+        const int window = L.global ? 0 : cfg.window;
+        attention_launch(qkv, o, n, d, window, attention_chunks(n, d, window, cus), scratch, stream);
+        gemm(EPI_K_RESSTATS, o, h(L.wo), x, n, d, d, nullptr, nullptr, 0.0f, nullptr, nullptr, stats_a);
+        gemm(EPI_K_LNGEGLU, x, h(L.wi), mid, n, 2 * I, d, stats_a, f(L.wi_colsum), cfg.norm_eps,
+             nullptr, nullptr, nullptr);
+        gemm(EPI_K_RESSTATS, mid, h(L.wo_mlp), x, n, d, I, nullptr, nullptr, 0.0f, nullptr, nullptr,
+             stats_b);
+    }
+
+    // The persistent layer kernel: one cooperative launch per layer.
+    void launch_layer_fused(int l, int n) {
+        const EncoderLayer& L = layout.layers[l];
+        LayerArgs a{};
+        a.x = x, a.qkv = qkv, a.o = o, a.mid = mid, a.stats_attn = stats_a, a.stats_mlp = stats_b;
+        a.wqkv = h(L.wqkv), a.qkv_colsum = f(L.qkv_colsum);
+        a.rope = f(L.global ? layout.rope_global : layout.rope_local);
+        a.wo = h(L.wo), a.wi = h(L.wi), a.wi_colsum = f(L.wi_colsum), a.wo_mlp = h(L.wo_mlp);
+        a.m = n, a.d = cfg.d, a.inter = cfg.inter, a.eps = cfg.norm_eps;
+        a.window = L.global ? 0 : cfg.window;
+        a.rope_rows = cfg.max_positions;
+        layer_kernel.launch(a, layer_kernel.default_plan(n, cfg.d, cfg.inter, a.window), scratch,
+                            stream);
+    }
+
+    // ---- the head (src/forward.rs GpuHead) -------------------------------------------------
+    // The final norm + type embedding (statistics into stats_a), the head layers (in_proj: LN
+    // with bias from stats_a; global attention, no RoPE; out_proj + bias + residual, statistics
+    // into stats_b; linear1: LN from stats_b, bias, ReLU; linear2 + bias + residual, statistics
+    // into stats_a), the scorer's lin1 (LN from stats_a, bias, GELU) and the score.
+    void launch_head(int n, int qtype, const uint32_t* markers, int nm, float* logits) {
+        const int d = cfg.d, F = cfg.head_ff;
+        norm_add_launch(x, n, d, f(layout.final_norm), f(layout.type_emb) + (size_t)qtype * d,
+                        cfg.norm_eps, hx, stats_a, stream);
+        for (const HeadLayer& H : layout.head) {
+            gemm(EPI_K_LNBIAS, hx, h(H.in_proj), qkv, n, 3 * d, d, stats_a, f(H.in_proj_colsum),
+                 cfg.head_eps, f(H.in_proj_b), nullptr, nullptr);
+            attention_launch(qkv, o, n, d, 0, attention_chunks(n, d, 0, cus), scratch, stream);
+            gemm(EPI_K_BIASRESSTATS, o, h(H.out_proj), hx, n, d, d, nullptr, nullptr, 0.0f,
+                 f(H.out_proj_b), nullptr, stats_b);
+            gemm(EPI_K_LNBIASRELU, hx, h(H.linear1), mid, n, F, d, stats_b, f(H.linear1_colsum),
+                 cfg.head_eps, f(H.linear1_b), nullptr, nullptr);
+            gemm(EPI_K_BIASRESSTATS, mid, h(H.linear2), hx, n, d, F, nullptr, nullptr, 0.0f,
+                 f(H.linear2_b), nullptr, stats_a);
+        }
+        const Scorer& S = layout.scorer;
+        gemm(EPI_K_LNBIASGELU, hx, h(S.lin1), o, n, d, d, stats_a, f(S.lin1_colsum), cfg.head_eps,
+             f(S.lin1_b), nullptr, nullptr);
+        score_launch(o, n, d, h(S.lin2), S.lin2_b, markers, nm, logits, stream);
+    }
+
+    // One request's forward pass (src/engine.rs:66-112 `launch`): ids already on the device.
+    void launch(const uint32_t* ids, int n, int qtype, const uint32_t* markers, int nm,
+                float* logits, bool fused) {
+        embed_launch(ids, n, h(layout.tok_embeddings), cfg.vocab, cfg.d, f(layout.emb_norm),
+                     cfg.norm_eps, x, stream);
+        for (int l = 0; l < cfg.layers; l++) {
+            if (fused)
+                launch_layer_fused(l, n);
+            else
+                launch_layer(l, n);
+        }
+        launch_head(n, qtype, markers, nm, logits);
+    }
+};
+
+namespace {
+
+Engine* load_engine(const char* dir, size_t max_length) {
+    if (!dir) throw std::runtime_error("no model given");
+    const ModelConfig spec = parse_model_spec(dir);
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+        throw std::runtime_error("no HIP device is available");
+    std::unique_ptr<Engine> e(new Engine());
+    e->device = 0;
+    hip_check(hipSetDevice(0), "hipSetDevice");
+    hipDeviceProp_t prop;
+    hip_check(hipGetDeviceProperties(&prop, 0), "hipGetDeviceProperties");
+    const std::string arch = prop.gcnArchName;
+    if (arch.compare(0, 6, "gfx950") != 0)
+        throw std::runtime_error(std::string("this library has gfx950 kernels, but ") + prop.name +
+                                 " is " + arch);
+    e->name = prop.name;
+    e->cus = prop.multiProcessorCount;
+    e->cfg = spec;
+    const ModelConfig& c = e->cfg;
+    const size_t ml = max_length ? max_length : (size_t)c.max_positions;
+    if (ml > (size_t)c.max_positions)
+        throw std::runtime_error("max_length " + std::to_string(ml) + " is over the model's " +
+                                 std::to_string(c.max_positions));
+    e->max_length = (int)ml;
+    HostWeights hw = prepare_synthetic(c);
+    e->layout = hw.layout;
+    e->n16 = hw.f16.size(), e->n32 = hw.f32.size();
+    hip_check(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking), "hipStreamCreate");
+    e->w16 = dalloc<jh_half>(e->n16, "weights (f16)");
+    e->w32 = dalloc<float>(e->n32, "weights (f32)");
+    hip_check(hipMemcpy(e->w16, hw.f16.data(), e->n16 * 2, hipMemcpyHostToDevice), "upload");
+    hip_check(hipMemcpy(e->w32, hw.f32.data(), e->n32 * 4, hipMemcpyHostToDevice), "upload");
+
+    const size_t n = ml, d = c.d, wide = std::max<size_t>(c.inter, c.head_ff);
+    e->x = dalloc<jh_half>(n * d, "x");
+    e->qkv = dalloc<jh_half>(n * 3 * d, "qkv");
+    e->o = dalloc<jh_half>(n * d, "o");
+    e->mid = dalloc<jh_half>(n * std::max(wide, d), "mid");
+    e->hx = dalloc<jh_half>(n * d, "hx");
+    e->stats_a = dalloc<float>(n * (d / 64) * 2, "stats");
+    e->stats_b = dalloc<float>(n * (d / 64) * 2, "stats");
+    e->ids_d = dalloc<uint32_t>(QUEUE * n, "ids");
+    e->markers_d = dalloc<uint32_t>(QUEUE * n, "markers");
+    e->logits_d = dalloc<float>(QUEUE * n, "logits");
+    hip_check(hipHostMalloc((void**)&e->ids_h, QUEUE * n * 4, hipHostMallocDefault), "pinned ids");
+    hip_check(hipHostMalloc((void**)&e->markers_h, QUEUE * n * 4, hipHostMallocDefault), "pinned markers");
+    hip_check(hipHostMalloc((void**)&e->logits_h, QUEUE * n * 4, hipHostMallocDefault), "pinned logits");
+    for (int i = 0; i < QUEUE; i++) {
+        hip_check(hipEventCreate(&e->ev_start[i]), "hipEventCreate");
+        hip_check(hipEventCreate(&e->ev_end[i]), "hipEventCreate");
+    }
+
+    // Scratch for the largest split-K / key-range partials any request up to max_length needs.
+    size_t ws = 0, counters = 0;
+    const int shapes[][2] = {{3 * (int)d, (int)d}, {(int)d, (int)d},  {2 * c.inter, (int)d},
+                             {(int)d, c.inter},     {c.head_ff, (int)d}, {(int)d, c.head_ff}};
+    for (int m = 1; m <= (int)ml; m++) {
+        for (auto& s : shapes) {
+            const GemmConfig cfg = gemm_choose(m, s[0], s[1], e->cus);
+            ws = std::max(ws, gemm_ws_floats(m, s[0], cfg));
+            counters = std::max(counters, gemm_counters(m, s[0], cfg));
+        }
+        const int ch = attention_chunks(m, (int)d, 0, e->cus);
+        ws = std::max(ws, attention_ws_floats(m, (int)d, ch));
+        counters = std::max(counters, attention_counters(m, (int)d));
+    }
+    e->layer_kernel.init(e->cus);
+    ws = std::max(ws, e->layer_kernel.ws_floats((int)ml, (int)d, c.inter));
+    counters = std::max(counters, e->layer_kernel.counters((int)ml, (int)d, c.inter));
+    e->scratch.ws = dalloc<float>(ws, "scratch");
+    e->scratch.ws_floats = ws;
+    e->scratch.counters = dalloc<uint32_t>(counters + 64, "counters");
+    e->scratch.n_counters = counters;
+    hip_check(hipMemset(e->scratch.counters, 0, (counters + 64) * 4), "hipMemset");
+    e->layer_kernel.bind(e->scratch.counters + counters);  // the grid barrier's counter
+    hip_check(hipDeviceSynchronize(), "load");
+    return e.release();
+}
+
+struct Request {
+    const uint32_t* ids;
+    size_t n;
+    const uint32_t* markers;
+    size_t nm;
+    uint32_t qtype;
+};
+
+void check_request(const Engine& e, const Request& r, size_t i) {
+    if (r.qtype > 2 || (int)r.qtype >= e.cfg.n_qtypes)
+        throw std::runtime_error("sequence " + std::to_string(i) + ": no question type " +
+                                 std::to_string(r.qtype));
+    if (r.n == 0 || r.n > (size_t)e.max_length)
+        throw std::runtime_error("sequence " + std::to_string(i) + ": " + std::to_string(r.n) +
+                                 " tokens, not 1 to " + std::to_string(e.max_length));
+    for (size_t j = 0; j < r.nm; j++)
+        if (r.markers[j] >= r.n) throw std::runtime_error("a marker is past the sequence");
+    for (size_t j = 0; j < r.n; j++)
+        if (r.ids[j] >= (uint32_t)e.cfg.vocab)
+            throw std::runtime_error("sequence " + std::to_string(i) + ": token id " +
+                                     std::to_string(r.ids[j]) + " is past the vocabulary");
+}
+
+// src/engine.rs:170-196 `Engine::run`: chunks of QUEUE requests, queued back to back (copy in,
+// start event, forward, end event, logits out), then one wait per chunk.
+void run_requests(Engine& e, const std::vector<Request>& reqs, bool fused, float* logits_out,
+                  float* gpu_ms) {
+    hip_check(hipSetDevice(e.device), "hipSetDevice");
+    size_t out_at = 0;
+    for (size_t c0 = 0; c0 < reqs.size(); c0 += QUEUE) {
+        const size_t c1 = std::min(reqs.size(), c0 + QUEUE);
+        for (size_t i = c0; i < c1; i++) check_request(e, reqs[i], i);
+        for (size_t i = c0; i < c1; i++) {
+            const Request& r = reqs[i];
+            const size_t q = i - c0, slot = q * e.max_length;
+            memcpy(e.ids_h + slot, r.ids, r.n * 4);
+            if (r.nm) memcpy(e.markers_h + slot, r.markers, r.nm * 4);
+            hip_check(hipMemcpyAsync(e.ids_d + slot, e.ids_h + slot, r.n * 4, hipMemcpyHostToDevice,
+                                     e.stream), "ids");
+            if (r.nm)
+                hip_check(hipMemcpyAsync(e.markers_d + slot, e.markers_h + slot, r.nm * 4,
+                                         hipMemcpyHostToDevice, e.stream), "markers");
+            hip_check(hipEventRecord(e.ev_start[q], e.stream), "hipEventRecord");
+            e.launch(e.ids_d + slot, (int)r.n, (int)r.qtype, e.markers_d + slot, (int)r.nm,
+                     e.logits_d + slot, fused);
+            hip_check(hipEventRecord(e.ev_end[q], e.stream), "hipEventRecord");
+            if (r.nm)
+                hip_check(hipMemcpyAsync(e.logits_h + slot, e.logits_d + slot, r.nm * 4,
+                                         hipMemcpyDeviceToHost, e.stream), "logits");
+        }
+        hip_check(hipStreamSynchronize(e.stream), "the forward pass");
+        if (fused && e.layer_kernel.barrier_timed_out())
+            throw std::runtime_error("layer: a grid barrier timed out (blocks not co-resident)");
+        for (size_t i = c0; i < c1; i++) {
+            const Request& r = reqs[i];
+            const size_t q = i - c0, slot = q * e.max_length;
+            float ms = 0.0f;
+            hip_check(hipEventElapsedTime(&ms, e.ev_start[q], e.ev_end[q]), "hipEventElapsedTime");
+            for (size_t j = 0; j < r.nm; j++)
+                if (!std::isfinite(e.logits_h[slot + j]))
+                    throw std::runtime_error("inference returned nonfinite logits");
+            if (r.nm) memcpy(logits_out + out_at, e.logits_h + slot, r.nm * 4);
+            out_at += r.nm;
+            if (gpu_ms) gpu_ms[i] = ms;
+        }
+    }
+}
+
+void report(char* err, size_t len, const std::string& msg) {
+    if (!err || len == 0) return;
+    const size_t n = std::min(msg.size(), len - 1);
+    memcpy(err, msg.data(), n);
+    err[n] = 0;
+}
+
+template <typename F>
+int guarded(char* err, size_t len, F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& ex) {
+        report(err, len, ex.what());
+    } catch (...) {
+        report(err, len, "julia-hip: unknown exception");
+    }
+    return -1;
+}
+
+// src/timing.rs:43-74: warm-up calls, then batches of back-to-back calls between two events,
+// one wait at the end; min and median per call.
+template <typename F>
+void time_calls(F&& launch, int warmup, int batches, int per_batch, hipStream_t st,
+                       float* min_us, float* median_us) {
+    if (batches <= 0 || per_batch <= 0) throw std::runtime_error("time: no batches");
+    for (int i = 0; i < warmup; i++) launch();
+    std::vector<hipEvent_t> ev(2 * batches);
+    for (auto& e : ev) hip_check(hipEventCreate(&e), "hipEventCreate");
+    for (int b = 0; b < batches; b++) {
+        hip_check(hipEventRecord(ev[2 * b], st), "hipEventRecord");
+        for (int i = 0; i < per_batch; i++) launch();
+        hip_check(hipEventRecord(ev[2 * b + 1], st), "hipEventRecord");
+    }
+    hip_check(hipStreamSynchronize(st), "time");
+    std::vector<float> us(batches);
+    for (int b = 0; b < batches; b++) {
+        float ms = 0.0f;
+        hip_check(hipEventElapsedTime(&ms, ev[2 * b], ev[2 * b + 1]), "hipEventElapsedTime");
+        us[b] = ms * 1000.0f / per_batch;
+    }
+    for (auto& e : ev) hipEventDestroy(e);
+    std::sort(us.begin(), us.end());
+    if (min_us) *min_us = us[0];
+    if (median_us) *median_us = us[us.size() / 2];
+}
+
+}  // namespace
+
+struct julia_hip_scratch {
+    Scratch s;
+};
+
+extern "C" {
+
+// ---------------------------------------------------------------- Part 1: src/capi.rs
+const char* julia_cuda_tier(void) { return "gfx950"; }
+
+Engine* julia_cuda_load(const char* dir, size_t max_length, char* err, size_t err_len) {
+    Engine* e = nullptr;
+    guarded(err, err_len, [&] { e = load_engine(dir, max_length); });
+    return e;
+}
+
+void julia_cuda_free(Engine* engine) { delete engine; }
+
+void julia_cuda_device(const Engine* engine, char* buf, size_t len) {
+    if (engine) report(buf, len, engine->name);
+}
+
+int julia_cuda_run(const Engine* engine, size_t b, const uint32_t* ids, const size_t* lens,
+                   const uint32_t* markers, const size_t* n_markers, const uint32_t* qtypes,
+                   int layer_fused, float* logits, float* gpu_ms, char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!engine) throw std::runtime_error("no engine");
+        if (b == 0) return;
+        if (!ids || !lens || !n_markers || !qtypes) throw std::runtime_error("null argument");
+        std::vector<Request> reqs(b);
+        size_t at_id = 0, at_m = 0;
+        for (size_t i = 0; i < b; i++) {
+            reqs[i] = Request{ids + at_id, lens[i], markers ? markers + at_m : nullptr, n_markers[i],
+                              qtypes[i]};
+            if (n_markers[i] && !markers) throw std::runtime_error("null markers");
+            at_id += lens[i];
+            at_m += n_markers[i];
+        }
+        if (at_m && !logits) throw std::runtime_error("null logits");
+        run_requests(*const_cast<Engine*>(engine), reqs, layer_fused != 0, logits, gpu_ms);
+    });
+}
+
+// ---------------------------------------------------------------- Part 2: per-op surface
+julia_hip_scratch* julia_hip_scratch_new(size_t ws_floats, size_t counters, char* err,
+                                         size_t err_len) {
+    julia_hip_scratch* s = nullptr;
+    guarded(err, err_len, [&] {
+        std::unique_ptr<julia_hip_scratch> p(new julia_hip_scratch());
+        p->s.ws = dalloc<float>(ws_floats, "scratch");
+        p->s.ws_floats = ws_floats;
+        p->s.counters = dalloc<uint32_t>(counters, "counters");
+        p->s.n_counters = counters;
+        hip_check(hipMemset(p->s.counters, 0, std::max<size_t>(counters, 1) * 4), "hipMemset");
+        hip_check(hipDeviceSynchronize(), "scratch");
+        s = p.release();
+    });
+    return s;
+}
+
+void julia_hip_scratch_free(julia_hip_scratch* s) {
+    if (!s) return;
+    if (s->s.ws) hipFree(s->s.ws);
+    if (s->s.counters) hipFree(s->s.counters);
+    delete s;
+}
+
+static Gemm to_gemm(const julia_hip_gemm_args* g) {
+    if (!g) throw std::runtime_error("gemm: no arguments");
+    Gemm x{};
+    x.epi = g->epi, x.a = (const jh_half*)g->a, x.w = (const jh_half*)g->w, x.c = (jh_half*)g->c;
+    x.m = g->m, x.n = g->n, x.k = g->k, x.stats_in = g->stats_in, x.colsum = g->colsum;
+    x.eps = g->eps, x.bias = g->bias, x.rope = g->rope, x.pos = g->positions;
+    x.rope_rows = g->rope_rows, x.stats_out = g->stats_out;
+    return x;
+}
+
+static int device_cus() {
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess)
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    return cus > 0 ? cus : 256;
+}
+
+static Scratch scratch_of(const julia_hip_scratch* s) { return s ? s->s : Scratch{}; }
+
+int julia_hip_gemm(const julia_hip_gemm_args* g, julia_hip_gemm_config cfg,
+                   const julia_hip_scratch* s, void* stream, char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        const Gemm x = to_gemm(g);
+        GemmConfig c{cfg.bm, cfg.splits};
+        if (c.bm == 0) c = gemm_choose(x.m, x.n, x.k, device_cus());
+        gemm_launch(x, c, scratch_of(s), (hipStream_t)stream);
+    });
+}
+
+int julia_hip_attention(const void* qkv, void* o, int n, int d, int window, int chunks,
+                        const julia_hip_scratch* s, void* stream, char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        const int ch = chunks > 0 ? chunks : attention_chunks(n, d, window, device_cus());
+        attention_launch((const jh_half*)qkv, (jh_half*)o, n, d, window, ch, scratch_of(s),
+                         (hipStream_t)stream);
+    });
+}
+
+int julia_hip_embed(const uint32_t* ids, int n, const void* table, int vocab, int d,
+                    const float* gamma, float eps, void* x, void* stream, char* err,
+                    size_t err_len) {
+    return guarded(err, err_len, [&] {
+        embed_launch(ids, n, (const jh_half*)table, vocab, d, gamma, eps, (jh_half*)x,
+                     (hipStream_t)stream);
+    });
+}
+
+int julia_hip_norm_add(const void* x, int n, int d, const float* gamma, const float* add,
+                       float eps, void* out, float* stats, void* stream, char* err,
+                       size_t err_len) {
+    return guarded(err, err_len, [&] {
+        norm_add_launch((const jh_half*)x, n, d, gamma, add, eps, (jh_half*)out, stats,
+                        (hipStream_t)stream);
+    });
+}
+
+int julia_hip_score(const void* y, int n, int d, const void* w, float b, const uint32_t* markers,
+                    int k, float* logits, void* stream, char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        score_launch((const jh_half*)y, n, d, (const jh_half*)w, b, markers, k, logits,
+                     (hipStream_t)stream);
+    });
+}
+
+int julia_hip_time_gemm(const julia_hip_gemm_args* g, julia_hip_gemm_config cfg,
+                        const julia_hip_scratch* s, int warmup, int batches, int per_batch,
+                        float* min_us, float* median_us, char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        const Gemm x = to_gemm(g);
+        GemmConfig c{cfg.bm, cfg.splits};
+        if (c.bm == 0) c = gemm_choose(x.m, x.n, x.k, device_cus());
+        const Scratch sc = scratch_of(s);
+        gemm_check(x, c, sc);
+        hipStream_t st = nullptr;
+        hip_check(hipStreamCreate(&st), "hipStreamCreate");
+        try {
+            time_calls([&] { gemm_launch(x, c, sc, st); }, warmup, batches, per_batch, st, min_us,
+                       median_us);
+        } catch (...) {
+            hipStreamSynchronize(st);
+            hipStreamDestroy(st);
+            throw;
+        }
+        hipStreamDestroy(st);
+    });
+}
+
+int julia_hip_time_attention(const void* qkv, void* o, int n, int d, int window, int chunks,
+                             const julia_hip_scratch* s, int warmup, int batches, int per_batch,
+                             float* min_us, float* median_us, char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        const int ch = chunks > 0 ? chunks : attention_chunks(n, d, window, device_cus());
+        const Scratch sc = scratch_of(s);
+        hipStream_t st = nullptr;
+        hip_check(hipStreamCreate(&st), "hipStreamCreate");
+        try {
+            time_calls([&] {
+                attention_launch((const jh_half*)qkv, (jh_half*)o, n, d, window, ch, sc, st);
+            }, warmup, batches, per_batch, st, min_us, median_us);
+        } catch (...) {
+            hipStreamSynchronize(st);
+            hipStreamDestroy(st);
+            throw;
+        }
+        hipStreamDestroy(st);
+    });
+}
+
+int julia_hip_copy(void* dst, const void* src, size_t bytes, int kind, char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        const hipMemcpyKind k = kind == 1 ? hipMemcpyHostToDevice
+                                : kind == 2 ? hipMemcpyDeviceToHost
+                                : kind == 3 ? hipMemcpyDeviceToDevice
+                                            : hipMemcpyDefault;
+        hip_check(hipMemcpy(dst, src, bytes, k), "hipMemcpy");
+    });
+}
+
+int julia_hip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+// ---------------------------------------------------------------- Part 3: host-side logic
+void julia_hip_prep_fold_layernorm(const float* w, const float* gamma, int out, int k,
+                                   uint16_t* w16, float* colsum) {
+    fold_layernorm(w, gamma, out, k, w16, colsum);
+}
+
+void julia_hip_prep_fold_layernorm_bias(const float* w, const float* gamma, const float* beta,
+                                        const float* b, int out, int k, uint16_t* w16,
+                                        float* colsum, float* bias) {
+    fold_layernorm_bias(w, gamma, beta, b, out, k, w16, colsum, bias);
+}
+
+void julia_hip_prep_geglu_rows(int inter, int32_t* src) { geglu_rows(inter, src); }
+
+void julia_hip_prep_rope_table(float theta, int npos, float* table) {
+    rope_table(theta, npos, table);
+}
+
+void julia_hip_synth(uint64_t seed, uint32_t id, uint64_t start, uint64_t count, double mean,
+                     double std, float* out) {
+    synth(seed, id, start, count, mean, std, out);
+}
+
+void julia_hip_round_f16(const float* in, uint16_t* out, size_t n) {
+    for (size_t i = 0; i < n; i++) out[i] = f32_to_f16(in[i]);
+}
+
+julia_hip_gemm_config julia_hip_gemm_choose(int m, int n, int k, int cus) {
+    const GemmConfig c = gemm_choose(m, n, k, cus);
+    return julia_hip_gemm_config{c.bm, c.splits};
+}
+
+// src/forward.rs:771-806 `phase_cost`, the 2080 Ti latency model: a task costs 5 us (10 with
+// 64-row tiles) plus 0.35 us per 32-deep K step; c tasks at once on an SM take 1 + 0.2 (c - 1)
+// times one; split tiles add 0.4 us per split and 32 rows; the busiest SM has ceil(tasks / SMs).
+static double phase_cost_2080ti(int n, int cols, int k, int bm, int z, int sms, int per_sm) {
+    const long tasks = (long)(cols / 64) * ((n + bm - 1) / bm) * z;
+    const double steps = (double)(k / 32) / z;
+    const double task = (bm == 32 ? 5.0 : 10.0) + 0.35 * steps;
+    auto at_once = [](long c) { return 1.0 + 0.2 * ((double)c - 1.0); };
+    const long on_sm = (tasks + sms - 1) / sms;
+    const long rounds = on_sm / per_sm, rest = on_sm % per_sm;
+    double t = (double)rounds * at_once(per_sm) * task;
+    if (rest > 0) t += at_once(rest) * task;
+    if (z > 1) t += 0.4 * z * (bm / 32);
+    return t;
+}
+
+// src/forward.rs:759-769 `gemm_plan`: the (bm in {32, 64}, z in 1-4, at least 3 K steps a split)
+// with the lowest phase_cost; ties keep the first.
+void julia_hip_gemm_plan_2080ti(int n, int cols, int k, int sms, int per_sm, int* bm, int* splits) {
+    double best = 1e300;
+    int bb = 32, bz = 1;
+    for (int b : {32, 64})
+        for (int z = 1; z <= 4; z++) {
+            if (k / 32 / z < 3) continue;
+            const double c = phase_cost_2080ti(n, cols, k, b, z, sms, per_sm);
+            if (c < best) best = c, bb = b, bz = z;
+        }
+    if (bm) *bm = bb;
+    if (splits) *splits = bz;
+}
+
+// src/gemm.rs:153-172: tile height by m, and 4 splits only while there are at most half as many
+// tiles as SMs (each split at least 3 K steps).
+julia_hip_gemm_config julia_hip_gemm_choose_2080ti(int m, int n, int k, int sms) {
+    const int bm = m <= 200 ? 32 : (m <= 400 ? 64 : 128);
+    const long tiles = (long)(n / 64) * ((m + bm - 1) / bm);
+    int z = 2 * tiles > sms ? 1 : 4;
+    z = std::min(z, std::max(k / 32 / 3, 1));
+    return julia_hip_gemm_config{bm, z};
+}
+
+int julia_hip_engine_info_get(const Engine* e, julia_hip_engine_info* out) {
+    if (!e || !out) return -1;
+    const ModelConfig& c = e->cfg;
+    out->d = c.d, out->layers = c.layers, out->inter = c.inter, out->vocab = c.vocab;
+    out->head_layers = c.head_layers, out->head_ff = c.head_ff, out->n_qtypes = c.n_qtypes;
+    out->window = c.window, out->global_every = c.global_every;
+    out->max_positions = c.max_positions, out->max_length = e->max_length, out->cus = e->cus;
+    out->norm_eps = c.norm_eps, out->head_eps = c.head_eps, out->seed = c.seed;
+    out->weight_bytes_f16 = e->n16 * 2, out->weight_bytes_f32 = e->n32 * 4;
+    return 0;
+}
+
+const void* julia_hip_engine_tensor(const Engine* e, const char* name, int index, size_t* bytes) {
+    if (!e || !name) return nullptr;
+    const std::string nm = name;
+    const Layout& L = e->layout;
+    const Span* s16 = nullptr;
+    const Span* s32 = nullptr;
+    const bool lok = index >= 0 && index < (int)L.layers.size();
+    const bool hok = index >= 0 && index < (int)L.head.size();
+    if (nm == "tok_emb") s16 = &L.tok_embeddings;
+    else if (nm == "emb_norm") s32 = &L.emb_norm;
+    else if (nm == "rope_global") s32 = &L.rope_global;
+    else if (nm == "rope_local") s32 = &L.rope_local;
+    else if (nm == "final_norm") s32 = &L.final_norm;
+    else if (nm == "type_emb") s32 = &L.type_emb;
+    else if (nm == "wqkv" && lok) s16 = &L.layers[index].wqkv;
+    else if (nm == "qkv_colsum" && lok) s32 = &L.layers[index].qkv_colsum;
+    else if (nm == "wo" && lok) s16 = &L.layers[index].wo;
+    else if (nm == "wi" && lok) s16 = &L.layers[index].wi;
+    else if (nm == "wi_colsum" && lok) s32 = &L.layers[index].wi_colsum;
+    else if (nm == "wo_mlp" && lok) s16 = &L.layers[index].wo_mlp;
+    else if (nm == "in_proj" && hok) s16 = &L.head[index].in_proj;
+    else if (nm == "in_proj_colsum" && hok) s32 = &L.head[index].in_proj_colsum;
+    else if (nm == "in_proj_b" && hok) s32 = &L.head[index].in_proj_b;
+    else if (nm == "out_proj" && hok) s16 = &L.head[index].out_proj;
+    else if (nm == "out_proj_b" && hok) s32 = &L.head[index].out_proj_b;
+    else if (nm == "linear1" && hok) s16 = &L.head[index].linear1;
+    else if (nm == "linear1_colsum" && hok) s32 = &L.head[index].linear1_colsum;
+    else if (nm == "linear1_b" && hok) s32 = &L.head[index].linear1_b;
+    else if (nm == "linear2" && hok) s16 = &L.head[index].linear2;
+    else if (nm == "linear2_b" && hok) s32 = &L.head[index].linear2_b;
+    else if (nm == "lin1") s16 = &L.scorer.lin1;
+    else if (nm == "lin1_colsum") s32 = &L.scorer.lin1_colsum;
+    else if (nm == "lin1_b") s32 = &L.scorer.lin1_b;
+    else if (nm == "lin2") s16 = &L.scorer.lin2;
+    if (s16 && s16->present) {
+        if (bytes) *bytes = s16->len * 2;
+        return e->w16 + s16->start;
+    }
+    if (s32 && s32->present) {
+        if (bytes) *bytes = s32->len * 4;
+        return e->w32 + s32->start;
+    }
+    if (nm == "lin2_b") {
+        if (bytes) *bytes = 0;
+        return nullptr;
+    }
+    return nullptr;
+}
+
+int julia_hip_run_trace(const Engine* ce, const uint32_t* ids, size_t n, const uint32_t* markers,
+                        size_t n_markers, uint32_t qtype, int layer_fused, float* logits,
+                        uint16_t* x_trace, uint16_t* head_x, char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!ce) throw std::runtime_error("no engine");
+        Engine& e = *const_cast<Engine*>(ce);
+        hip_check(hipSetDevice(e.device), "hipSetDevice");
+        const Request r{ids, n, markers, n_markers, qtype};
+        check_request(e, r, 0);
+        hip_check(hipMemcpy(e.ids_d, ids, n * 4, hipMemcpyHostToDevice), "ids");
+        if (n_markers) hip_check(hipMemcpy(e.markers_d, markers, n_markers * 4, hipMemcpyHostToDevice), "markers");
+        const size_t d = e.cfg.d;
+        embed_launch(e.ids_d, (int)n, e.h(e.layout.tok_embeddings), e.cfg.vocab, e.cfg.d,
+                     e.f(e.layout.emb_norm), e.cfg.norm_eps, e.x, e.stream);
+        for (int l = 0; l < e.cfg.layers; l++) {
+            if (layer_fused)
+                e.launch_layer_fused(l, (int)n);
+            else
+                e.launch_layer(l, (int)n);
+            if (x_trace) {
+                hip_check(hipMemcpyAsync(x_trace + (size_t)l * n * d, e.x, n * d * 2,
+                                         hipMemcpyDeviceToHost, e.stream), "trace");
+                hip_check(hipStreamSynchronize(e.stream), "trace");
+            }
+        }
+        e.launch_head((int)n, (int)qtype, e.markers_d, (int)n_markers, e.logits_d);
+        hip_check(hipStreamSynchronize(e.stream), "forward");
+        if (layer_fused && e.layer_kernel.barrier_timed_out())
+            throw std::runtime_error("layer: a grid barrier timed out (blocks not co-resident)");
+        if (head_x) hip_check(hipMemcpy(head_x, e.hx, n * d * 2, hipMemcpyDeviceToHost), "head_x");
+        if (n_markers) hip_check(hipMemcpy(logits, e.logits_d, n_markers * 4, hipMemcpyDeviceToHost), "logits");
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,317 @@
+// The fused-epilogue GEMM family on MFMA (gfx950): c = epilogue(a . w^T), f16 in, f32
+// accumulate, f16 out. The reference's tensor-core GEMM (kernels/src/gemm.rs, gemm_tile in
+// kernels/src/main.rs:886-1041) walks K through shared tiles with 4-8 warps each owning a
+// piece of the output; here two kernels cover the two regimes of a 256-CU GPU:
+//
+//  - gemm_lat (BM = 16/32/64 rows x 64 columns): the small-M, latency-bound regime of one
+//    request (M = 72-1024). Its four waves split K between them (each streams its own a and w
+//    fragments straight from L2 into registers, two K steps in flight, no LDS staging) and
+//    reduce their partial tiles through LDS, so a tile's serial K loop is a quarter as long and
+//    there are more tiles to spread over 256 CUs. Grid split-K on top is deterministic: the
+//    last block of a tile to arrive sums every split's partial in split order.
+//  - gemm_tput (BM = 128/256 x 128): the MFMA-bound regime (M >= 2048): a and w tiles staged
+//    through swizzled LDS, double-buffered, four waves each owning a 64 x 64 (or 128 x 64)
+//    output block.
+//
+// Both hand the finished f32 tile to jh::epilogue (device.h) with the same thread layout.
+#include <algorithm>
+#include <stdexcept>
+#include <string>
+
+#include "gemm_tile.h"
+
+namespace jh {
+
+// ---------------------------------------------------------------------------------------------
+// gemm_lat: grid = tiles_n * tiles_m * splits blocks (1-D, XCD-mapped), 256 threads.
+template <int BM, int EPI>
+__global__ __launch_bounds__(256) void gemm_lat(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) float red[lat_lds_floats<BM>()];
+    __shared__ uint32_t s_last;
+    gemm_lat_tile<BM, EPI>(p, blockIdx.x, red, &s_last);
+}
+
+// ---------------------------------------------------------------------------------------------
+// gemm_tput: BM x 128 tiles (BM = 128 or 256), BK = 64, 4 waves in a 2 x 2 grid, each owning
+// (BM/2) x 64 of the output. a and w tiles go global -> registers -> swizzled LDS, two stages;
+// the next stage's global loads are in flight while the current one feeds the MFMAs.
+//
+// LDS tile rows are 64 f16 (128 B) as eight 16-B chunks; chunk c of row r is stored at chunk
+// c ^ (r & 7), so the 16 rows one fragment load reads spread over all banks.
+template <int BM>
+struct Tput {
+    static constexpr int BN = 128, BK = 64;
+    static constexpr int A_CH = BM * 8, W_CH = BN * 8;  // 16-B chunks per stage
+    static constexpr int A_PER = A_CH / 256, W_PER = W_CH / 256;
+    static constexpr int WM = BM / 2, MI = WM / 16;     // wave rows, m fragments per wave
+    static constexpr int STAGE = (BM + BN) * BK;        // f16 per stage
+};
+
+__device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
+
+template <int BM, int EPI>
+__global__ __launch_bounds__(256) void gemm_tput(GemmParams p) {
+    using C = Tput<BM>;
+    constexpr int NPASS = BM / 32;  // epilogue passes per 64-column group
+    // Two stages of f16 tiles; reused for the f32 output, one 64-column group (BM x 68) at a time.
+    constexpr int LDS_F16 = 2 * C::STAGE;
+    constexpr int OUT_F32 = BM * 68;
+    constexpr int LDS_BYTES = (LDS_F16 * 2 > OUT_F32 * 4) ? LDS_F16 * 2 : OUT_F32 * 4;
+    __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
+    __shared__ uint32_t s_last;
+    f16* sm = (f16*)smem;
+
+    const int T = p.tiles_n * p.tiles_m * p.splits;
+    const int L = xcd_task(blockIdx.x, T);
+    const int z = L % p.splits, t2 = L / p.splits;
+    const int by = t2 % p.tiles_m, bx = t2 / p.tiles_m;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g = l >> 4;
+    const int wm = w >> 1, wn = w & 1;
+
+    const int KT = p.k / C::BK;  // host checks k % 64 == 0 for this kernel
+    const int kt0 = z * KT / p.splits, kt1 = (z + 1) * KT / p.splits;
+
+    // Global chunk assignment: chunk q = tid + 256 h -> row q / 8, chunk q % 8.
+    const f16* ag[C::A_PER];
+    const f16* wg[C::W_PER];
+#pragma unroll
+    for (int h = 0; h < C::A_PER; h++) {
+        const int q = tid + 256 * h, r = q >> 3;
+        ag[h] = (const f16*)p.a + (size_t)min(by * BM + r, p.m - 1) * p.k + (q & 7) * 8;
+    }
+#pragma unroll
+    for (int h = 0; h < C::W_PER; h++) {
+        const int q = tid + 256 * h, r = q >> 3;
+        wg[h] = (const f16*)p.w + (size_t)(bx * C::BN + r) * p.k + (q & 7) * 8;
+    }
+    half8 ra[C::A_PER], rw[C::W_PER];
+    auto gload = [&](int kt) {
+#pragma unroll
+        for (int h = 0; h < C::A_PER; h++) ra[h] = *(const half8*)(ag[h] + kt * C::BK);
+#pragma unroll
+        for (int h = 0; h < C::W_PER; h++) rw[h] = *(const half8*)(wg[h] + kt * C::BK);
+    };
+    auto lstore = [&](int stage) {
+        f16* as = sm + stage * C::STAGE;
+        f16* ws = as + BM * C::BK;
+#pragma unroll
+        for (int h = 0; h < C::A_PER; h++) {
+            const int q = tid + 256 * h;
+            *(half8*)(as + swz(q >> 3, q & 7)) = ra[h];
+        }
+#pragma unroll
+        for (int h = 0; h < C::W_PER; h++) {
+            const int q = tid + 256 * h;
+            *(half8*)(ws + swz(q >> 3, q & 7)) = rw[h];
+        }
+    };
+
+    floatx4 acc[C::MI][4];
+#pragma unroll
+    for (int i = 0; i < C::MI; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    if (kt0 < kt1) {
+        gload(kt0);
+        lstore(0);
+    }
+    __syncthreads();
+    for (int kt = kt0; kt < kt1; kt++) {
+        const int cur = (kt - kt0) & 1;
+        if (kt + 1 < kt1) gload(kt + 1);
+        const f16* as = sm + cur * C::STAGE;
+        const f16* ws = as + BM * C::BK;
+#pragma unroll
+        for (int s = 0; s < 2; s++) {  // two K-32 steps per stage; lane group g takes chunk 4s+g
+            half8 fa[C::MI], fw[4];
+#pragma unroll
+            for (int i = 0; i < C::MI; i++)
+                fa[i] = *(const half8*)(as + swz(wm * C::WM + 16 * i + r16, 4 * s + g));
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                fw[j] = *(const half8*)(ws + swz(wn * 64 + 16 * j + r16, 4 * s + g));
+#pragma unroll
+            for (int i = 0; i < C::MI; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = mfma16(fw[j], fa[i], acc[i][j]);
+        }
+        if (kt + 1 < kt1) lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // The output through LDS (f32, rows of 64 + 4 pad), one 64-column group (the waves with
+    // wn == grp) at a time, into the epilogue layout.
+    float* out = (float*)smem;
+    const int c0 = (tid & 7) * 4;
+#pragma unroll
+    for (int grp = 0; grp < 2; grp++) {
+        if (wn == grp) {
+#pragma unroll
+            for (int i = 0; i < C::MI; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    *(floatx4*)&out[(wm * C::WM + 16 * i + r16) * 68 + 16 * j + 4 * g] = acc[i][j];
+        }
+        __syncthreads();
+        float v[NPASS][8];
+#pragma unroll
+        for (int ps = 0; ps < NPASS; ps++) {
+            const float* src = &out[(ps * 32 + (tid >> 3)) * 68 + c0];
+            const float4 lo = *(const float4*)src, hi = *(const float4*)(src + 32);
+            v[ps][0] = lo.x, v[ps][1] = lo.y, v[ps][2] = lo.z, v[ps][3] = lo.w;
+            v[ps][4] = hi.x, v[ps][5] = hi.y, v[ps][6] = hi.z, v[ps][7] = hi.w;
+        }
+        __syncthreads();  // every thread has read the group before the next one is written
+        // Each 64-column group is its own split-K "tile" (two per block).
+        finish<NPASS, EPI>(p, v, (bx * p.tiles_m + by) * 2 + grp, z, by * BM, bx * 2 + grp, BM,
+                           &s_last);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host side.
+
+namespace {
+
+std::string cfg_str(GemmConfig c) {
+    return std::to_string(c.bm) + "x" + (c.bm >= 128 ? "128" : "64") + " split " +
+           std::to_string(c.splits);
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+size_t gemm_ws_floats(int m, int n, GemmConfig cfg) {
+    if (cfg.splits <= 1) return 0;
+    const int bn = cfg.bm >= 128 ? 128 : 64;
+    const size_t tiles = (size_t)(n / bn) * ((m + cfg.bm - 1) / cfg.bm);
+    const size_t rows = cfg.bm >= 128 ? cfg.bm : (cfg.bm < 32 ? 32 : cfg.bm);
+    return tiles * cfg.splits * rows * bn;
+}
+
+size_t gemm_counters(int m, int n, GemmConfig cfg) {
+    if (cfg.splits <= 1) return 0;
+    const int bn = cfg.bm >= 128 ? 128 : 64;
+    return (size_t)(n / bn) * ((m + cfg.bm - 1) / cfg.bm) * (bn / 64);
+}
+
+void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
+    auto fail = [&](const std::string& msg) { throw std::runtime_error("gemm: " + msg); };
+    if (g.k <= 0 || g.k % 64) fail("k = " + std::to_string(g.k) + " is not a multiple of 64");
+    if (g.m <= 0) fail("no rows");
+    if (g.n <= 0 || g.n % 64) fail("n = " + std::to_string(g.n) + " is not a multiple of 64");
+    const bool tput = cfg.bm >= 128;
+    if (!(cfg.bm == 16 || cfg.bm == 32 || cfg.bm == 64 || cfg.bm == 128 || cfg.bm == 256))
+        fail("no tile height " + std::to_string(cfg.bm));
+    if (tput && g.n % 128) fail("the " + cfg_str(cfg) + " tiles need n % 128 == 0");
+    const int ksteps = tput ? g.k / 64 : g.k / 32;
+    if (cfg.splits < 1 || cfg.splits > 8 || cfg.splits > ksteps)
+        fail(std::to_string(cfg.splits) + " splits for " + std::to_string(ksteps) + " K steps");
+    if (cfg.splits > 1 && (gemm_ws_floats(g.m, g.n, cfg) > s.ws_floats ||
+                           gemm_counters(g.m, g.n, cfg) > s.n_counters || !s.ws || !s.counters))
+        fail("the split-K scratch is too small for m = " + std::to_string(g.m));
+    if (!g.a || !g.w || !g.c) fail("a, w or c is null");
+    if (!aligned(g.a, 16) || !aligned(g.w, 16) || !aligned(g.c, 16))
+        fail("a, w and c must be 16-byte aligned");
+    if ((const void*)g.a == (const void*)g.c) fail("c may not alias a");
+    const bool ln = g.epi & EPI_LN;
+    if (ln != (g.stats_in && g.colsum)) fail("LayerNorm inputs go with the ln epilogues");
+    if (ln && (!aligned(g.colsum, 16) || !aligned(g.stats_in, 8)))
+        fail("colsum must be 16-byte and stats 8-byte aligned");
+    const bool rope = g.epi & EPI_ROPE;
+    if (rope != (g.rope != nullptr)) fail("a RoPE table goes with the rope epilogues");
+    if (rope && (g.n % 192 || (!g.pos && g.rope_rows < g.m) || !aligned(g.rope, 16)))
+        fail("the RoPE table is too short for " + std::to_string(g.m) +
+             " positions, or n = " + std::to_string(g.n) + " isn't qkv");
+    const bool stats = g.epi & EPI_STATS;
+    if (stats != (g.stats_out != nullptr)) fail("output statistics go with the resstats epilogues");
+    if (stats && !aligned(g.stats_out, 8)) fail("stats_out must be 8-byte aligned");
+    const bool bias = g.epi & EPI_BIAS;
+    if (bias != (g.bias != nullptr)) fail("a bias goes with the bias epilogues");
+    if (bias && !aligned(g.bias, 16)) fail("bias must be 16-byte aligned");
+    if ((g.epi & EPI_GEGLU) && (g.epi & (EPI_RES | EPI_STATS | EPI_ROPE)))
+        fail("GeGLU does not combine with a residual, statistics or RoPE");
+    if (stats && (g.stats_out == g.stats_in)) fail("stats_out may not alias stats_in");
+}
+
+template <int BM, int EPI>
+static void launch_one(const GemmParams& p, hipStream_t st) {
+    const int blocks = p.tiles_n * p.tiles_m * p.splits;
+    if (BM >= 128)
+        hipLaunchKernelGGL((gemm_tput<BM >= 128 ? BM : 128, EPI>), dim3(blocks), dim3(256), 0, st, p);
+    else
+        hipLaunchKernelGGL((gemm_lat<BM < 128 ? BM : 64, EPI>), dim3(blocks), dim3(256), 0, st, p);
+}
+
+template <int EPI>
+static void launch_epi(const GemmParams& p, int bm, hipStream_t st) {
+    switch (bm) {
+        case 16: launch_one<16, EPI>(p, st); break;
+        case 32: launch_one<32, EPI>(p, st); break;
+        case 64: launch_one<64, EPI>(p, st); break;
+        case 128: launch_one<128, EPI>(p, st); break;
+        default: launch_one<256, EPI>(p, st); break;
+    }
+}
+
+void gemm_launch(const Gemm& g, GemmConfig cfg, const Scratch& s, hipStream_t st) {
+    gemm_check(g, cfg, s);
+    GemmParams p{};
+    p.a = g.a, p.w = g.w, p.c = g.c;
+    p.stats_in = g.stats_in, p.colsum = g.colsum, p.bias = g.bias, p.rope = g.rope, p.pos = g.pos;
+    p.stats_out = g.stats_out, p.ws = s.ws, p.counters = s.counters;
+    p.m = g.m, p.n = g.n, p.k = g.k, p.eps = g.eps;
+    p.rope_cols = (g.epi & EPI_ROPE) ? 2 * (g.n / 3) : 0;
+    p.splits = cfg.splits;
+    p.tiles_n = g.n / (cfg.bm >= 128 ? 128 : 64);
+    p.tiles_m = (g.m + cfg.bm - 1) / cfg.bm;
+    switch (g.epi) {
+        case EPI_K_ROPE: launch_epi<EPI_K_ROPE>(p, cfg.bm, st); break;
+        case EPI_K_LNROPE: launch_epi<EPI_K_LNROPE>(p, cfg.bm, st); break;
+        case EPI_K_LNGEGLU: launch_epi<EPI_K_LNGEGLU>(p, cfg.bm, st); break;
+        case EPI_K_RESSTATS: launch_epi<EPI_K_RESSTATS>(p, cfg.bm, st); break;
+        case EPI_K_LNBIAS: launch_epi<EPI_K_LNBIAS>(p, cfg.bm, st); break;
+        case EPI_K_LNBIASRELU: launch_epi<EPI_K_LNBIASRELU>(p, cfg.bm, st); break;
+        case EPI_K_LNBIASGELU: launch_epi<EPI_K_LNBIASGELU>(p, cfg.bm, st); break;
+        case EPI_K_BIASRESSTATS: launch_epi<EPI_K_BIASRESSTATS>(p, cfg.bm, st); break;
+        case 0: launch_epi<0>(p, cfg.bm, st); break;
+        default: throw std::runtime_error("gemm: no kernel for epilogue " + std::to_string(g.epi));
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        throw std::runtime_error(std::string("gemm (") + cfg_str(cfg) + "): " + hipGetErrorString(e));
+}
+
+// The tiling for one request's GEMMs on a 256-CU GPU. Small M is latency-bound: what matters is
+// the longest chain of dependent K steps on the busiest CU. The model: a latency-kernel task
+// costs a fixed part plus a part per K step of its wave (K / 32 / 4 / splits steps), growing a
+// little with the tile height; tasks fill the CUs in rounds; split-K adds a reduction. Large M
+// goes to the throughput kernel's 128- or 256-row tiles.
+GemmConfig gemm_choose(int m, int n, int k, int cus) {
+    if (cus <= 0) cus = 256;
+    if (m >= 2048 && n % 128 == 0 && k % 64 == 0) {
+        const long t256 = (long)(n / 128) * ((m + 255) / 256);
+        return GemmConfig{t256 >= cus ? 256 : 128, 1};
+    }
+    GemmConfig best{64, 1};
+    double best_cost = 1e30;
+    const int units = k / 32;
+    for (int bm : {16, 32, 64}) {
+        for (int s = 1; s <= 4; s++) {
+            if (units / (4 * s) < 2) continue;
+            const long tasks = (long)(n / 64) * ((m + bm - 1) / bm) * s;
+            const int per_cu = bm == 64 ? 2 : 4;  // resident tiles per CU (LDS, waves)
+            const long rounds = (tasks + (long)cus * per_cu - 1) / ((long)cus * per_cu);
+            const double busy = (double)std::min<long>(tasks, (long)cus * per_cu) / cus;
+            const double steps = (double)units / (4.0 * s);
+            const double task = 2.0 + steps * (0.12 + 0.03 * (bm / 16)) * (0.75 + 0.25 * busy);
+            double cost = (double)rounds * task + (s > 1 ? 1.0 + 0.1 * s : 0.0);
+            if (cost < best_cost - 1e-9) best_cost = cost, best = GemmConfig{bm, s};
+        }
+    }
+    return best;
+}
+
+}  // namespace jh

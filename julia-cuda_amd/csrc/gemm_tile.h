@@ -1,0 +1,176 @@
+// One output tile of the latency GEMM (BM = 16/32/64 rows x 64 columns), as a device function:
+// the body of the per-GEMM `gemm_lat` kernels and a task of the persistent layer kernel, which
+// pass their own LDS. See gemm.hip for the design.
+#pragma once
+
+#include "device.h"
+
+namespace jh {
+
+// LDS floats gemm_lat_tile<BM> needs: four waves' partial BM x 64 tiles, rows padded to 68.
+template <int BM>
+constexpr int lat_lds_floats() { return 4 * BM * 68; }
+
+// Shared tail: each thread's 8 values (K fully summed within the block) -> the split-K
+// reduction when the grid splits K -> the epilogue. Thread t owns row (pass * 32 + t / 8) of the
+// tile and columns c0 = 4 (t % 8), c0 + 32 of 64-column group `grp`.
+//
+// Split-K (kernels/src/gemm.rs:355-433): every block writes its partial to the scratch, then
+// counts its arrival; the last of the tile's splits (which resets the counter) sums all partials
+// in split order, so the result does not depend on arrival order.
+template <int NPASS, int EPI>
+__device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8], int tile_id,
+                                       int z, int row0, int grp, int rows_in_tile,
+                                       uint32_t* s_last) {
+    const int tid = threadIdx.x;
+    if (p.splits > 1) {
+        // [tile][split][pass][half][thread] float4s: coalesced stores and loads.
+        float* part = p.ws + (size_t)(tile_id * p.splits) * NPASS * 2 * 256 * 4;
+        float* mine = part + (size_t)z * NPASS * 2 * 256 * 4;
+#pragma unroll
+        for (int ps = 0; ps < NPASS; ps++)
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+                *(float4*)(mine + ((ps * 2 + h) * 256 + tid) * 4) =
+                    make_float4(v[ps][4 * h], v[ps][4 * h + 1], v[ps][4 * h + 2], v[ps][4 * h + 3]);
+        fence_agent();
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t old = atomic_add_agent(p.counters + tile_id, 1u);
+            const uint32_t last = old == (uint32_t)(p.splits - 1);
+            if (last) atomic_store_agent(p.counters + tile_id, 0u);
+            *s_last = last;
+        }
+        __syncthreads();
+        const uint32_t last = *s_last;
+        __syncthreads();  // every thread has read s_last before anyone can write it again
+        if (last == 0) return;
+        fence_agent();
+#pragma unroll
+        for (int ps = 0; ps < NPASS; ps++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[ps][e] = 0.0f;
+        for (int zz = 0; zz < p.splits; zz++) {
+            const float* src = part + (size_t)zz * NPASS * 2 * 256 * 4;
+#pragma unroll
+            for (int ps = 0; ps < NPASS; ps++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const float4 q = *(const float4*)(src + ((ps * 2 + h) * 256 + tid) * 4);
+                    v[ps][4 * h] += q.x;
+                    v[ps][4 * h + 1] += q.y;
+                    v[ps][4 * h + 2] += q.z;
+                    v[ps][4 * h + 3] += q.w;
+                }
+        }
+    }
+    const int c0 = (tid & 7) * 4;
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ps++) {
+        const int r = ps * 32 + (tid >> 3);
+        const int row = row0 + r;
+        epilogue<EPI>(p, row, grp, c0, v[ps], r < rows_in_tile && row < p.m);
+    }
+}
+
+// Task `task` (of tiles_n * tiles_m * splits; XCD-mapped) of c = epilogue(a . w^T). The four
+// waves split the tile's K steps between them; `red` is lat_lds_floats<BM>() floats of LDS.
+// Every thread of the block calls it; it ends with a block barrier, so the caller may reuse
+// `red` right after.
+template <int BM, int EPI>
+__device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, float* red,
+                                              uint32_t* s_last) {
+    constexpr int MI = BM / 16;
+    constexpr int NPASS = (BM + 31) / 32;
+    const int T = p.tiles_n * p.tiles_m * p.splits;
+    const int L = xcd_task(task, T);
+    const int z = L % p.splits, t2 = L / p.splits;
+    const int by = t2 % p.tiles_m, bx = t2 / p.tiles_m;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g = l >> 4;
+
+    // This block's K steps (32 wide), then this wave's quarter of them.
+    const int U = p.k >> 5;
+    const int ub = z * U / p.splits, ue = (z + 1) * U / p.splits, nu = ue - ub;
+    const int u0 = ub + w * nu / 4, u1 = ub + (w + 1) * nu / 4;
+
+    const f16* ap[MI];
+    const f16* wp[4];
+#pragma unroll
+    for (int i = 0; i < MI; i++) {
+        const int row = min(by * BM + 16 * i + r16, p.m - 1);  // rows past m: read, never stored
+        ap[i] = (const f16*)p.a + (size_t)row * p.k + 8 * g;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) wp[j] = (const f16*)p.w + (size_t)(bx * 64 + 16 * j + r16) * p.k + 8 * g;
+
+    floatx4 acc[MI][4];
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Two K steps in flight: the next step's fragments load while the current one multiplies.
+    half8 fa0[MI], fw0[4], fa1[MI], fw1[4];
+    int u = u0;
+    if (u < u1) {
+#pragma unroll
+        for (int i = 0; i < MI; i++) fa0[i] = *(const half8*)(ap[i] + u * 32);
+#pragma unroll
+        for (int j = 0; j < 4; j++) fw0[j] = *(const half8*)(wp[j] + u * 32);
+    }
+    for (; u < u1; u += 2) {
+        if (u + 1 < u1) {
+#pragma unroll
+            for (int i = 0; i < MI; i++) fa1[i] = *(const half8*)(ap[i] + (u + 1) * 32);
+#pragma unroll
+            for (int j = 0; j < 4; j++) fw1[j] = *(const half8*)(wp[j] + (u + 1) * 32);
+        }
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] = mfma16(fw0[j], fa0[i], acc[i][j]);
+        if (u + 1 < u1) {
+            if (u + 2 < u1) {
+#pragma unroll
+                for (int i = 0; i < MI; i++) fa0[i] = *(const half8*)(ap[i] + (u + 2) * 32);
+#pragma unroll
+                for (int j = 0; j < 4; j++) fw0[j] = *(const half8*)(wp[j] + (u + 2) * 32);
+            }
+#pragma unroll
+            for (int i = 0; i < MI; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = mfma16(fw1[j], fa1[i], acc[i][j]);
+        }
+    }
+
+    // acc[i][j] lane: row 16 i + r16, columns 16 j + 4 g + e of the tile. Wave w's partial at
+    // red[w][row][col] (rows of 68 floats).
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            *(floatx4*)&red[(w * BM + 16 * i + r16) * 68 + 16 * j + 4 * g] = acc[i][j];
+    __syncthreads();
+
+    float v[NPASS][8];
+    const int c0 = (tid & 7) * 4;
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ps++) {
+        const int r = ps * 32 + (tid >> 3);
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[ps][e] = 0.0f;
+        if (r < BM) {
+#pragma unroll
+            for (int ww = 0; ww < 4; ww++) {
+                const float4 lo = *(const float4*)&red[(ww * BM + r) * 68 + c0];
+                const float4 hi = *(const float4*)&red[(ww * BM + r) * 68 + 32 + c0];
+                v[ps][0] += lo.x, v[ps][1] += lo.y, v[ps][2] += lo.z, v[ps][3] += lo.w;
+                v[ps][4] += hi.x, v[ps][5] += hi.y, v[ps][6] += hi.z, v[ps][7] += hi.w;
+            }
+        }
+    }
+    __syncthreads();  // red is free again
+    finish<NPASS, EPI>(p, v, bx * p.tiles_m + by, z, by * BM, bx, BM, s_last);
+}
+
+}  // namespace jh

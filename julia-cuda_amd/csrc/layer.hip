@@ -1,0 +1,267 @@
+// The persistent layer kernel (the reference's `layer`, kernels/src/main.rs:578-842): one
+// encoder layer as one cooperative launch. Its five steps are phases (qkv, attention, wo, wi,
+// wo_mlp); every block strides over a phase's tasks (the per-step kernels' own tile functions,
+// so the arithmetic is theirs), with a grid barrier between two selected phases. The grid is at
+// most the number of blocks resident at once (the cooperative launch checks it), a multiple of
+// 8 so that task t runs on XCD t % 8 as in the per-step kernels.
+//
+// The row statistics need no clearing phase here: the resstats epilogue writes (not adds) one
+// partial per row and 64-column group.
+#include <algorithm>
+#include <stdexcept>
+#include <string>
+
+#include "attn_tile.h"
+#include "gemm_tile.h"
+#include "layer.h"
+
+namespace jh {
+
+struct LayerParams {
+    GemmParams g[4];  // qkv, wo, wi, wo_mlp
+    AttnParams at;
+    int bm[4];
+    int epi0;         // EPI_K_ROPE (layer 0) or EPI_K_LNROPE
+    unsigned phases;  // bits 0-4
+    uint32_t* bar;    // bar[0]: arrivals (monotonic), bar[1]: set when a barrier timed out
+    uint32_t bar_base;
+};
+
+// A barrier across the grid on a monotonic arrival counter: block b's k-th barrier of this launch
+// waits until the count reaches bar_base + k * grid (compared with wrap-around). Every thread
+// releases its writes at agent scope before the block arrives, and acquires after, so everything
+// written before the barrier is visible to every block after it, through ordinary loads, across
+// the XCDs' separate L2s (kernels/src/gemm.rs:435-489 is the reference's). The wait is bounded:
+// past ~0.2 s (far beyond any real barrier) it gives up and raises bar[1], which the host turns
+// into an error, so a broken launch cannot hang the GPU.
+__device__ __forceinline__ void grid_sync(uint32_t* bar, uint32_t target) {
+    fence_agent();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        atomic_add_agent(bar, 1u);
+        const uint64_t t0 = wall_clock64();
+        while ((int32_t)(atomic_load_agent(bar) - target) < 0) {
+            __builtin_amdgcn_s_sleep(1);
+            if (wall_clock64() - t0 > 20000000ull) {
+                __hip_atomic_store(bar + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    fence_agent();
+}
+
+constexpr int LAYER_LDS_FLOATS = lat_lds_floats<32>();
+static_assert(ATT_LDS_F16 / 2 <= LAYER_LDS_FLOATS, "attention tiles fit the GEMM's LDS");
+
+template <int EPI>
+__device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, float* lds,
+                                           uint32_t* s_last) {
+    const int T = g.tiles_n * g.tiles_m * g.splits;
+    for (int t = blockIdx.x; t < T; t += gridDim.x) {
+        if (bm == 16)
+            gemm_lat_tile<16, EPI>(g, t, lds, s_last);
+        else
+            gemm_lat_tile<32, EPI>(g, t, lds, s_last);
+    }
+}
+
+__global__ __launch_bounds__(256) void layer_kernel(LayerParams P) {
+    __shared__ __attribute__((aligned(16))) float lds[LAYER_LDS_FLOATS];
+    __shared__ uint32_t s_last;
+    const uint32_t grid = gridDim.x;
+    uint32_t nbar = 0;
+    auto on = [&](int ph) { return (P.phases >> ph) & 1u; };
+    auto sync_if = [&](int next) {
+        if (on(next)) {
+            nbar++;
+            grid_sync(P.bar, P.bar_base + nbar * grid);
+        }
+    };
+    if (on(0)) {
+        if (P.epi0 == EPI_K_LNROPE)
+            gemm_phase<EPI_K_LNROPE>(P.g[0], P.bm[0], lds, &s_last);
+        else
+            gemm_phase<EPI_K_ROPE>(P.g[0], P.bm[0], lds, &s_last);
+        sync_if(1);
+    }
+    if (on(1)) {
+        const AttnParams& a = P.at;
+        const int heads = a.d >> 6, T = ((a.n + 63) >> 6) * heads * a.chunks;
+        for (int t = blockIdx.x; t < T; t += gridDim.x) {
+            const int tile = t / a.chunks;
+            attention_tile(a, tile / heads, tile % heads, t % a.chunks, (f16*)lds, &s_last);
+        }
+        sync_if(2);
+    }
+    if (on(2)) {
+        gemm_phase<EPI_K_RESSTATS>(P.g[1], P.bm[1], lds, &s_last);
+        sync_if(3);
+    }
+    if (on(3)) {
+        gemm_phase<EPI_K_LNGEGLU>(P.g[2], P.bm[2], lds, &s_last);
+        sync_if(4);
+    }
+    if (on(4)) gemm_phase<EPI_K_RESSTATS>(P.g[3], P.bm[3], lds, &s_last);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Host side.
+
+std::string LayerPlan::str() const {
+    static const char* names[4] = {"qkv", "wo", "wi", "wo_mlp"};
+    std::string s;
+    for (int g = 0; g < 4; g++)
+        s += std::string(names[g]) + " " + std::to_string(bm[g]) + "/" + std::to_string(splits[g]) + " ";
+    return s + "kv " + std::to_string(kv[0]) + "/" + std::to_string(kv[1]);
+}
+
+void LayerKernel::init(int cus) {
+    cus_ = cus > 0 ? cus : 256;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(layer_kernel),
+                                                     256, 0) != hipSuccess)
+        n = 0;
+    per_cu_ = n;
+}
+
+static void shapes(int d, int inter, int cols[4], int ks[4]) {
+    cols[0] = 3 * d, ks[0] = d;
+    cols[1] = d, ks[1] = d;
+    cols[2] = 2 * inter, ks[2] = d;
+    cols[3] = d, ks[3] = inter;
+}
+
+// Per GEMM the latency chooser's pick, limited to the layer kernel's tile heights (16 and 32
+// rows, which keep the kernel's LDS at 34.8 KB); key ranges for global attention as the
+// per-step attention's, none for sliding-window layers (src/forward.rs:173-189's rule).
+LayerPlan LayerKernel::default_plan(int m, int d, int inter, int window) const {
+    LayerPlan p{};
+    int cols[4], ks[4];
+    shapes(d, inter, cols, ks);
+    for (int g = 0; g < 4; g++) {
+        GemmConfig c = gemm_choose(std::min(m, 1024), cols[g], ks[g], cus_);
+        if (c.bm > 32) c = GemmConfig{32, c.bm >= 128 ? 1 : c.splits};
+        p.bm[g] = c.bm, p.splits[g] = c.splits;
+    }
+    p.kv[0] = attention_chunks(m, d, 0, cus_);
+    p.kv[1] = 1;
+    (void)window;
+    return p;
+}
+
+size_t LayerKernel::ws_floats(int max_m, int d, int inter) const {
+    size_t ws = 0;
+    int cols[4], ks[4];
+    shapes(d, inter, cols, ks);
+    for (int m = 1; m <= max_m; m++) {
+        const LayerPlan p = default_plan(m, d, inter, 0);
+        for (int g = 0; g < 4; g++)
+            ws = std::max(ws, gemm_ws_floats(m, cols[g], GemmConfig{p.bm[g], p.splits[g]}));
+        ws = std::max(ws, attention_ws_floats(m, d, p.kv[0]));
+    }
+    return ws;
+}
+
+size_t LayerKernel::counters(int max_m, int d, int inter) const {
+    size_t c = attention_counters(max_m, d);
+    int cols[4], ks[4];
+    shapes(d, inter, cols, ks);
+    for (int g = 0; g < 4; g++) c = std::max(c, gemm_counters(max_m, cols[g], GemmConfig{16, 2}));
+    return c;
+}
+
+static void fill(GemmParams& p, const Gemm& g, GemmConfig c, const Scratch& s) {
+    p = GemmParams{};
+    p.a = g.a, p.w = g.w, p.c = g.c, p.stats_in = g.stats_in, p.colsum = g.colsum;
+    p.bias = g.bias, p.rope = g.rope, p.pos = g.pos, p.stats_out = g.stats_out;
+    p.ws = s.ws, p.counters = s.counters;
+    p.m = g.m, p.n = g.n, p.k = g.k, p.eps = g.eps;
+    p.rope_cols = (g.epi & EPI_ROPE) ? 2 * (g.n / 3) : 0;
+    p.splits = c.splits, p.tiles_n = g.n / 64, p.tiles_m = (g.m + c.bm - 1) / c.bm;
+}
+
+int LayerKernel::grid(const LayerArgs& a, const LayerPlan& plan) const {
+    int cols[4], ks[4];
+    shapes(a.d, a.inter, cols, ks);
+    long most = (long)((a.m + 63) / 64) * (a.d / 64) * plan.kv[a.window > 0 ? 1 : 0];
+    for (int g = 0; g < 4; g++)
+        most = std::max(most, (long)(cols[g] / 64) * ((a.m + plan.bm[g] - 1) / plan.bm[g]) * plan.splits[g]);
+    long grid = std::min<long>((long)per_cu_ * cus_, most);
+    if (grid > 8) grid -= grid % 8;
+    return (int)std::max<long>(grid, 1);
+}
+
+void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratch& s,
+                         hipStream_t stream, unsigned phases) {
+    auto fail = [&](const std::string& m) { throw std::runtime_error("layer: " + m); };
+    if (per_cu_ <= 0) fail("the layer kernel does not fit on a CU");
+    if (!bar_) fail("no grid-barrier counter");
+    for (int g = 0; g < 4; g++)
+        if (!(plan.bm[g] == 16 || plan.bm[g] == 32) || plan.splits[g] < 1 || plan.splits[g] > 4)
+            fail("no such plan: " + plan.str());
+    const int kv = plan.kv[a.window > 0 ? 1 : 0];
+    if (kv < 1 || kv > 8) fail("no such plan: " + plan.str());
+    if (phases == 0 || phases > 0x1f) fail("no phases selected");
+
+    const bool ln0 = a.qkv_colsum != nullptr;
+    Gemm g[4] = {};
+    g[0].epi = ln0 ? EPI_K_LNROPE : EPI_K_ROPE, g[0].a = a.x, g[0].w = a.wqkv, g[0].c = a.qkv;
+    g[0].m = a.m, g[0].n = 3 * a.d, g[0].k = a.d, g[0].eps = a.eps, g[0].rope = a.rope;
+    g[0].rope_rows = a.rope_rows;
+    if (ln0) g[0].stats_in = a.stats_mlp, g[0].colsum = a.qkv_colsum;
+    g[1].epi = EPI_K_RESSTATS, g[1].a = a.o, g[1].w = a.wo, g[1].c = a.x, g[1].m = a.m;
+    g[1].n = a.d, g[1].k = a.d, g[1].stats_out = a.stats_attn;
+    g[2].epi = EPI_K_LNGEGLU, g[2].a = a.x, g[2].w = a.wi, g[2].c = a.mid, g[2].m = a.m;
+    g[2].n = 2 * a.inter, g[2].k = a.d, g[2].stats_in = a.stats_attn, g[2].colsum = a.wi_colsum;
+    g[2].eps = a.eps;
+    g[3].epi = EPI_K_RESSTATS, g[3].a = a.mid, g[3].w = a.wo_mlp, g[3].c = a.x, g[3].m = a.m;
+    g[3].n = a.d, g[3].k = a.inter, g[3].stats_out = a.stats_mlp;
+
+    LayerParams P{};
+    for (int i = 0; i < 4; i++) {
+        const GemmConfig c{plan.bm[i], plan.splits[i]};
+        gemm_check(g[i], c, s);
+        fill(P.g[i], g[i], c, s);
+        P.bm[i] = plan.bm[i];
+    }
+    if (kv > 1 && (attention_ws_floats(a.m, a.d, kv) > s.ws_floats ||
+                   attention_counters(a.m, a.d) > s.n_counters))
+        fail("the key-range scratch is too small for " + std::to_string(a.m) + " tokens");
+    P.at = AttnParams{a.qkv, a.o, a.m, a.d, a.window, kv, s.ws, s.counters};
+    P.epi0 = g[0].epi;
+    P.phases = phases;
+    P.bar = bar_;
+    P.bar_base = bar_count_;
+
+    const int grid_blocks = grid(a, plan);
+    // A barrier between two consecutive selected phases only (the kernel's sync_if).
+    unsigned barriers = 0;
+    for (int ph = 1; ph < 5; ph++)
+        if (((phases >> ph) & 1) && ((phases >> (ph - 1)) & 1)) barriers++;
+    void* args[] = {&P};
+    hipError_t e;
+    if (barriers > 0)
+        e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(layer_kernel), dim3(grid_blocks),
+                                       dim3(256), args, 0, stream);
+    else
+        e = hipLaunchKernel(reinterpret_cast<const void*>(layer_kernel), dim3(grid_blocks),
+                            dim3(256), args, 0, stream);
+    if (e != hipSuccess) fail(std::string(hipGetErrorString(e)) + " (" + plan.str() + ", grid " +
+                              std::to_string(grid_blocks) + ")");
+    bar_count_ += barriers * (uint32_t)grid_blocks;
+}
+
+bool LayerKernel::barrier_timed_out() {
+    if (!bar_) return false;
+    uint32_t flag = 0;
+    if (hipMemcpy(&flag, bar_ + 1, 4, hipMemcpyDeviceToHost) != hipSuccess) return true;
+    if (flag) {
+        const uint32_t zero = 0;
+        hipMemcpy(bar_ + 1, &zero, 4, hipMemcpyHostToDevice);
+    }
+    return flag != 0;
+}
+
+}  // namespace jh

@@ -1,0 +1,379 @@
+"""ctypes binding of libjulia_hip.so (include/julia_hip.h), the way the reference's callers bind
+its C interface (src/capi.rs:1-2: megaLaya's harness loads the library with ctypes).
+
+`Engine` mirrors src/capi.rs (julia_cuda_load / run / free / device / tier); the op functions
+mirror the reference's internal per-op surface (gemm::launch, attn::launch, embed_into, ...) on
+caller-owned device memory: pass device addresses (e.g. torch.Tensor.data_ptr()) and a HIP
+stream handle (torch.cuda.current_stream().cuda_stream), or 0 for the null stream.
+
+The library must be built (`make -C julia-cuda_amd`); there is no fallback.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libjulia_hip.so")
+_LIB = None
+
+EPI_RES, EPI_GEGLU, EPI_LN, EPI_STATS, EPI_ROPE, EPI_BIAS, EPI_RELU, EPI_GELU = (
+    1, 2, 4, 8, 16, 32, 64, 128)
+EPI = {
+    "rope": EPI_ROPE,
+    "lnrope": EPI_LN | EPI_ROPE,
+    "lngeglu": EPI_LN | EPI_GEGLU,
+    "resstats": EPI_RES | EPI_STATS,
+    "lnbias": EPI_LN | EPI_BIAS,
+    "lnbiasrelu": EPI_LN | EPI_BIAS | EPI_RELU,
+    "lnbiasgelu": EPI_LN | EPI_BIAS | EPI_GELU,
+    "biasresstats": EPI_BIAS | EPI_RES | EPI_STATS,
+}
+
+ERR_LEN = 1024
+
+
+class JuliaHipError(RuntimeError):
+    pass
+
+
+class GemmArgs(ctypes.Structure):
+    _fields_ = [
+        ("epi", ctypes.c_int),
+        ("a", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("c", ctypes.c_void_p),
+        ("m", ctypes.c_int),
+        ("n", ctypes.c_int),
+        ("k", ctypes.c_int),
+        ("stats_in", ctypes.c_void_p),
+        ("colsum", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("bias", ctypes.c_void_p),
+        ("rope", ctypes.c_void_p),
+        ("positions", ctypes.c_void_p),
+        ("rope_rows", ctypes.c_int),
+        ("stats_out", ctypes.c_void_p),
+    ]
+
+
+class GemmConfig(ctypes.Structure):
+    _fields_ = [("bm", ctypes.c_int), ("splits", ctypes.c_int)]
+
+    def __repr__(self):
+        return f"GemmConfig(bm={self.bm}, splits={self.splits})"
+
+
+class EngineInfo(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "d", "layers", "inter", "vocab", "head_layers", "head_ff", "n_qtypes", "window",
+        "global_every", "max_positions", "max_length", "cus")] + [
+        ("norm_eps", ctypes.c_float), ("head_eps", ctypes.c_float), ("seed", ctypes.c_uint64),
+        ("weight_bytes_f16", ctypes.c_size_t), ("weight_bytes_f32", ctypes.c_size_t)]
+
+
+# Every symbol include/julia_hip.h declares.
+EXPORTS = [
+    "julia_cuda_tier", "julia_cuda_load", "julia_cuda_free", "julia_cuda_device", "julia_cuda_run",
+    "julia_hip_scratch_new", "julia_hip_scratch_free", "julia_hip_gemm", "julia_hip_attention",
+    "julia_hip_embed", "julia_hip_norm_add", "julia_hip_score", "julia_hip_time_gemm",
+    "julia_hip_time_attention", "julia_hip_copy", "julia_hip_device_count",
+    "julia_hip_prep_fold_layernorm", "julia_hip_prep_fold_layernorm_bias",
+    "julia_hip_prep_geglu_rows", "julia_hip_prep_rope_table", "julia_hip_synth",
+    "julia_hip_round_f16", "julia_hip_gemm_choose", "julia_hip_gemm_plan_2080ti",
+    "julia_hip_gemm_choose_2080ti", "julia_hip_engine_info_get", "julia_hip_engine_tensor",
+    "julia_hip_run_trace",
+]
+
+_VP, _SZ, _I, _F, _CP = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_char_p
+_F32P = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_U16P = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_I32P = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+
+
+def lib():
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise JuliaHipError(f"{LIB_PATH} is not built: run `make -C julia-cuda_amd`")
+    L = ctypes.CDLL(LIB_PATH)
+    sig = {
+        "julia_cuda_tier": (_CP, []),
+        "julia_cuda_load": (_VP, [_CP, _SZ, _CP, _SZ]),
+        "julia_cuda_free": (None, [_VP]),
+        "julia_cuda_device": (None, [_VP, _CP, _SZ]),
+        "julia_cuda_run": (_I, [_VP, _SZ, _VP, _VP, _VP, _VP, _VP, _I, _VP, _VP, _CP, _SZ]),
+        "julia_hip_scratch_new": (_VP, [_SZ, _SZ, _CP, _SZ]),
+        "julia_hip_scratch_free": (None, [_VP]),
+        "julia_hip_gemm": (_I, [ctypes.POINTER(GemmArgs), GemmConfig, _VP, _VP, _CP, _SZ]),
+        "julia_hip_attention": (_I, [_VP, _VP, _I, _I, _I, _I, _VP, _VP, _CP, _SZ]),
+        "julia_hip_embed": (_I, [_VP, _I, _VP, _I, _I, _VP, _F, _VP, _VP, _CP, _SZ]),
+        "julia_hip_norm_add": (_I, [_VP, _I, _I, _VP, _VP, _F, _VP, _VP, _VP, _CP, _SZ]),
+        "julia_hip_score": (_I, [_VP, _I, _I, _VP, _F, _VP, _I, _VP, _VP, _CP, _SZ]),
+        "julia_hip_time_gemm": (_I, [ctypes.POINTER(GemmArgs), GemmConfig, _VP, _I, _I, _I,
+                                     ctypes.POINTER(_F), ctypes.POINTER(_F), _CP, _SZ]),
+        "julia_hip_time_attention": (_I, [_VP, _VP, _I, _I, _I, _I, _VP, _I, _I, _I,
+                                          ctypes.POINTER(_F), ctypes.POINTER(_F), _CP, _SZ]),
+        "julia_hip_copy": (_I, [_VP, _VP, _SZ, _I, _CP, _SZ]),
+        "julia_hip_device_count": (_I, []),
+        "julia_hip_prep_fold_layernorm": (None, [_F32P, _F32P, _I, _I, _U16P, _F32P]),
+        "julia_hip_prep_fold_layernorm_bias": (None, [_F32P, _F32P, _F32P, _F32P, _I, _I, _U16P,
+                                                      _F32P, _F32P]),
+        "julia_hip_prep_geglu_rows": (None, [_I, _I32P]),
+        "julia_hip_prep_rope_table": (None, [_F, _I, _F32P]),
+        "julia_hip_synth": (None, [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint64,
+                                   ctypes.c_uint64, ctypes.c_double, ctypes.c_double, _F32P]),
+        "julia_hip_round_f16": (None, [_F32P, _U16P, _SZ]),
+        "julia_hip_gemm_choose": (GemmConfig, [_I, _I, _I, _I]),
+        "julia_hip_gemm_plan_2080ti": (None, [_I, _I, _I, _I, _I, ctypes.POINTER(_I),
+                                              ctypes.POINTER(_I)]),
+        "julia_hip_gemm_choose_2080ti": (GemmConfig, [_I, _I, _I, _I]),
+        "julia_hip_engine_info_get": (_I, [_VP, ctypes.POINTER(EngineInfo)]),
+        "julia_hip_engine_tensor": (_VP, [_VP, _CP, _I, ctypes.POINTER(_SZ)]),
+        "julia_hip_run_trace": (_I, [_VP, _VP, _SZ, _VP, _SZ, ctypes.c_uint32, _I, _VP, _VP, _VP,
+                                     _CP, _SZ]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+    _LIB = L
+    return L
+
+
+def _err():
+    return ctypes.create_string_buffer(ERR_LEN)
+
+
+def _call(fn, *args):
+    e = _err()
+    rc = fn(*args, e, ERR_LEN)
+    if rc != 0:
+        raise JuliaHipError(e.value.decode(errors="replace"))
+
+
+def _np_ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def tier():
+    return lib().julia_cuda_tier().decode()
+
+
+def device_count():
+    return lib().julia_hip_device_count()
+
+
+# ---------------------------------------------------------------- Part 1: the engine
+class Engine:
+    """julia_cuda_load / julia_cuda_run / julia_cuda_free (src/capi.rs)."""
+
+    def __init__(self, spec="synthetic", max_length=0):
+        e = _err()
+        self.ptr = lib().julia_cuda_load(spec.encode(), max_length, e, ERR_LEN)
+        if not self.ptr:
+            raise JuliaHipError(e.value.decode(errors="replace"))
+
+    def close(self):
+        if getattr(self, "ptr", None):
+            lib().julia_cuda_free(self.ptr)
+            self.ptr = None
+
+    __del__ = close
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def device(self):
+        buf = ctypes.create_string_buffer(256)
+        lib().julia_cuda_device(self.ptr, buf, 256)
+        return buf.value.decode()
+
+    def info(self):
+        i = EngineInfo()
+        if lib().julia_hip_engine_info_get(self.ptr, ctypes.byref(i)):
+            raise JuliaHipError("no engine")
+        return i
+
+    def run(self, requests, layer_fused=False):
+        """requests: [(ids, markers, qtype)]. Returns ([logits per request], [gpu ms])."""
+        ids = np.ascontiguousarray(np.concatenate([np.asarray(r[0], np.uint32) for r in requests])
+                                   if requests else np.zeros(0), np.uint32)
+        lens = np.array([len(r[0]) for r in requests], np.uintp)
+        marks = [np.asarray(r[1], np.uint32) for r in requests]
+        markers = np.ascontiguousarray(np.concatenate(marks) if marks else np.zeros(0), np.uint32)
+        nm = np.array([len(m) for m in marks], np.uintp)
+        qt = np.array([r[2] for r in requests], np.uint32)
+        logits = np.zeros(max(len(markers), 1), np.float32)
+        ms = np.zeros(max(len(requests), 1), np.float32)
+        _call(lib().julia_cuda_run, self.ptr, len(requests), _np_ptr(ids), _np_ptr(lens),
+              _np_ptr(markers), _np_ptr(nm), _np_ptr(qt), int(bool(layer_fused)),
+              _np_ptr(logits), _np_ptr(ms))
+        out, at = [], 0
+        for m in nm:
+            out.append(logits[at:at + m].copy())
+            at += m
+        return out, ms[: len(requests)].copy()
+
+    def run_trace(self, ids, markers, qtype, layer_fused=False, trace=True, head_x=False):
+        inf = self.info()
+        ids = np.ascontiguousarray(ids, np.uint32)
+        markers = np.ascontiguousarray(markers, np.uint32)
+        n = len(ids)
+        logits = np.zeros(max(len(markers), 1), np.float32)
+        xt = np.zeros((inf.layers, n, inf.d), np.uint16) if trace else None
+        hx = np.zeros((n, inf.d), np.uint16) if head_x else None
+        _call(lib().julia_hip_run_trace, self.ptr, _np_ptr(ids), n, _np_ptr(markers), len(markers),
+              qtype, int(bool(layer_fused)), _np_ptr(logits), _np_ptr(xt), _np_ptr(hx))
+        return logits[: len(markers)], xt, hx
+
+    def tensor(self, name, index=0):
+        """(device address, bytes) of a prepared weight tensor."""
+        nb = ctypes.c_size_t()
+        p = lib().julia_hip_engine_tensor(self.ptr, name.encode(), index, ctypes.byref(nb))
+        if not p:
+            raise KeyError(f"{name}[{index}]")
+        return p, nb.value
+
+    def tensor_host(self, name, index=0, dtype=np.uint16):
+        p, nb = self.tensor(name, index)
+        out = np.empty(nb // np.dtype(dtype).itemsize, dtype)
+        copy(_np_ptr(out).value, p, nb, kind=2)
+        return out
+
+
+def copy(dst, src, nbytes, kind=4):
+    """hipMemcpy: kind 1 host->device, 2 device->host, 3 device->device, 4 default."""
+    _call(lib().julia_hip_copy, dst, src, nbytes, kind)
+
+
+# ---------------------------------------------------------------- Part 2: per-op surface
+class Scratch:
+    """Split-K / key-range partials and arrival counters (src/gemm.rs `Scratch`)."""
+
+    def __init__(self, ws_floats=1 << 22, counters=1 << 16):
+        e = _err()
+        self.ptr = lib().julia_hip_scratch_new(ws_floats, counters, e, ERR_LEN)
+        if not self.ptr:
+            raise JuliaHipError(e.value.decode(errors="replace"))
+
+    def close(self):
+        if getattr(self, "ptr", None):
+            lib().julia_hip_scratch_free(self.ptr)
+            self.ptr = None
+
+    __del__ = close
+
+
+def gemm_args(epi, a, w, c, m, n, k, stats_in=0, colsum=0, eps=1e-5, bias=0, rope=0, positions=0,
+              rope_rows=0, stats_out=0):
+    if isinstance(epi, str):
+        epi = EPI[epi]
+    return GemmArgs(epi, a, w, c, m, n, k, stats_in or None, colsum or None, eps, bias or None,
+                    rope or None, positions or None, rope_rows, stats_out or None)
+
+
+def gemm(args, bm=0, splits=1, scratch=None, stream=0):
+    _call(lib().julia_hip_gemm, ctypes.byref(args), GemmConfig(bm, splits),
+          scratch.ptr if scratch else None, stream or None)
+
+
+def time_gemm(args, bm=0, splits=1, scratch=None, warmup=20, batches=10, per_batch=50):
+    mn, md = ctypes.c_float(), ctypes.c_float()
+    _call(lib().julia_hip_time_gemm, ctypes.byref(args), GemmConfig(bm, splits),
+          scratch.ptr if scratch else None, warmup, batches, per_batch, ctypes.byref(mn),
+          ctypes.byref(md))
+    return mn.value, md.value
+
+
+def attention(qkv, o, n, d, window=0, chunks=1, scratch=None, stream=0):
+    _call(lib().julia_hip_attention, qkv, o, n, d, window, chunks,
+          scratch.ptr if scratch else None, stream or None)
+
+
+def time_attention(qkv, o, n, d, window=0, chunks=1, scratch=None, warmup=20, batches=10,
+                   per_batch=50):
+    mn, md = ctypes.c_float(), ctypes.c_float()
+    _call(lib().julia_hip_time_attention, qkv, o, n, d, window, chunks,
+          scratch.ptr if scratch else None, warmup, batches, per_batch, ctypes.byref(mn),
+          ctypes.byref(md))
+    return mn.value, md.value
+
+
+def embed(ids, n, table, vocab, d, gamma, eps, x, stream=0):
+    _call(lib().julia_hip_embed, ids, n, table, vocab, d, gamma, eps, x, stream or None)
+
+
+def norm_add(x, n, d, gamma, add, eps, out, stats, stream=0):
+    _call(lib().julia_hip_norm_add, x, n, d, gamma, add, eps, out, stats, stream or None)
+
+
+def score(y, n, d, w, b, markers, k, logits, stream=0):
+    _call(lib().julia_hip_score, y, n, d, w, b, markers, k, logits, stream or None)
+
+
+# ---------------------------------------------------------------- Part 3: host logic
+def fold_layernorm(w, gamma):
+    w = np.ascontiguousarray(w, np.float32)
+    out, k = w.shape
+    w16 = np.empty((out, k), np.uint16)
+    cs = np.empty(out, np.float32)
+    lib().julia_hip_prep_fold_layernorm(w, np.ascontiguousarray(gamma, np.float32), out, k, w16, cs)
+    return w16, cs
+
+
+def fold_layernorm_bias(w, gamma, beta, b):
+    w = np.ascontiguousarray(w, np.float32)
+    out, k = w.shape
+    w16 = np.empty((out, k), np.uint16)
+    cs = np.empty(out, np.float32)
+    bias = np.empty(out, np.float32)
+    f32 = lambda v: np.ascontiguousarray(v, np.float32)
+    lib().julia_hip_prep_fold_layernorm_bias(w, f32(gamma), f32(beta), f32(b), out, k, w16, cs, bias)
+    return w16, cs, bias
+
+
+def geglu_rows(inter):
+    src = np.empty(2 * inter, np.int32)
+    lib().julia_hip_prep_geglu_rows(inter, src)
+    return src
+
+
+def rope_table(theta, npos):
+    t = np.empty((npos, 32, 2), np.float32)
+    lib().julia_hip_prep_rope_table(theta, npos, t)
+    return t
+
+
+def synth(seed, tid, count, mean, std, start=0):
+    out = np.empty(count, np.float32)
+    lib().julia_hip_synth(seed, tid, start, count, mean, std, out)
+    return out
+
+
+def round_f16(x):
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().julia_hip_round_f16(x.ravel(), out.ravel(), x.size)
+    return out
+
+
+def gemm_choose(m, n, k, cus=256):
+    c = lib().julia_hip_gemm_choose(m, n, k, cus)
+    return c.bm, c.splits
+
+
+def gemm_plan_2080ti(n, cols, k, sms=68, per_sm=2):
+    bm, sp = ctypes.c_int(), ctypes.c_int()
+    lib().julia_hip_gemm_plan_2080ti(n, cols, k, sms, per_sm, ctypes.byref(bm), ctypes.byref(sp))
+    return bm.value, sp.value
+
+
+def gemm_choose_2080ti(m, n, k, sms=68):
+    c = lib().julia_hip_gemm_choose_2080ti(m, n, k, sms)
+    return c.bm, c.splits

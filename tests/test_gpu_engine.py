@@ -1,0 +1,179 @@
+"""The whole forward pass through the drop-in C ABI (julia_cuda_load / julia_cuda_run), against
+the CPU oracle's f32 forward on the same seeded synthetic model: the reference's --check flow
+(src/main.rs:180-232) as tests: the weight upload (bit-exact against the oracle's own
+preparation), each encoder layer's residual stream, the head and the logits, per-step kernels
+and the persistent layer kernel, and the C ABI's error paths (src/capi.rs, src/engine.rs)."""
+
+import numpy as np
+import pytest
+
+import julia_hip as jh
+import oracle as O
+from checks import check_logits, compare, f32
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(d=384, layers=4, inter=1152, vocab=1000, head_ff=768, max_positions=2048, seed=7)
+CHAINED_REL = 3e-2  # src/check.rs:395-402: the chain through all layers
+
+
+def spec(c):
+    return "synthetic:" + ",".join(f"{k}={v}" for k, v in c.items())
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def small(torch_cuda):
+    say("engine: small synthetic model", spec(SMALL))
+    e = jh.Engine(spec(SMALL), max_length=1024)
+    m = O.Model(O.cfg(**SMALL))
+    yield e, m
+    e.close()
+
+
+def request(rng, n, vocab, nm=4):
+    ids = rng.integers(0, vocab, n).astype(np.uint32)
+    markers = np.sort(rng.choice(n, size=min(nm, n), replace=False)).astype(np.uint32)
+    return ids, markers
+
+
+def test_tier_and_device(small):
+    e, _ = small
+    assert jh.tier() == "gfx950"
+    say("device:", e.device())
+    assert e.device()
+
+
+def test_weights_match_the_oracle_preparation(small):
+    """GpuWeights::verify (src/weights.rs:257-271), against an independent preparation."""
+    e, m = small
+    c = SMALL
+    d, I = c["d"], c["inter"]
+    seed = c["seed"]
+    # layer 0: converted only; layer 1: folded; wi interleaved for GeGLU
+    w0 = O.synth(seed, O.LAYER_BASE + O.L_WQKV, 3 * d * d).reshape(3 * d, d)
+    assert np.array_equal(e.tensor_host("wqkv", 0), O.to_f16_bits(w0).ravel())
+    b = O.LAYER_BASE + 16
+    w1 = O.synth(seed, b + O.L_WQKV, 3 * d * d).reshape(3 * d, d)
+    g1 = O.synth(seed, b + O.L_ATTN_NORM, d)
+    w16, cs = O.fold_layernorm(w1, g1)
+    assert np.array_equal(e.tensor_host("wqkv", 1), w16.ravel())
+    assert np.array_equal(e.tensor_host("qkv_colsum", 1, np.float32), cs)
+    wi = O.synth(seed, b + O.L_WI, 2 * I * d).reshape(2 * I, d)
+    gi = O.synth(seed, b + O.L_MLP_NORM, d)
+    wi16, wcs = O.fold_layernorm(wi, gi)
+    rows = O.geglu_rows(I)
+    assert np.array_equal(e.tensor_host("wi", 1), wi16[rows].ravel())
+    assert np.array_equal(e.tensor_host("wi_colsum", 1, np.float32), wcs[rows])
+    # the head's bias fold and the embedding table
+    hb = O.HEAD_BASE + 32
+    ip = O.synth(seed, hb + O.H_IN_PROJ_W, 3 * d * d).reshape(3 * d, d)
+    _, _, ipb = O.fold_layernorm_bias(ip, O.synth(seed, hb + O.H_NORM1_W, d),
+                                      O.synth(seed, hb + O.H_NORM1_B, d),
+                                      O.synth(seed, hb + O.H_IN_PROJ_B, 3 * d))
+    assert np.array_equal(e.tensor_host("in_proj_b", 1, np.float32), ipb)
+    emb = e.tensor_host("tok_emb", 0)
+    assert np.array_equal(emb[: 10 * d], O.to_f16_bits(O.synth(seed, O.TOK_EMB, 10 * d)))
+
+
+@pytest.mark.parametrize("n", [72, 363])
+def test_forward_matches_oracle(small, n):
+    e, m = small
+    say(f"forward n={n} (per-step kernels)")
+    rng = np.random.default_rng(n)
+    ids, markers = request(rng, n, SMALL["vocab"])
+    want, trace = m.forward(ids, 0, markers, trace=True)
+    logits, xt, _ = e.run_trace(ids, markers, 0)
+    for layer in range(SMALL["layers"]):
+        compare(f32(xt[layer]), trace[layer], CHAINED_REL, 1e-1, what=f"layer {layer} stream")
+    mean, mx = check_logits(logits, want)
+    say(f"  logits {np.round(logits, 4)} vs {np.round(want, 4)}: mean |d| {mean:.2e} max {mx:.2e}")
+    # and through julia_cuda_run
+    out, ms = e.run([(ids, markers, 0)])
+    np.testing.assert_allclose(out[0], logits, rtol=0, atol=1e-6)
+    assert ms[0] > 0
+
+
+def test_layer_kernel_matches_per_step(small):
+    """src/check.rs:665-760 `layer_kernel`: the persistent kernel against the per-step kernels
+    (same tasks; summation order differs only in the split-K / key-range merges)."""
+    e, m = small
+    rng = np.random.default_rng(3)
+    for n in (72, 363, 1000):
+        say(f"layer kernel n={n}")
+        ids, markers = request(rng, n, SMALL["vocab"])
+        ls, xs, _ = e.run_trace(ids, markers, 1)
+        lf, xf, _ = e.run_trace(ids, markers, 1, layer_fused=True)
+        for layer in range(SMALL["layers"]):
+            compare(f32(xf[layer]), f32(xs[layer]), 1e-2, 5e-2, what=f"fused layer {layer}")
+        want = m.forward(ids, 1, markers)
+        check_logits(lf, want, "layer kernel logits")
+
+
+def test_batch_of_requests(small):
+    """Engine::run's queue (src/engine.rs:170-196): more requests than one queue of 16, mixed
+    lengths and question types, against each request run alone."""
+    e, m = small
+    rng = np.random.default_rng(9)
+    reqs = []
+    for i in range(20):
+        n = int(rng.integers(1, 300))
+        ids, markers = request(rng, n, SMALL["vocab"], nm=int(rng.integers(0, 4)))
+        reqs.append((ids, markers, i % 3))
+    out, ms = e.run(reqs)
+    assert len(out) == 20 and np.all(ms > 0)
+    for (ids, markers, q), lg in list(zip(reqs, out))[::4]:
+        alone, _ = e.run([(ids, markers, q)])
+        np.testing.assert_allclose(lg, alone[0], rtol=0, atol=1e-6)
+        if len(markers):
+            check_logits(lg, m.forward(ids, q, markers))
+
+
+def test_run_errors(small):
+    """The C ABI's failures (src/capi.rs:157-168, src/engine.rs:78-81): -1 and a message."""
+    e, _ = small
+    ids = np.arange(10, dtype=np.uint32)
+    with pytest.raises(jh.JuliaHipError, match="question type"):
+        e.run([(ids, [1], 3)])
+    with pytest.raises(jh.JuliaHipError, match="marker is past"):
+        e.run([(ids, [10], 0)])
+    with pytest.raises(jh.JuliaHipError, match="tokens, not 1 to"):
+        e.run([(np.zeros(0, np.uint32), [], 0)])
+    with pytest.raises(jh.JuliaHipError, match="tokens, not 1 to"):
+        e.run([(np.zeros(1025, np.uint32), [], 0)])
+    with pytest.raises(jh.JuliaHipError, match="vocabulary"):
+        e.run([(np.array([5, 1000], np.uint32), [0], 0)])
+    # the engine still works afterwards
+    out, _ = e.run([(ids, [3], 0)])
+    assert np.isfinite(out[0]).all()
+
+
+def test_load_errors(torch_cuda):
+    with pytest.raises(jh.JuliaHipError, match="max_length"):
+        jh.Engine(spec(dict(SMALL, max_positions=512)), max_length=600)
+    with pytest.raises(jh.JuliaHipError, match="no model"):
+        jh.Engine("/no/such/checkpoint")
+
+
+def test_full_model_293_tokens(torch_cuda):
+    """Config 4's model (ModernBERT-base shapes, 22 layers, head_ff 1536) on one 293-token
+    request: logits within the north star's tolerance of the f32 oracle."""
+    say("full model d=768 layers=22 n=293")
+    e = jh.Engine("synthetic", max_length=1024)
+    try:
+        m = O.Model(O.cfg())
+        rng = np.random.default_rng(293)
+        ids, markers = request(rng, 293, 50368, nm=6)
+        want, trace = m.forward(ids, 0, markers, trace=True)
+        logits, xt, _ = e.run_trace(ids, markers, 0)
+        worst = max(O.rel_err(f32(xt[l]), trace[l]) for l in range(22))
+        mean, mx = check_logits(logits, want)
+        lf, _, _ = e.run_trace(ids, markers, 0, layer_fused=True, trace=False)
+        check_logits(lf, want, "layer kernel")
+        say(f"  worst layer stream rel err {worst:.2e}; logits mean |d| {mean:.2e} max {mx:.2e}")
+        assert worst < CHAINED_REL
+    finally:
+        e.close()

@@ -1,0 +1,190 @@
+"""CPU tests of the product library: it loads without a GPU and exports every symbol
+include/julia_hip.h declares; its host-side logic (the synthetic generator, the weight
+preparation of src/prep.rs, the tile choosers) against the oracle's independent restatement and
+the reference's own known-answer tests; the C ABI's error paths that need no GPU."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import julia_hip as jh
+import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_every_declared_symbol():
+    header = open(os.path.join(ROOT, "include", "julia_hip.h")).read()
+    header = re.sub(r"/\*.*?\*/", "", header, flags=re.S)
+    declared = set(re.findall(r"\b(julia_(?:cuda|hip)_\w+)\s*\(", header))
+    assert declared == set(jh.EXPORTS), declared ^ set(jh.EXPORTS)
+    L = jh.lib()
+    for name in declared:
+        assert getattr(L, name) is not None
+
+
+def test_tier():
+    assert jh.tier() == "gfx950"
+
+
+def test_load_without_a_gpu_or_model_is_an_error():
+    # A bad model spec fails before any device work; a good one fails on the GPU check here.
+    with pytest.raises(jh.JuliaHipError, match="unknown model spec key"):
+        jh.Engine("synthetic:bogus=1")
+    with pytest.raises(jh.JuliaHipError, match="no model at"):
+        jh.Engine("/some/checkpoint/dir")
+    with pytest.raises(jh.JuliaHipError, match="d must be"):
+        jh.Engine("synthetic:d=100")
+    if jh.device_count() == 0:
+        with pytest.raises(jh.JuliaHipError, match="no HIP device"):
+            jh.Engine("synthetic:layers=1")
+
+
+def test_null_engine_and_free():
+    L = jh.lib()
+    L.julia_cuda_free(None)  # NULL is fine (src/capi.rs:91-96)
+    err = ctypes.create_string_buffer(64)
+    rc = L.julia_cuda_run(None, 1, None, None, None, None, None, 0, None, None, err, 64)
+    assert rc == -1 and b"no engine" in err.value
+    # the message is truncated to the buffer and NUL-terminated (src/capi.rs:23-33)
+    err = ctypes.create_string_buffer(4)
+    rc = L.julia_cuda_run(None, 1, None, None, None, None, None, 0, None, None, err, 4)
+    assert rc == -1 and err.value == b"no "
+
+
+@pytest.mark.parametrize("tid", [O.TOK_EMB, O.EMB_NORM, O.TYPE_EMB, O.LAYER_BASE + 1,
+                                 O.LAYER_BASE + 16 * 21 + 4, O.HEAD_BASE + 32 + 7,
+                                 O.SCORER_BASE + 5])
+def test_synthetic_generator_matches_the_oracle(tid):
+    mean, std = O.dist(tid)
+    a = jh.synth(42, tid, 4099, mean, std, start=12345)
+    b = O.synth(42, tid, 4099, start=12345)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # moments of the stream
+    big = jh.synth(1, tid, 200000, 0.0, 1.0)
+    assert abs(big.mean()) < 0.01 and abs(big.std() - 1) < 0.01
+
+
+def test_f16_rounding_matches_numpy():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(100000) * 10 ** rng.uniform(-9, 5, 100000),
+                        [0.0, -0.0, 65504, 65519, 65520, 1e9, -1e9, 2 ** -25, 2 ** -24,
+                         3 * 2 ** -25, 6e-8, np.inf, -np.inf]]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(jh.round_f16(x), want)
+    assert np.array_equal(O.to_f16_bits(x), want)
+
+
+def test_fold_layernorm_matches_the_oracle():
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((96, 128)) * 0.02).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(128)).astype(np.float32)
+    beta = (0.05 * rng.standard_normal(128)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(96)).astype(np.float32)
+    a16, acs = jh.fold_layernorm(w, g)
+    b16, bcs = O.fold_layernorm(w, g)
+    assert np.array_equal(a16, b16) and np.array_equal(acs.view(np.uint32), bcs.view(np.uint32))
+    a16, acs, ab = jh.fold_layernorm_bias(w, g, beta, b)
+    b16, bcs, bb = O.fold_layernorm_bias(w, g, beta, b)
+    assert np.array_equal(a16, b16) and np.array_equal(ab.view(np.uint32), bb.view(np.uint32))
+
+
+def test_bias_fold_matches_layernorm_then_linear():
+    """The reference's known-answer test src/prep.rs:279-314, restated: xorshift64 from
+    0x9e3779b97f4a7c15, k = 64, out = 32, 5 rows of mean ~3; the folded form within 2e-2 of
+    LayerNorm (with bias) then linear (with bias), in f64."""
+    seed = [0x9E3779B97F4A7C15]
+    M = (1 << 64) - 1
+
+    def rnd():
+        s = seed[0]
+        s ^= (s << 13) & M
+        s ^= s >> 7
+        s ^= (s << 17) & M
+        seed[0] = s
+        return (s >> 40) / float(1 << 24) - 0.5
+
+    k, out, rows = 64, 32, 5
+    w = np.array([rnd() for _ in range(out * k)], np.float32).reshape(out, k)
+    gb = [(1.0 + rnd(), rnd()) for _ in range(k)]
+    gamma = np.array([g for g, _ in gb], np.float32)
+    beta = np.array([b for _, b in gb], np.float32)
+    b = np.array([rnd() for _ in range(out)], np.float32)
+    x = np.array([3.0 + rnd() for _ in range(rows * k)], np.float32).reshape(rows, k)
+    w16, cs, bias = jh.fold_layernorm_bias(w, gamma, beta, b)
+    wf = O.f16_bits_to_f32(w16).astype(np.float64)
+    for row in x.astype(np.float64):
+        mean = row.mean()
+        r = 1.0 / np.sqrt(((row - mean) ** 2).mean() + 1e-5)
+        ln = (row - mean) * r * gamma + beta
+        want = w.astype(np.float64) @ ln + b
+        got = r * (wf @ row - mean * cs.astype(np.float64)) + bias
+        assert np.max(np.abs(got - want)) < 2e-2
+
+
+def test_geglu_interleave_matches_the_epilogue():
+    """The interleave against this library's GeGLU epilogue, as src/prep.rs:248-274 checks the
+    reference's against its own: the thread owning columns c0 + e and c0 + 32 + e (c0 = 4 (t % 8),
+    e < 4) of 64-column group g reads the input of output column 32 g + c0 + e at the first and
+    its gate at the second; every output column is produced once."""
+    inter = 1152
+    rows = jh.geglu_rows(inter)
+    assert np.array_equal(rows, O.geglu_rows(inter))
+    seen = np.zeros(inter, bool)
+    for g in range(2 * inter // 64):
+        for t in range(8):
+            for e in range(4):
+                c0 = 4 * t
+                col = 32 * g + c0 + e
+                assert rows[64 * g + c0 + e] == col
+                assert rows[64 * g + 32 + c0 + e] == inter + col
+                assert not seen[col]
+                seen[col] = True
+    assert seen.all()
+    assert sorted(rows) == list(range(2 * inter))
+
+
+def test_rope_table_matches_the_oracle_and_closed_form():
+    a = jh.rope_table(160000.0, 300)
+    assert np.array_equal(a, O.rope_table(160000.0, 300))
+    p = np.arange(300)[:, None].astype(np.float64)
+    j = np.arange(32)[None, :]
+    ang = p * 160000.0 ** (-2.0 * j / 64)
+    assert np.max(np.abs(a[:, :, 0] - np.cos(ang))) < 1e-4
+    assert np.max(np.abs(a[:, :, 1] - np.sin(ang))) < 1e-4
+
+
+def test_plan_matches_the_2080ti_sweeps():
+    """The reference's golden picks, src/forward.rs:812-823 (68 SMs x 2 blocks, inter 1152,
+    its D = 384): gemm_plan at 72, 363 and 512 tokens."""
+    d, inter = 384, 1152
+    shapes = [(3 * d, d), (d, d), (2 * inter, d), (d, inter)]
+    picks = lambda n: [jh.gemm_plan_2080ti(n, c, k, 68, 2) for c, k in shapes]
+    assert picks(72) == [(32, 1), (32, 3), (32, 1), (32, 3)]
+    assert picks(363) == [(64, 1), (32, 1), (64, 1), (64, 3)]
+    assert picks(512) == [(64, 1), (32, 1), (64, 1), (32, 1)]
+
+
+def test_reference_choose_rule():
+    """src/gemm.rs:153-172 in closed form."""
+    assert jh.gemm_choose_2080ti(72, 1152, 384, 68) == (32, 1)     # 36 x 3 tiles > 34
+    assert jh.gemm_choose_2080ti(72, 384, 384, 68) == (32, 4)      # 6 x 3 = 18 tiles
+    assert jh.gemm_choose_2080ti(300, 384, 384, 68) == (64, 4)
+    assert jh.gemm_choose_2080ti(500, 384, 384, 68) == (128, 4)     # 6 x 4 = 24 tiles
+    assert jh.gemm_choose_2080ti(500, 1152, 384, 68) == (128, 1)    # 18 x 4 = 72 tiles
+    assert jh.gemm_choose_2080ti(72, 384, 256, 68) == (32, 2)      # 8 K steps: 8 / 3 = 2
+
+
+@pytest.mark.parametrize("m", [1, 72, 293, 512, 1024, 4096, 18752])
+@pytest.mark.parametrize("n,k", [(2304, 768), (768, 768), (768, 1152), (1536, 768)])
+def test_chooser_picks_valid_configs(m, n, k):
+    bm, sp = jh.gemm_choose(m, n, k, 256)
+    assert bm in (16, 32, 64, 128, 256)
+    if bm >= 128:
+        assert n % 128 == 0 and sp == 1
+    else:
+        assert 1 <= sp <= 4 and (k // 32) // (4 * sp) >= 2
