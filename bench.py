@@ -1,0 +1,255 @@
+"""Benchmark: the full Julia-1-shaped forward pass (22-layer ModernBERT
+encoder, hidden 768, 12 heads, GeGLU 1152, plus the head and scorer; seeded synthetic weights)
+on one 293-token request per step, through the drop-in C ABI (julia_cuda_run), on one MI355X.
+
+Prints one JSON line: `value` is GPU ms per request (HIP events, embed to logits, as the
+reference's engine measures it: src/engine.rs:98-105), the better of the per-step kernels and the
+persistent layer kernel; it also carries
+  - the fused GEMMs' TFLOP/s and fraction of f16 MFMA peak at M >= 4096 (the metric's first part),
+  - `roofline` for the dominant kernel of the forward pass (per-layer kernel timings with HIP
+    events, rotating through the 22 layers' weights, src/main.rs:307-312),
+  - `cpu_baseline`: the f32 CPU oracle (oracle/liboracle.so) on the box's host cores, on a
+    bounded sample of the same workload,
+  - config 4's latency distribution (mean, p50, p99 over seeded request lengths 72-1024),
+  - config 5's persistent layer kernel at 448 tokens.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "julia-cuda_amd"))
+
+import julia_hip as jh  # noqa: E402
+
+METRIC = "fused-GEMM TFLOP/s & % f16 MFMA peak; encoder ms/request @293 tokens"
+PEAK_F16 = 2.5e15   # dense f16 MFMA, MI355X
+PEAK_HBM = 8.0e12   # HBM3E bytes/s
+D, I, H, L, VOCAB, FF = 768, 1152, 12, 22, 50368, 1536
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def percentile(xs, p):
+    """src/serve.rs:85: the value at index round((len - 1) p) of the sorted values."""
+    s = sorted(xs)
+    return s[int(round((len(s) - 1) * p))]
+
+
+def request(rng, n, nm=6):
+    ids = rng.integers(0, VOCAB, n).astype(np.uint32)
+    markers = np.sort(rng.choice(n, size=min(nm, n), replace=False)).astype(np.uint32)
+    return ids, markers, 0
+
+
+def lengths(rng, count):
+    """Config 4's request lengths: log-normal (median 260, sigma 0.5), clipped to [72, 1024];
+    mean ~293."""
+    return np.clip(np.round(rng.lognormal(np.log(260.0), 0.5, count)), 72, 1024).astype(int)
+
+
+def gemm_bytes(m, n, k, epi):
+    """Algorithmic HBM bytes of one fused GEMM: a, w and c once (c read too with a residual),
+    plus the epilogue's vectors (colsum, bias, row statistics, RoPE table rows)."""
+    b = 2 * (m * k + n * k) + 2 * m * (n // 2 if epi == "lngeglu" else n)
+    if epi in ("resstats", "biasresstats"):
+        b += 2 * m * n + 4 * 2 * m * (n // 64)
+    if epi.startswith("ln"):
+        b += 4 * n + 4 * 2 * m * (k // 64)
+    if "rope" in epi:
+        b += 4 * 64 * m
+    return b
+
+
+STEP_SHAPES = {  # step: (n, k, epilogue, count per forward)
+    "qkv": (3 * D, D, "lnrope", L),
+    "wo": (D, D, "resstats", L),
+    "wi": (2 * I, D, "lngeglu", L),
+    "wo_mlp": (D, I, "resstats", L),
+}
+
+
+def attention_flops(n, window):
+    pairs = n * n if window == 0 else sum(min(n, i + window + 1) - max(0, i - window) for i in range(n))
+    return 4 * 64 * H * pairs
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="forward timing only")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(requests are independent: the multi-GPU design is one engine per GPU)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    rng = np.random.default_rng(293)
+    eng = jh.Engine("synthetic", max_length=1024)
+    info = eng.info()
+    log(f"device {eng.device()}, {info.cus} CUs; weights {info.weight_bytes_f16 / 1e6:.1f} MB f16")
+    req = request(rng, 293)
+
+    def timed(fused):
+        eng.run([req] * args.warmup, layer_fused=fused)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        _, ms = eng.run([req] * args.steps, layer_fused=fused)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3 / args.steps
+        return float(np.mean(ms)), float(np.median(ms)), wall
+
+    per_step = timed(False)
+    fused = timed(True)
+    log(f"293 tokens: per-step kernels {per_step[0]:.3f} ms GPU ({per_step[2]:.3f} wall), "
+        f"layer kernel {fused[0]:.3f} ms GPU ({fused[2]:.3f} wall)")
+    best_fused = fused[0] < per_step[0]
+    best = fused if best_fused else per_step
+
+    out = {
+        "metric": METRIC,
+        "value": round(best[0], 4),
+        "unit": "ms/request",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(best[2], 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded ModernBERT-base-shaped weights and token ids)",
+        "config": {
+            "workload": "config 4: full forward (embed, 22-layer encoder, 2-layer head, scorer) "
+                        "of one 293-token request, 6 markers",
+            "d": D, "heads": H, "inter": I, "layers": L, "head_ff": FF, "vocab": VOCAB,
+            "tokens": 293, "path": "layer kernel" if best_fused else "per-step kernels",
+        },
+        "per_step_ms": {"mean": round(per_step[0], 4), "median": round(per_step[1], 4),
+                        "wall": round(per_step[2], 4)},
+        "layer_kernel_ms": {"mean": round(fused[0], 4), "median": round(fused[1], 4),
+                            "wall": round(fused[2], 4)},
+    }
+    if args.quick:
+        print(json.dumps(out), flush=True)
+        return
+
+    # ---- per-kernel timings at 293 tokens, rotating through the layers' weights ----
+    kern = {}
+    for step, (n, k, epi, cnt) in STEP_SHAPES.items():
+        mn, md = eng.time_step(step, 293)
+        kern[step] = dict(us=round(md, 3), us_min=round(mn, 3), per_forward=cnt,
+                          bytes=gemm_bytes(293, n, k, epi), flops=2 * 293 * n * k,
+                          config=list(jh.gemm_choose(293, n, k, info.cus)))
+    for step, window in (("attention_global", 0), ("attention", None)):
+        mn, md = eng.time_step(step, 293)
+        kern[step] = dict(us=round(md, 3), us_min=round(mn, 3),
+                          per_forward=(8 if step == "attention_global" else L),
+                          bytes=2 * 293 * 4 * D,
+                          flops=attention_flops(293, 0) if window == 0 else None)
+    kern["attention"]["per_forward"] = L  # mixed global / window, rotating layers
+    kern["attention_global"]["per_forward"] = 0  # included in "attention"
+    for v in kern.values():
+        v["total_us"] = round(v["us"] * v["per_forward"], 2)
+        if v.get("bytes"):
+            v["GBps"] = round(v["bytes"] / (v["us"] * 1e-6) / 1e9, 1)
+        if v.get("flops"):
+            v["TFLOPs"] = round(v["flops"] / (v["us"] * 1e-6) / 1e12, 2)
+    out["kernels_293"] = kern
+    dom = max((k for k in STEP_SHAPES), key=lambda s: kern[s]["total_us"])
+    dk = kern[dom]
+    n, k, epi, _ = STEP_SHAPES[dom]
+    t_hbm, t_mfma = dk["bytes"] / PEAK_HBM, dk["flops"] / PEAK_F16
+    if t_hbm >= t_mfma:
+        ach = dk["bytes"] / (dk["us"] * 1e-6) / 1e9
+        out["roofline"] = {"kernel": f"{dom} gemm_{epi} M=293 N={n} K={k}", "bound": "hbm",
+                           "achieved": round(ach, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                           "frac": round(ach / (PEAK_HBM / 1e9), 4), "traffic": None,
+                           "algorithmic_bytes": dk["bytes"], "us": dk["us"]}
+    else:
+        ach = dk["flops"] / (dk["us"] * 1e-6) / 1e12
+        out["roofline"] = {"kernel": f"{dom} gemm_{epi} M=293 N={n} K={k}", "bound": "mfma",
+                           "achieved": round(ach, 2), "peak": PEAK_F16 / 1e12, "unit": "TFLOP/s",
+                           "frac": round(ach / (PEAK_F16 / 1e12), 4), "traffic": None,
+                           "algorithmic_flops": dk["flops"], "us": dk["us"]}
+    log("kernels at 293 tokens:", json.dumps(kern))
+
+    # ---- the fused GEMMs at M >= 4096 (the metric's TFLOP/s and % of f16 MFMA peak) ----
+    big = {}
+    eng_big = jh.Engine("synthetic:layers=4,vocab=1000,max_positions=20480", max_length=18752)
+    for m in (4096, 18752):
+        for step, (n, k, epi, _) in STEP_SHAPES.items():
+            mn, md = eng_big.time_step(step, m, warmup=5, batches=5, per_batch=8)
+            fl = 2 * m * n * k
+            big[f"{step}@{m}"] = dict(us=round(md, 2), TFLOPs=round(fl / (md * 1e-6) / 1e12, 1),
+                                      frac_peak=round(fl / (md * 1e-6) / PEAK_F16, 4),
+                                      config=list(jh.gemm_choose(m, n, k, info.cus)))
+    tot_fl = sum(2 * 18752 * n * k for (n, k, _, _) in STEP_SHAPES.values())
+    tot_us = sum(big[f"{s}@18752"]["us"] for s in STEP_SHAPES)
+    out["fused_gemm_tflops"] = round(tot_fl / (tot_us * 1e-6) / 1e12, 1)
+    out["fused_gemm_frac_peak"] = round(tot_fl / (tot_us * 1e-6) / PEAK_F16, 4)
+    out["fused_gemm"] = big
+    log("fused GEMMs at M>=4096:", json.dumps(big))
+
+    # ---- config 5: the persistent layer kernel at 448 tokens, and the batched M ~ 18.8k ----
+    r448 = request(rng, 448)
+    for fused_flag in (False, True):
+        eng.run([r448] * 10, layer_fused=fused_flag)
+    _, ms_s = eng.run([r448] * 50)
+    _, ms_f = eng.run([r448] * 50, layer_fused=True)
+    out["config5_448"] = {"per_step_ms": round(float(np.mean(ms_s)), 4),
+                          "layer_kernel_ms": round(float(np.mean(ms_f)), 4)}
+    eng_big.close()
+
+    # ---- config 4's latency distribution ----
+    lens = lengths(np.random.default_rng(4), 64)
+    reqs = [request(rng, int(nn)) for nn in lens]
+    path_fused = best_fused
+    eng.run(reqs[:8], layer_fused=path_fused)
+    _, ms = eng.run(reqs, layer_fused=path_fused)
+    ms = [float(x) for x in ms]
+    out["config4_lengths"] = {"requests": len(lens), "mean_tokens": round(float(lens.mean()), 1),
+                              "mean_ms": round(float(np.mean(ms)), 4),
+                              "p50_ms": round(percentile(ms, 0.5), 4),
+                              "p99_ms": round(percentile(ms, 0.99), 4)}
+    eng.close()
+
+    # ---- the CPU baseline: the f32 oracle on the host cores, a bounded sample ----
+    if not args.no_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle as O
+
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        model = O.Model(O.cfg())
+        ids, markers, q = req
+        model.forward(ids, q, markers)  # warm-up
+        times = []
+        t_end = time.perf_counter() + 15.0
+        while time.perf_counter() < t_end or len(times) < 2:
+            t0 = time.perf_counter()
+            model.forward(ids, q, markers)
+            times.append((time.perf_counter() - t0) * 1e3)
+        out["cpu_baseline"] = {"value": round(float(np.median(times)), 2), "unit": "ms/request",
+                               "cores": threads, "kind": "port",
+                               "sample": f"{len(times)} forward passes of the same 293-token "
+                                         "request (22-layer encoder + head, f32, LayerNorms in "
+                                         "f64), median; weight generation excluded"}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -188,6 +188,14 @@ int julia_hip_engine_info_get(const Engine *e, julia_hip_engine_info *out);
  * type_emb, in_proj, in_proj_colsum, in_proj_b, out_proj, out_proj_b, linear1, linear1_colsum,
  * linear1_b, linear2, linear2_b, lin1, lin1_colsum, lin1_b, lin2; index = the layer. */
 const void *julia_hip_engine_tensor(const Engine *e, const char *name, int index, size_t *bytes);
+/* src/timing.rs / the reference's --time (src/main.rs:234-453): one encoder step of the engine
+ * on m rows, timed as julia_hip_time_gemm does, rotating through the layers' weights from call
+ * to call so they are not L2-resident (src/main.rs:307-312). step: 0 qkv, 1 attention (the
+ * layers' own global/window mix), 2 wo, 3 wi, 4 wo_mlp, 5 global attention. bm = 0: the
+ * chooser's tiling. */
+int julia_hip_time_encoder_step(const Engine *e, int step, int m, int bm, int splits, int warmup,
+                                int batches, int per_batch, float *min_us, float *median_us,
+                                char *err, size_t err_len);
 /* One request with the residual stream copied out after every encoder layer (x_trace, f16 bits
  * [layers][n][d], nullable) and the head's stream after its last layer (head_x, [n][d],
  * nullable): for step-by-step parity checks. */

@@ -14,7 +14,9 @@ constexpr int ATT_LDS_F16 = 64 * 72 + 64 * 68;
 
 // Tile (query block qb, head h), key range `chunk` of p.chunks. Every thread of the block calls
 // it; `lds` holds ATT_LDS_F16 f16 (16-byte aligned). It ends with a block barrier, so the
-// caller may reuse lds right after.
+// caller may reuse lds right after. XG: o is read by other blocks of the same kernel (the
+// persistent layer kernel), so it is stored device-coherent.
+template <bool XG = false>
 __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int h, int chunk,
                                                f16* lds, uint32_t* s_last) {
     f16 (*ks)[72] = (f16 (*)[72])lds;              // [key][d], rows of 144 B
@@ -153,10 +155,10 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
 #pragma unroll
         for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) mine[(dt * 4 + e) * 256] = oacc[dt][e];
-        mine[16 * 256] = mx;
-        mine[17 * 256] = lsum;
-        fence_agent();
+            for (int e = 0; e < 4; e++) xstore32(mine + (dt * 4 + e) * 256, oacc[dt][e]);
+        xstore32(mine + 16 * 256, mx);
+        xstore32(mine + 17 * 256, lsum);
+        release_wait();
         __syncthreads();
         if (tid == 0) {
             const uint32_t old = atomic_add_agent(p.counters + tile, 1u);
@@ -168,7 +170,7 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
         const uint32_t last = *s_last;
         __syncthreads();  // every thread has read s_last (and is done with the tiles)
         if (last == 0) return;
-        fence_agent();
+        acquire_agent();
         float m = -INFINITY;
         for (int z = 0; z < p.chunks; z++) m = fmaxf(m, slots[(size_t)z * ATT_PART * 256 + 16 * 256 + tid]);
         const float base = m == -INFINITY ? 0.0f : m;
@@ -196,7 +198,7 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
             half4 o;
 #pragma unroll
             for (int e = 0; e < 4; e++) o[e] = (f16)(oacc[dt][e] * inv);
-            *(half4*)(op + 16 * dt) = o;
+            store8<XG>(op + 16 * dt, o);
         }
     }
     __syncthreads();  // the tiles are free again

@@ -48,16 +48,62 @@ __device__ __forceinline__ float gelu(float x) {
     return x * (x >= 0.0f ? 1.0f - q : q);
 }
 
-__device__ __forceinline__ float ld_f32(const float* p) { return *p; }
+// ---- hand-offs between blocks on different XCDs -------------------------------------------------
+// The eight XCDs each have their own L2, which is not coherent with the others within a kernel.
+// A general release (an agent-scope release fence) writes back the whole L2, which costs tens
+// of microseconds per call here. Data that another block reads in the same kernel (split-K and
+// key-range partials, the layer kernel's phase outputs) is therefore stored with agent-scope
+// (device-coherent, write-through) stores, so that the release is only "my stores have
+// completed" (release_wait), and the reader's acquire is an L1/L2 invalidation (acquire_agent),
+// which writes nothing back.
+__device__ __forceinline__ void release_wait() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);  // every outstanding memory operation of this wave is done
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
-// Agent-scope release/acquire around the cross-block hand-offs (split-K partials, key-range
-// partials, grid barriers): the partial writers' L2 lines reach memory before the arrival is
-// counted, and the last arriver's caches are invalidated before it reads them, which matters on
-// a GPU whose eight XCDs each have their own L2.
-__device__ __forceinline__ void fence_agent() { __threadfence(); }
+__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+
+__device__ __forceinline__ void xstore64(void* p, uint64_t v) {
+    __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 8-byte stores, device-coherent when XG (the data is read by another block in this kernel).
+template <bool XG>
+__device__ __forceinline__ void store8(void* p, half4 v) {
+    if (XG) {
+        uint64_t u;
+        __builtin_memcpy(&u, &v, 8);
+        xstore64(p, u);
+    } else {
+        *(half4*)p = v;
+    }
+}
+
+template <bool XG>
+__device__ __forceinline__ void store8(void* p, float2 v) {
+    if (XG) {
+        uint64_t u;
+        __builtin_memcpy(&u, &v, 8);
+        xstore64(p, u);
+    } else {
+        *(float2*)p = v;
+    }
+}
+
+__device__ __forceinline__ void xstore32(float* p, float v) {
+    __hip_atomic_store((uint32_t*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void xstore16(void* p, float4 v) {
+    uint64_t u[2];
+    __builtin_memcpy(u, &v, 16);
+    xstore64(p, u[0]);
+    xstore64((char*)p + 8, u[1]);
+}
 
 __device__ __forceinline__ uint32_t atomic_add_agent(uint32_t* p, uint32_t v) {
-    return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void atomic_store_agent(uint32_t* p, uint32_t v) {
@@ -85,8 +131,9 @@ __device__ __forceinline__ int xcd_task(int b, int T) {
 //
 // Order as the reference's gemm_tile (kernels/src/main.rs:931-1038): LayerNorm from the input
 // statistics, bias, ReLU, GELU, RoPE, then GeGLU or the store with the residual and the output
-// statistics of the stored f16 values.
-template <int EPI>
+// statistics of the stored f16 values. XG: the outputs are read by other blocks of the same
+// kernel (the persistent layer kernel's next phase), so they are stored device-coherent.
+template <int EPI, bool XG = false>
 __device__ __forceinline__ void epilogue(const GemmParams& p, int row, int grp, int c0, float* v,
                                          bool valid) {
     const int gcol = grp * 64;
@@ -145,7 +192,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int row, int grp, 
             half4 o;
 #pragma unroll
             for (int e = 0; e < 4; e++) o[e] = (f16)(gelu(v[e]) * v[4 + e]);
-            *(half4*)((f16*)p.c + (size_t)row * (p.n >> 1) + grp * 32 + c0) = o;
+            store8<XG>((f16*)p.c + (size_t)row * (p.n >> 1) + grp * 32 + c0, o);
         }
     } else {
         half4 lo, hi;
@@ -164,8 +211,8 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int row, int grp, 
                 lo[e] = (f16)v[e];
                 hi[e] = (f16)v[4 + e];
             }
-            *(half4*)out = lo;
-            *(half4*)(out + 32) = hi;
+            store8<XG>(out, lo);
+            store8<XG>(out + 32, hi);
         }
         if (EPI & EPI_STATS) {
             float s = 0.0f, q = 0.0f;
@@ -180,8 +227,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int row, int grp, 
             s = group_sum<8>(s);
             q = group_sum<8>(q);
             if (valid && (threadIdx.x & 7) == 0) {
-                float2* so = (float2*)(p.stats_out + ((size_t)row * (p.n >> 6) + grp) * 2);
-                *so = make_float2(s, q);
+                store8<XG>(p.stats_out + ((size_t)row * (p.n >> 6) + grp) * 2, make_float2(s, q));
             }
         }
     }

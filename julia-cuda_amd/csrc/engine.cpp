@@ -243,9 +243,10 @@ Engine* load_engine(const char* dir, size_t max_length) {
     counters = std::max(counters, e->layer_kernel.counters((int)ml, (int)d, c.inter));
     e->scratch.ws = dalloc<float>(ws, "scratch");
     e->scratch.ws_floats = ws;
-    e->scratch.counters = dalloc<uint32_t>(counters + 64, "counters");
+    counters = (counters + 31) / 32 * 32;  // the barrier's words start on a 128-byte line
+    e->scratch.counters = dalloc<uint32_t>(counters + BAR_WORDS, "counters");
     e->scratch.n_counters = counters;
-    hip_check(hipMemset(e->scratch.counters, 0, (counters + 64) * 4), "hipMemset");
+    hip_check(hipMemset(e->scratch.counters, 0, (counters + BAR_WORDS) * 4), "hipMemset");
     e->layer_kernel.bind(e->scratch.counters + counters);  // the grid barrier's counter
     hip_check(hipDeviceSynchronize(), "load");
     return e.release();
@@ -690,6 +691,69 @@ const void* julia_hip_engine_tensor(const Engine* e, const char* name, int index
         return nullptr;
     }
     return nullptr;
+}
+
+int julia_hip_time_encoder_step(const Engine* ce, int step, int m, int bm, int splits, int warmup,
+                                int batches, int per_batch, float* min_us, float* median_us,
+                                char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!ce) throw std::runtime_error("no engine");
+        Engine& e = *const_cast<Engine*>(ce);
+        hip_check(hipSetDevice(e.device), "hipSetDevice");
+        if (m <= 0 || m > e.max_length) throw std::runtime_error("time: m out of range");
+        if (step < 0 || step > 5) throw std::runtime_error("time: no step " + std::to_string(step));
+        const int d = e.cfg.d, I = e.cfg.inter, L = e.cfg.layers;
+        // A real residual stream and statistics to run on: embed ids 0..m-1 and one layer.
+        std::vector<uint32_t> ids(m);
+        for (int i = 0; i < m; i++) ids[i] = (uint32_t)(i * 7919 % e.cfg.vocab);
+        hip_check(hipMemcpy(e.ids_d, ids.data(), m * 4, hipMemcpyHostToDevice), "ids");
+        embed_launch(e.ids_d, m, e.h(e.layout.tok_embeddings), e.cfg.vocab, d, e.f(e.layout.emb_norm),
+                     e.cfg.norm_eps, e.x, e.stream);
+        e.launch_layer(0, m);
+        hip_check(hipStreamSynchronize(e.stream), "time");
+        int l = 0;
+        auto gemm_cfg = [&](int n, int k) {
+            return bm > 0 ? GemmConfig{bm, splits} : gemm_choose(m, n, k, e.cus);
+        };
+        // Rotate through the layers' weights, as the reference's --time does (src/main.rs:
+        // 307-312), so the weights are not the last call's, still in L2. Layer 0 has no
+        // attention LayerNorm: the qkv step uses layers 1.. when there are more than one.
+        auto launch = [&] {
+            const int lo = (step == 0 && L > 1) ? 1 : 0;
+            l = lo + (l + 1 - lo) % (L - lo);
+            const EncoderLayer& Ly = e.layout.layers[l];
+            const float* rope = e.f(Ly.global ? e.layout.rope_global : e.layout.rope_local);
+            Gemm g{};
+            g.m = m, g.rope_rows = e.cfg.max_positions, g.eps = e.cfg.norm_eps;
+            switch (step) {
+                case 0:
+                    g.epi = Ly.qkv_colsum.present ? EPI_K_LNROPE : EPI_K_ROPE, g.a = e.x;
+                    g.w = e.h(Ly.wqkv), g.c = e.qkv, g.n = 3 * d, g.k = d, g.rope = rope;
+                    if (Ly.qkv_colsum.present) g.stats_in = e.stats_b, g.colsum = e.f(Ly.qkv_colsum);
+                    break;
+                case 2:
+                    g.epi = EPI_K_RESSTATS, g.a = e.o, g.w = e.h(Ly.wo), g.c = e.hx, g.n = d, g.k = d;
+                    g.stats_out = e.stats_a;
+                    break;
+                case 3:
+                    g.epi = EPI_K_LNGEGLU, g.a = e.x, g.w = e.h(Ly.wi), g.c = e.mid, g.n = 2 * I;
+                    g.k = d, g.stats_in = e.stats_a, g.colsum = e.f(Ly.wi_colsum);
+                    break;
+                case 4:
+                    g.epi = EPI_K_RESSTATS, g.a = e.mid, g.w = e.h(Ly.wo_mlp), g.c = e.hx, g.n = d;
+                    g.k = I, g.stats_out = e.stats_b;
+                    break;
+                default: {
+                    const int window = (step == 1 && !Ly.global) ? e.cfg.window : 0;
+                    attention_launch(e.qkv, e.o, m, d, window,
+                                     attention_chunks(m, d, window, e.cus), e.scratch, e.stream);
+                    return;
+                }
+            }
+            gemm_launch(g, gemm_cfg(g.n, g.k), e.scratch, e.stream);
+        };
+        time_calls(launch, warmup, batches, per_batch, e.stream, min_us, median_us);
+    });
 }
 
 int julia_hip_run_trace(const Engine* ce, const uint32_t* ids, size_t n, const uint32_t* markers,

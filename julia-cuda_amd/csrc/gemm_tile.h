@@ -15,10 +15,11 @@ constexpr int lat_lds_floats() { return 4 * BM * 68; }
 // reduction when the grid splits K -> the epilogue. Thread t owns row (pass * 32 + t / 8) of the
 // tile and columns c0 = 4 (t % 8), c0 + 32 of 64-column group `grp`.
 //
-// Split-K (kernels/src/gemm.rs:355-433): every block writes its partial to the scratch, then
-// counts its arrival; the last of the tile's splits (which resets the counter) sums all partials
-// in split order, so the result does not depend on arrival order.
-template <int NPASS, int EPI>
+// Split-K (kernels/src/gemm.rs:355-433): every block writes its partial to the scratch
+// (device-coherent stores), waits for them to complete, then counts its arrival; the last of the
+// tile's splits (which resets the counter) invalidates its caches and sums all partials in split
+// order, so the result does not depend on arrival order.
+template <int NPASS, int EPI, bool XG = false>
 __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8], int tile_id,
                                        int z, int row0, int grp, int rows_in_tile,
                                        uint32_t* s_last) {
@@ -31,9 +32,9 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
         for (int ps = 0; ps < NPASS; ps++)
 #pragma unroll
             for (int h = 0; h < 2; h++)
-                *(float4*)(mine + ((ps * 2 + h) * 256 + tid) * 4) =
-                    make_float4(v[ps][4 * h], v[ps][4 * h + 1], v[ps][4 * h + 2], v[ps][4 * h + 3]);
-        fence_agent();
+                xstore16(mine + ((ps * 2 + h) * 256 + tid) * 4,
+                         make_float4(v[ps][4 * h], v[ps][4 * h + 1], v[ps][4 * h + 2], v[ps][4 * h + 3]));
+        release_wait();
         __syncthreads();
         if (tid == 0) {
             const uint32_t old = atomic_add_agent(p.counters + tile_id, 1u);
@@ -45,7 +46,7 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
         const uint32_t last = *s_last;
         __syncthreads();  // every thread has read s_last before anyone can write it again
         if (last == 0) return;
-        fence_agent();
+        acquire_agent();
 #pragma unroll
         for (int ps = 0; ps < NPASS; ps++)
 #pragma unroll
@@ -69,7 +70,7 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
     for (int ps = 0; ps < NPASS; ps++) {
         const int r = ps * 32 + (tid >> 3);
         const int row = row0 + r;
-        epilogue<EPI>(p, row, grp, c0, v[ps], r < rows_in_tile && row < p.m);
+        epilogue<EPI, XG>(p, row, grp, c0, v[ps], r < rows_in_tile && row < p.m);
     }
 }
 
@@ -77,7 +78,7 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
 // waves split the tile's K steps between them; `red` is lat_lds_floats<BM>() floats of LDS.
 // Every thread of the block calls it; it ends with a block barrier, so the caller may reuse
 // `red` right after.
-template <int BM, int EPI>
+template <int BM, int EPI, bool XG = false>
 __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, float* red,
                                               uint32_t* s_last) {
     constexpr int MI = BM / 16;
@@ -170,7 +171,7 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
         }
     }
     __syncthreads();  // red is free again
-    finish<NPASS, EPI>(p, v, bx * p.tiles_m + by, z, by * BM, bx, BM, s_last);
+    finish<NPASS, EPI, XG>(p, v, bx * p.tiles_m + by, z, by * BM, bx, BM, s_last);
 }
 
 }  // namespace jh

@@ -12,6 +12,9 @@
 
 namespace jh {
 
+// u32 words of device memory the grid barrier needs (zeroed once; every barrier leaves them zero).
+constexpr int BAR_WORDS = 11 * 32;
+
 struct LayerArgs {
     jh_half *x, *qkv, *o, *mid;
     float *stats_attn, *stats_mlp;  // wo writes stats_attn (wi reads it), wo_mlp stats_mlp
@@ -52,8 +55,7 @@ public:
 
 private:
     int cus_ = 0, per_cu_ = 0;
-    uint32_t* bar_ = nullptr;
-    uint32_t bar_count_ = 0;  // arrivals counted so far on *bar_
+    uint32_t* bar_ = nullptr;  // BAR_WORDS words
 };
 
 }  // namespace jh

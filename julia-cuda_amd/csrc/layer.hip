@@ -23,33 +23,53 @@ struct LayerParams {
     int bm[4];
     int epi0;         // EPI_K_ROPE (layer 0) or EPI_K_LNROPE
     unsigned phases;  // bits 0-4
-    uint32_t* bar;    // bar[0]: arrivals (monotonic), bar[1]: set when a barrier timed out
-    uint32_t bar_base;
+    uint32_t* bar;    // the barrier's words (BAR_WORDS, zero between launches)
 };
 
-// A barrier across the grid on a monotonic arrival counter: block b's k-th barrier of this launch
-// waits until the count reaches bar_base + k * grid (compared with wrap-around). Every thread
-// releases its writes at agent scope before the block arrives, and acquires after, so everything
-// written before the barrier is visible to every block after it, through ordinary loads, across
-// the XCDs' separate L2s (kernels/src/gemm.rs:435-489 is the reference's). The wait is bounded:
-// past ~0.2 s (far beyond any real barrier) it gives up and raises bar[1], which the host turns
-// into an error, so a broken launch cannot hang the GPU.
-__device__ __forceinline__ void grid_sync(uint32_t* bar, uint32_t target) {
-    fence_agent();
+// The grid barrier's words, each on its own 128-byte line: eight group arrival counters, the
+// count of groups complete, the generation, and the time-out flag.
+constexpr int BAR_LINE = 32;
+constexpr int BAR_GROUPS = 8 * BAR_LINE, BAR_GEN = 9 * BAR_LINE, BAR_TIMEOUT = 10 * BAR_LINE;
+
+// A barrier across the grid (the reference's is kernels/src/gemm.rs:435-489): blocks arrive in
+// eight groups (block b in group b % 8, which is the XCD it is dispatched to), so no counter sees
+// more than an eighth of the arrivals; the last arrival of a group counts the group, the last
+// group advances the generation that every block waits on, and each counter is reset by its
+// last arrival, so the words are zero again at the end of every barrier.
+//
+// The phase outputs are stored device-coherent (XG), so the release is only each wave waiting
+// for its stores to complete; after the barrier every wave invalidates its L1/L2 view (the
+// acquire) before reading other blocks' outputs. The wait is bounded: past ~0.2 s (far beyond
+// any real barrier) it gives up and raises the time-out flag, which the host turns into an
+// error, so a broken launch cannot hang the GPU.
+__device__ __forceinline__ void grid_sync(uint32_t* bar) {
+    release_wait();
     __syncthreads();
     if (threadIdx.x == 0) {
-        atomic_add_agent(bar, 1u);
+        const uint32_t grid = gridDim.x, x = blockIdx.x & 7;
+        const uint32_t groups = grid < 8 ? grid : 8, in_group = (grid - x + 7) / 8;
+        uint32_t* gen = bar + BAR_GEN;
+        const uint32_t g0 = atomic_load_agent(gen);  // before arriving: it cannot move yet
+        release_wait();
+        if (atomic_add_agent(bar + x * BAR_LINE, 1u) == in_group - 1) {
+            atomic_store_agent(bar + x * BAR_LINE, 0u);
+            if (atomic_add_agent(bar + BAR_GROUPS, 1u) == groups - 1) {
+                atomic_store_agent(bar + BAR_GROUPS, 0u);
+                release_wait();  // the resets land before anyone can pass
+                atomic_add_agent(gen, 1u);
+            }
+        }
         const uint64_t t0 = wall_clock64();
-        while ((int32_t)(atomic_load_agent(bar) - target) < 0) {
+        while (atomic_load_agent(gen) == g0) {
             __builtin_amdgcn_s_sleep(1);
             if (wall_clock64() - t0 > 20000000ull) {
-                __hip_atomic_store(bar + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                atomic_store_agent(bar + BAR_TIMEOUT, 1u);
                 break;
             }
         }
     }
     __syncthreads();
-    fence_agent();
+    acquire_agent();
 }
 
 constexpr int LAYER_LDS_FLOATS = lat_lds_floats<32>();
@@ -61,23 +81,18 @@ __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, float* l
     const int T = g.tiles_n * g.tiles_m * g.splits;
     for (int t = blockIdx.x; t < T; t += gridDim.x) {
         if (bm == 16)
-            gemm_lat_tile<16, EPI>(g, t, lds, s_last);
+            gemm_lat_tile<16, EPI, true>(g, t, lds, s_last);
         else
-            gemm_lat_tile<32, EPI>(g, t, lds, s_last);
+            gemm_lat_tile<32, EPI, true>(g, t, lds, s_last);
     }
 }
 
 __global__ __launch_bounds__(256) void layer_kernel(LayerParams P) {
     __shared__ __attribute__((aligned(16))) float lds[LAYER_LDS_FLOATS];
     __shared__ uint32_t s_last;
-    const uint32_t grid = gridDim.x;
-    uint32_t nbar = 0;
     auto on = [&](int ph) { return (P.phases >> ph) & 1u; };
     auto sync_if = [&](int next) {
-        if (on(next)) {
-            nbar++;
-            grid_sync(P.bar, P.bar_base + nbar * grid);
-        }
+        if (on(next)) grid_sync(P.bar);
     };
     if (on(0)) {
         if (P.epi0 == EPI_K_LNROPE)
@@ -91,7 +106,7 @@ __global__ __launch_bounds__(256) void layer_kernel(LayerParams P) {
         const int heads = a.d >> 6, T = ((a.n + 63) >> 6) * heads * a.chunks;
         for (int t = blockIdx.x; t < T; t += gridDim.x) {
             const int tile = t / a.chunks;
-            attention_tile(a, tile / heads, tile % heads, t % a.chunks, (f16*)lds, &s_last);
+            attention_tile<true>(a, tile / heads, tile % heads, t % a.chunks, (f16*)lds, &s_last);
         }
         sync_if(2);
     }
@@ -233,7 +248,6 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
     P.epi0 = g[0].epi;
     P.phases = phases;
     P.bar = bar_;
-    P.bar_base = bar_count_;
 
     const int grid_blocks = grid(a, plan);
     // A barrier between two consecutive selected phases only (the kernel's sync_if).
@@ -250,17 +264,13 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
                             dim3(256), args, 0, stream);
     if (e != hipSuccess) fail(std::string(hipGetErrorString(e)) + " (" + plan.str() + ", grid " +
                               std::to_string(grid_blocks) + ")");
-    bar_count_ += barriers * (uint32_t)grid_blocks;
 }
 
 bool LayerKernel::barrier_timed_out() {
     if (!bar_) return false;
     uint32_t flag = 0;
-    if (hipMemcpy(&flag, bar_ + 1, 4, hipMemcpyDeviceToHost) != hipSuccess) return true;
-    if (flag) {
-        const uint32_t zero = 0;
-        hipMemcpy(bar_ + 1, &zero, 4, hipMemcpyHostToDevice);
-    }
+    if (hipMemcpy(&flag, bar_ + BAR_TIMEOUT, 4, hipMemcpyDeviceToHost) != hipSuccess) return true;
+    if (flag) hipMemset(bar_, 0, BAR_WORDS * 4);  // a barrier gave up: its counts are stale
     return flag != 0;
 }
 

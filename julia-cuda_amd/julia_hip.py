@@ -83,7 +83,7 @@ EXPORTS = [
     "julia_hip_prep_geglu_rows", "julia_hip_prep_rope_table", "julia_hip_synth",
     "julia_hip_round_f16", "julia_hip_gemm_choose", "julia_hip_gemm_plan_2080ti",
     "julia_hip_gemm_choose_2080ti", "julia_hip_engine_info_get", "julia_hip_engine_tensor",
-    "julia_hip_run_trace",
+    "julia_hip_time_encoder_step", "julia_hip_run_trace",
 ]
 
 _VP, _SZ, _I, _F, _CP = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_char_p
@@ -132,6 +132,8 @@ def lib():
         "julia_hip_gemm_choose_2080ti": (GemmConfig, [_I, _I, _I, _I]),
         "julia_hip_engine_info_get": (_I, [_VP, ctypes.POINTER(EngineInfo)]),
         "julia_hip_engine_tensor": (_VP, [_VP, _CP, _I, ctypes.POINTER(_SZ)]),
+        "julia_hip_time_encoder_step": (_I, [_VP, _I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_F),
+                                             ctypes.POINTER(_F), _CP, _SZ]),
         "julia_hip_run_trace": (_I, [_VP, _VP, _SZ, _VP, _SZ, ctypes.c_uint32, _I, _VP, _VP, _VP,
                                      _CP, _SZ]),
     }
@@ -231,6 +233,15 @@ class Engine:
         _call(lib().julia_hip_run_trace, self.ptr, _np_ptr(ids), n, _np_ptr(markers), len(markers),
               qtype, int(bool(layer_fused)), _np_ptr(logits), _np_ptr(xt), _np_ptr(hx))
         return logits[: len(markers)], xt, hx
+
+    STEPS = {"qkv": 0, "attention": 1, "wo": 2, "wi": 3, "wo_mlp": 4, "attention_global": 5}
+
+    def time_step(self, step, m, bm=0, splits=1, warmup=20, batches=10, per_batch=44):
+        """One encoder step on m rows, rotating through the layers' weights; (min, median) us."""
+        mn, md = ctypes.c_float(), ctypes.c_float()
+        _call(lib().julia_hip_time_encoder_step, self.ptr, self.STEPS.get(step, step), m, bm,
+              splits, warmup, batches, per_batch, ctypes.byref(mn), ctypes.byref(md))
+        return mn.value, md.value
 
     def tensor(self, name, index=0):
         """(device address, bytes) of a prepared weight tensor."""
