@@ -140,6 +140,12 @@ int julia_hip_time_attention(const void *qkv, void *o, int n, int d, int window,
                              const julia_hip_scratch *s, int warmup, int batches, int per_batch,
                              float *min_us, float *median_us, char *err, size_t err_len);
 
+/* A plain device copy kernel of `bytes` (16-byte multiple) between two fresh buffers, timed as
+ * julia_hip_time_gemm: the achievable-bandwidth reference for the bandwidth-bound kernels and the
+ * known-size kernel rocprofv3's byte counters are calibrated against. */
+int julia_hip_time_copy(size_t bytes, int warmup, int batches, int per_batch, float *min_us,
+                        float *median_us, char *err, size_t err_len);
+
 /* hipMemcpy helpers for callers without a HIP binding (tests). */
 int julia_hip_copy(void *dst, const void *src, size_t bytes, int kind, char *err, size_t err_len);
 int julia_hip_device_count(void);
@@ -196,6 +202,13 @@ const void *julia_hip_engine_tensor(const Engine *e, const char *name, int index
 int julia_hip_time_encoder_step(const Engine *e, int step, int m, int bm, int splits, int warmup,
                                 int batches, int per_batch, float *min_us, float *median_us,
                                 char *err, size_t err_len);
+/* src/profile.rs:84-241 with kernels/src/prof.rs's stamps: runs the encoder up to `layer` on n
+ * tokens (per-step), then that layer with the persistent layer kernel recording, per block, the
+ * 100 MHz clock at each phase's start and end (16 u64 per block: phase p at 2p, 2p + 1; the CU
+ * at 10). plan: NULL for the default, else 10 ints (bm[4], splits[4], kv[2]); plan_out (nullable)
+ * receives the plan used, grid the block count. */
+int julia_hip_profile_layer(const Engine *e, int n, int layer, const int *plan, uint64_t *stamps,
+                            int max_blocks, int *grid, int *plan_out, char *err, size_t err_len);
 /* One request with the residual stream copied out after every encoder layer (x_trace, f16 bits
  * [layers][n][d], nullable) and the head's stream after its last layer (head_x, [n][d],
  * nullable): for step-by-step parity checks. */

@@ -40,8 +40,8 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
     half8 qf[2];
     {
         const f16* qp = (const f16*)p.qkv + (size_t)min(qi, n - 1) * ld + h * 64 + 8 * g;
-        qf[0] = *(const half8*)qp;
-        qf[1] = *(const half8*)(qp + 32);
+        qf[0] = load16h<XG>(qp);
+        qf[1] = load16h<XG>(qp + 32);
         if (qi >= n) qf[0] = qf[1] = half8{};
     }
 
@@ -49,27 +49,30 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
     // and V chunks keyed the other way round (key t % 64, d chunk t / 64 and + 4) so that its
     // transposed LDS writes are consecutive in the key. Keys past n are zero.
     half8 kr[2], vr[2];
+    uint32_t kmask[2], vmask[2];
     auto gload = [&](int kb) {
         const int base = kb * 64;
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int ck = tid + 256 * u;
             const int key = base + (ck >> 3);
-            kr[u] = key < n ? *(const half8*)((const f16*)p.qkv + (size_t)key * ld + d + h * 64 + (ck & 7) * 8)
-                            : half8{};
+            // Unconditional loads (clamped rows, masked after): see the GEMM's main loop.
+            kr[u] = load16h<XG>((const f16*)p.qkv + (size_t)min(key, n - 1) * ld + d + h * 64 + (ck & 7) * 8);
             const int vkey = base + (tid & 63), vch = (tid >> 6) + 4 * u;
-            vr[u] = vkey < n ? *(const half8*)((const f16*)p.qkv + (size_t)vkey * ld + 2 * d + h * 64 + vch * 8)
-                             : half8{};
+            vr[u] = load16h<XG>((const f16*)p.qkv + (size_t)min(vkey, n - 1) * ld + 2 * d + h * 64 + vch * 8);
+            kmask[u] = key < n ? 0xffffffffu : 0u;
+            vmask[u] = vkey < n ? 0xffffffffu : 0u;
         }
     };
     auto lstore = [&]() {
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const int ck = tid + 256 * u;
-            *(half8*)&ks[ck >> 3][(ck & 7) * 8] = kr[u];
+            *(half8*)&ks[ck >> 3][(ck & 7) * 8] = mask16(kr[u], kmask[u]);
             const int vkey = tid & 63, vch = (tid >> 6) + 4 * u;
+            const half8 v = mask16(vr[u], vmask[u]);
 #pragma unroll
-            for (int e = 0; e < 8; e++) vt[vch * 8 + e][vkey] = vr[u][e];
+            for (int e = 0; e < 8; e++) vt[vch * 8 + e][vkey] = v[e];
         }
     };
 
@@ -170,21 +173,21 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
         const uint32_t last = *s_last;
         __syncthreads();  // every thread has read s_last (and is done with the tiles)
         if (last == 0) return;
-        acquire_agent();
+        // The other ranges' partials through the coherent path (no cache invalidation).
         float m = -INFINITY;
-        for (int z = 0; z < p.chunks; z++) m = fmaxf(m, slots[(size_t)z * ATT_PART * 256 + 16 * 256 + tid]);
+        for (int z = 0; z < p.chunks; z++) m = fmaxf(m, xload32(slots + (size_t)z * ATT_PART * 256 + 16 * 256 + tid));
         const float base = m == -INFINITY ? 0.0f : m;
         lsum = 0.0f;
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) oacc[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         for (int z = 0; z < p.chunks; z++) {
             const float* src = slots + (size_t)z * ATT_PART * 256 + tid;
-            const float f = exp2f(src[16 * 256] - base);
-            lsum += src[17 * 256] * f;
+            const float f = exp2f(xload32(src + 16 * 256) - base);
+            lsum += xload32(src + 17 * 256) * f;
 #pragma unroll
             for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) oacc[dt][e] += src[(dt * 4 + e) * 256] * f;
+                for (int e = 0; e < 4; e++) oacc[dt][e] += xload32(src + (dt * 4 + e) * 256) * f;
         }
     }
 

@@ -22,6 +22,16 @@ __device__ __forceinline__ floatx4 mfma16(half8 a, half8 b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// v & keep on all 128 bits (keep is 0 or all ones): a select without a branch.
+__device__ __forceinline__ half8 mask16(half8 v, uint32_t keep) {
+    uint32_t u[4];
+    __builtin_memcpy(u, &v, 16);
+#pragma unroll
+    for (int i = 0; i < 4; i++) u[i] &= keep;
+    __builtin_memcpy(&v, u, 16);
+    return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
@@ -51,18 +61,16 @@ __device__ __forceinline__ float gelu(float x) {
 // ---- hand-offs between blocks on different XCDs -------------------------------------------------
 // The eight XCDs each have their own L2, which is not coherent with the others within a kernel.
 // A general release (an agent-scope release fence) writes back the whole L2, which costs tens
-// of microseconds per call here. Data that another block reads in the same kernel (split-K and
-// key-range partials, the layer kernel's phase outputs) is therefore stored with agent-scope
-// (device-coherent, write-through) stores, so that the release is only "my stores have
-// completed" (release_wait), and the reader's acquire is an L1/L2 invalidation (acquire_agent),
-// which writes nothing back.
+// of microseconds per call here, and a general acquire invalidates it, which throws away what
+// other blocks share through it. Data that another block reads in the same kernel (split-K and
+// key-range partials, the layer kernel's phase outputs) is therefore stored AND loaded with
+// agent-scope (device-coherent) accesses: the release is only "my stores have completed"
+// (release_wait), and the reader needs no cache maintenance at all.
 __device__ __forceinline__ void release_wait() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);  // every outstanding memory operation of this wave is done
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
-
-__device__ __forceinline__ void acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
 
 __device__ __forceinline__ void xstore64(void* p, uint64_t v) {
     __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -89,6 +97,57 @@ __device__ __forceinline__ void store8(void* p, float2 v) {
     } else {
         *(float2*)p = v;
     }
+}
+
+// Device-coherent loads for data another block wrote in this kernel: they fetch from the
+// coherence point instead of a possibly stale L1/L2 line, so readers need no cache
+// invalidation (which would also throw away the weights other blocks share through L2).
+__device__ __forceinline__ uint64_t xload64(const void* p) {
+    return __hip_atomic_load((uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <bool XG>
+__device__ __forceinline__ half8 load16h(const f16* p) {
+    if (XG) {
+        const uint64_t u[2] = {xload64(p), xload64(p + 4)};
+        half8 v;
+        __builtin_memcpy(&v, u, 16);
+        return v;
+    }
+    return *(const half8*)p;
+}
+
+template <bool XG>
+__device__ __forceinline__ half4 load8h(const f16* p) {
+    if (XG) {
+        const uint64_t u = xload64(p);
+        half4 v;
+        __builtin_memcpy(&v, &u, 8);
+        return v;
+    }
+    return *(const half4*)p;
+}
+
+template <bool XG>
+__device__ __forceinline__ float2 load8f(const float* p) {
+    if (XG) {
+        const uint64_t u = xload64(p);
+        float2 v;
+        __builtin_memcpy(&v, &u, 8);
+        return v;
+    }
+    return *(const float2*)p;
+}
+
+__device__ __forceinline__ float xload32(const float* p) {
+    return __uint_as_float(__hip_atomic_load((uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+__device__ __forceinline__ float4 xload16f(const float* p) {
+    const uint64_t u[2] = {xload64(p), xload64(p + 2)};
+    float4 v;
+    __builtin_memcpy(&v, u, 16);
+    return v;
 }
 
 __device__ __forceinline__ void xstore32(float* p, float v) {
@@ -143,8 +202,9 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int row, int grp, 
             const float* st = p.stats_in + (size_t)row * slots * 2;
             float S = 0.0f, Q = 0.0f;
             for (int s = 0; s < slots; s++) {
-                S += st[2 * s];
-                Q += st[2 * s + 1];
+                const float2 sq = load8f<XG>(st + 2 * s);
+                S += sq.x;
+                Q += sq.y;
             }
             const float mean = S / (float)p.k;
             const float var = fmaxf(Q / (float)p.k - mean * mean, 0.0f);
@@ -199,7 +259,7 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int row, int grp, 
         f16* out = (f16*)p.c + (size_t)row * p.n + gcol + c0;
         if (valid) {
             if (EPI & EPI_RES) {
-                const half4 rl = *(const half4*)out, rh = *(const half4*)(out + 32);
+                const half4 rl = load8h<XG>(out), rh = load8h<XG>(out + 32);
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     v[e] += (float)rl[e];

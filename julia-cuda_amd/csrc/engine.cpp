@@ -10,8 +10,10 @@
 #include <string.h>
 
 #include <algorithm>
+#include <map>
 #include <memory>
 #include <stdexcept>
+#include <tuple>
 #include <string>
 #include <vector>
 
@@ -58,6 +60,13 @@ struct Engine {
     hipEvent_t ev_start[QUEUE] = {}, ev_end[QUEUE] = {};
     Scratch scratch{};
     LayerKernel layer_kernel;
+    // The per-step forward pass as HIP graphs, one per (tokens, markers, question type): 124
+    // launches submitted as one. They read the request from fixed buffers (gin: ids, then
+    // markers at max_length) and write glogits; stream order keeps queued requests apart.
+    bool use_graphs = true;
+    uint32_t* gin = nullptr;
+    float* glogits = nullptr;
+    std::map<std::tuple<int, int, int>, hipGraphExec_t> graphs;
 
     const jh_half* h(const Span& s) const { return s.present ? w16 + s.start : nullptr; }
     const float* f(const Span& s) const { return s.present ? w32 + s.start : nullptr; }
@@ -65,6 +74,9 @@ struct Engine {
     ~Engine() {
         if (device >= 0) hipSetDevice(device);
         if (stream) hipStreamSynchronize(stream);
+        for (auto& kv : graphs) hipGraphExecDestroy(kv.second);
+        if (gin) hipFree(gin);
+        if (glogits) hipFree(glogits);
         for (int i = 0; i < QUEUE; i++) {
             if (ev_start[i]) hipEventDestroy(ev_start[i]);
             if (ev_end[i]) hipEventDestroy(ev_end[i]);
@@ -155,6 +167,35 @@ struct Engine {
         score_launch(o, n, d, h(S.lin2), S.lin2_b, markers, nm, logits, stream);
     }
 
+    // The per-step forward pass for (n, nm, qtype) as an executable graph (captured and
+    // instantiated on first use), reading gin and writing glogits.
+    hipGraphExec_t graph_for(int n, int nm, int qtype) {
+        const auto key = std::make_tuple(n, nm, qtype);
+        auto it = graphs.find(key);
+        if (it != graphs.end()) return it->second;
+        if (graphs.size() >= 512) {  // bound the cache: drop everything, start over
+            hip_check(hipStreamSynchronize(stream), "graph cache");
+            for (auto& kv : graphs) hipGraphExecDestroy(kv.second);
+            graphs.clear();
+        }
+        hipGraph_t g = nullptr;
+        hip_check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "capture");
+        try {
+            launch(gin, n, qtype, gin + max_length, nm, glogits, false);
+        } catch (...) {
+            hipStreamEndCapture(stream, &g);
+            if (g) hipGraphDestroy(g);
+            throw;
+        }
+        hip_check(hipStreamEndCapture(stream, &g), "capture");
+        hipGraphExec_t ex = nullptr;
+        const hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        hip_check(e, "hipGraphInstantiate");
+        graphs[key] = ex;
+        return ex;
+    }
+
     // One request's forward pass (src/engine.rs:66-112 `launch`): ids already on the device.
     void launch(const uint32_t* ids, int n, int qtype, const uint32_t* markers, int nm,
                 float* logits, bool fused) {
@@ -216,6 +257,9 @@ Engine* load_engine(const char* dir, size_t max_length) {
     e->ids_d = dalloc<uint32_t>(QUEUE * n, "ids");
     e->markers_d = dalloc<uint32_t>(QUEUE * n, "markers");
     e->logits_d = dalloc<float>(QUEUE * n, "logits");
+    e->gin = dalloc<uint32_t>(2 * n, "graph input");
+    e->glogits = dalloc<float>(n, "graph logits");
+    if (const char* g = getenv("JULIA_HIP_GRAPHS")) e->use_graphs = strcmp(g, "0") != 0;
     hip_check(hipHostMalloc((void**)&e->ids_h, QUEUE * n * 4, hipHostMallocDefault), "pinned ids");
     hip_check(hipHostMalloc((void**)&e->markers_h, QUEUE * n * 4, hipHostMallocDefault), "pinned markers");
     hip_check(hipHostMalloc((void**)&e->logits_h, QUEUE * n * 4, hipHostMallocDefault), "pinned logits");
@@ -289,17 +333,25 @@ void run_requests(Engine& e, const std::vector<Request>& reqs, bool fused, float
             const size_t q = i - c0, slot = q * e.max_length;
             memcpy(e.ids_h + slot, r.ids, r.n * 4);
             if (r.nm) memcpy(e.markers_h + slot, r.markers, r.nm * 4);
-            hip_check(hipMemcpyAsync(e.ids_d + slot, e.ids_h + slot, r.n * 4, hipMemcpyHostToDevice,
+            const bool graph = e.use_graphs && !fused;
+            // The graph reads its request from gin; otherwise the request has its own slot.
+            uint32_t* ids_dst = graph ? e.gin : e.ids_d + slot;
+            uint32_t* markers_dst = graph ? e.gin + e.max_length : e.markers_d + slot;
+            float* logits_src = graph ? e.glogits : e.logits_d + slot;
+            hipGraphExec_t ex = graph ? e.graph_for((int)r.n, (int)r.nm, (int)r.qtype) : nullptr;
+            hip_check(hipMemcpyAsync(ids_dst, e.ids_h + slot, r.n * 4, hipMemcpyHostToDevice,
                                      e.stream), "ids");
             if (r.nm)
-                hip_check(hipMemcpyAsync(e.markers_d + slot, e.markers_h + slot, r.nm * 4,
+                hip_check(hipMemcpyAsync(markers_dst, e.markers_h + slot, r.nm * 4,
                                          hipMemcpyHostToDevice, e.stream), "markers");
             hip_check(hipEventRecord(e.ev_start[q], e.stream), "hipEventRecord");
-            e.launch(e.ids_d + slot, (int)r.n, (int)r.qtype, e.markers_d + slot, (int)r.nm,
-                     e.logits_d + slot, fused);
+            if (graph)
+                hip_check(hipGraphLaunch(ex, e.stream), "hipGraphLaunch");
+            else
+                e.launch(ids_dst, (int)r.n, (int)r.qtype, markers_dst, (int)r.nm, logits_src, fused);
             hip_check(hipEventRecord(e.ev_end[q], e.stream), "hipEventRecord");
             if (r.nm)
-                hip_check(hipMemcpyAsync(e.logits_h + slot, e.logits_d + slot, r.nm * 4,
+                hip_check(hipMemcpyAsync(e.logits_h + slot, logits_src, r.nm * 4,
                                          hipMemcpyDeviceToHost, e.stream), "logits");
         }
         hip_check(hipStreamSynchronize(e.stream), "the forward pass");
@@ -543,6 +595,30 @@ int julia_hip_time_attention(const void* qkv, void* o, int n, int d, int window,
     });
 }
 
+int julia_hip_time_copy(size_t bytes, int warmup, int batches, int per_batch, float* min_us,
+                        float* median_us, char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        void *a = nullptr, *b = nullptr;
+        hipStream_t st = nullptr;
+        hip_check(hipMalloc(&a, bytes), "copy buffer");
+        try {
+            hip_check(hipMalloc(&b, bytes), "copy buffer");
+            hip_check(hipMemset(a, 1, bytes), "hipMemset");
+            hip_check(hipStreamCreate(&st), "hipStreamCreate");
+            time_calls([&] { stream_copy_launch(b, a, bytes, st); }, warmup, batches, per_batch, st,
+                       min_us, median_us);
+        } catch (...) {
+            if (st) hipStreamSynchronize(st), hipStreamDestroy(st);
+            hipFree(a);
+            if (b) hipFree(b);
+            throw;
+        }
+        hipStreamDestroy(st);
+        hipFree(a);
+        hipFree(b);
+    });
+}
+
 int julia_hip_copy(void* dst, const void* src, size_t bytes, int kind, char* err, size_t err_len) {
     return guarded(err, err_len, [&] {
         const hipMemcpyKind k = kind == 1 ? hipMemcpyHostToDevice
@@ -753,6 +829,57 @@ int julia_hip_time_encoder_step(const Engine* ce, int step, int m, int bm, int s
             gemm_launch(g, gemm_cfg(g.n, g.k), e.scratch, e.stream);
         };
         time_calls(launch, warmup, batches, per_batch, e.stream, min_us, median_us);
+    });
+}
+
+int julia_hip_profile_layer(const Engine* ce, int n, int layer, const int* plan, uint64_t* stamps,
+                            int max_blocks, int* grid, int* plan_out, char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!ce) throw std::runtime_error("no engine");
+        Engine& e = *const_cast<Engine*>(ce);
+        hip_check(hipSetDevice(e.device), "hipSetDevice");
+        if (n <= 0 || n > e.max_length) throw std::runtime_error("profile: n out of range");
+        if (layer < 0 || layer >= e.cfg.layers) throw std::runtime_error("profile: no such layer");
+        std::vector<uint32_t> ids(n);
+        for (int i = 0; i < n; i++) ids[i] = (uint32_t)(i * 7919 % e.cfg.vocab);
+        hip_check(hipMemcpy(e.ids_d, ids.data(), n * 4, hipMemcpyHostToDevice), "ids");
+        embed_launch(e.ids_d, n, e.h(e.layout.tok_embeddings), e.cfg.vocab, e.cfg.d,
+                     e.f(e.layout.emb_norm), e.cfg.norm_eps, e.x, e.stream);
+        for (int l = 0; l < layer; l++) e.launch_layer(l, n);
+        const EncoderLayer& L = e.layout.layers[layer];
+        LayerArgs a{};
+        a.x = e.x, a.qkv = e.qkv, a.o = e.o, a.mid = e.mid, a.stats_attn = e.stats_a;
+        a.stats_mlp = e.stats_b, a.wqkv = e.h(L.wqkv), a.qkv_colsum = e.f(L.qkv_colsum);
+        a.rope = e.f(L.global ? e.layout.rope_global : e.layout.rope_local);
+        a.wo = e.h(L.wo), a.wi = e.h(L.wi), a.wi_colsum = e.f(L.wi_colsum), a.wo_mlp = e.h(L.wo_mlp);
+        a.m = n, a.d = e.cfg.d, a.inter = e.cfg.inter, a.eps = e.cfg.norm_eps;
+        a.window = L.global ? 0 : e.cfg.window, a.rope_rows = e.cfg.max_positions;
+        LayerPlan p = e.layer_kernel.default_plan(n, e.cfg.d, e.cfg.inter, a.window);
+        if (plan) {
+            for (int g = 0; g < 4; g++) p.bm[g] = plan[g], p.splits[g] = plan[4 + g];
+            p.kv[0] = plan[8], p.kv[1] = plan[9];
+        }
+        const int gb = e.layer_kernel.grid(a, p);
+        if (grid) *grid = gb;
+        if (plan_out) {
+            for (int g = 0; g < 4; g++) plan_out[g] = p.bm[g], plan_out[4 + g] = p.splits[g];
+            plan_out[8] = p.kv[0], plan_out[9] = p.kv[1];
+        }
+        if (gb > max_blocks) throw std::runtime_error("profile: the stamps buffer is too small");
+        uint64_t* prof = dalloc<uint64_t>((size_t)gb * PROF_WORDS, "profile");
+        try {
+            hip_check(hipMemset(prof, 0, (size_t)gb * PROF_WORDS * 8), "hipMemset");
+            e.layer_kernel.launch(a, p, e.scratch, e.stream, 0x1f, prof);
+            hip_check(hipStreamSynchronize(e.stream), "profile");
+            if (e.layer_kernel.barrier_timed_out())
+                throw std::runtime_error("layer: a grid barrier timed out");
+            hip_check(hipMemcpy(stamps, prof, (size_t)gb * PROF_WORDS * 8, hipMemcpyDeviceToHost),
+                      "profile");
+        } catch (...) {
+            hipFree(prof);
+            throw;
+        }
+        hipFree(prof);
     });
 }
 

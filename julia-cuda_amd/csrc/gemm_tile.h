@@ -46,7 +46,6 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
         const uint32_t last = *s_last;
         __syncthreads();  // every thread has read s_last before anyone can write it again
         if (last == 0) return;
-        acquire_agent();
 #pragma unroll
         for (int ps = 0; ps < NPASS; ps++)
 #pragma unroll
@@ -57,7 +56,7 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
             for (int ps = 0; ps < NPASS; ps++)
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
-                    const float4 q = *(const float4*)(src + ((ps * 2 + h) * 256 + tid) * 4);
+                    const float4 q = xload16f(src + ((ps * 2 + h) * 256 + tid) * 4);
                     v[ps][4 * h] += q.x;
                     v[ps][4 * h + 1] += q.y;
                     v[ps][4 * h + 2] += q.z;
@@ -110,37 +109,36 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Two K steps in flight: the next step's fragments load while the current one multiplies.
-    half8 fa0[MI], fw0[4], fa1[MI], fw1[4];
-    int u = u0;
-    if (u < u1) {
+    // The wave's K steps in chunks of up to UMAX, each chunk's fragments all loaded before its
+    // MFMAs: a small tile's K loop is latency-bound, so one round trip per chunk instead of one
+    // per step. The a operand (an activation) comes through the coherent path when XG.
+    //
+    // The loads are unconditional (a step past the wave's range re-reads its last step, and its
+    // a fragment is masked to zero without a branch): a guarded load becomes a branch, and the
+    // compiler drains every outstanding load at each branch, which would serialise the steps.
+    constexpr int UMAX = MI == 1 ? 9 : (MI == 2 ? 6 : 4);
+    for (int u = u0; u < u1; u += UMAX) {
+        half8 fa[UMAX][MI], fw[UMAX][4];
 #pragma unroll
-        for (int i = 0; i < MI; i++) fa0[i] = *(const half8*)(ap[i] + u * 32);
+        for (int s = 0; s < UMAX; s++) {
+            const int uu = min(u + s, u1 - 1);
 #pragma unroll
-        for (int j = 0; j < 4; j++) fw0[j] = *(const half8*)(wp[j] + u * 32);
-    }
-    for (; u < u1; u += 2) {
-        if (u + 1 < u1) {
+            for (int j = 0; j < 4; j++) fw[s][j] = *(const half8*)(wp[j] + uu * 32);
 #pragma unroll
-            for (int i = 0; i < MI; i++) fa1[i] = *(const half8*)(ap[i] + (u + 1) * 32);
-#pragma unroll
-            for (int j = 0; j < 4; j++) fw1[j] = *(const half8*)(wp[j] + (u + 1) * 32);
+            for (int i = 0; i < MI; i++) fa[s][i] = load16h<XG>(ap[i] + uu * 32);
         }
+        // Keep the scheduler from interleaving the MFMAs into the loads (it would reuse the
+        // fragment registers and wait for each step's loads before issuing the next).
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < MI; i++)
+        for (int s = 0; s < UMAX; s++) {
+            const uint32_t keep = u + s < u1 ? 0xffffffffu : 0u;
 #pragma unroll
-            for (int j = 0; j < 4; j++) acc[i][j] = mfma16(fw0[j], fa0[i], acc[i][j]);
-        if (u + 1 < u1) {
-            if (u + 2 < u1) {
+            for (int i = 0; i < MI; i++) {
+                const half8 a = mask16(fa[s][i], keep);
 #pragma unroll
-                for (int i = 0; i < MI; i++) fa0[i] = *(const half8*)(ap[i] + (u + 2) * 32);
-#pragma unroll
-                for (int j = 0; j < 4; j++) fw0[j] = *(const half8*)(wp[j] + (u + 2) * 32);
+                for (int j = 0; j < 4; j++) acc[i][j] = mfma16(fw[s][j], a, acc[i][j]);
             }
-#pragma unroll
-            for (int i = 0; i < MI; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = mfma16(fw1[j], fa1[i], acc[i][j]);
         }
     }
 

@@ -121,5 +121,6 @@ void norm_add_launch(const jh_half* x, int n, int d, const float* gamma, const f
                      float eps, jh_half* out, float* stats, hipStream_t stream);
 void score_launch(const jh_half* y, int n, int d, const jh_half* w, float b,
                   const uint32_t* markers, int k, float* logits, hipStream_t stream);
+void stream_copy_launch(void* dst, const void* src, size_t bytes, hipStream_t stream);
 
 }  // namespace jh

@@ -14,6 +14,9 @@ namespace jh {
 
 // u32 words of device memory the grid barrier needs (zeroed once; every barrier leaves them zero).
 constexpr int BAR_WORDS = 11 * 32;
+// u64 words per block of the layer kernel's timestamps: (start, end) of phase p at 2p, 2p + 1
+// (100 MHz clock), the block's CU id at 10.
+constexpr int PROF_WORDS = 16;
 
 struct LayerArgs {
     jh_half *x, *qkv, *o, *mid;
@@ -44,8 +47,9 @@ public:
     size_t ws_floats(int max_m, int d, int inter) const;
     size_t counters(int max_m, int d, int inter) const;
     // Phases: bits 0-4 select qkv, attention, wo, wi, wo_mlp (0x1f: the whole layer).
+    // prof: null, or PROF_WORDS u64 per block of the grid (grid()).
     void launch(const LayerArgs& a, const LayerPlan& plan, const Scratch& s, hipStream_t stream,
-                unsigned phases = 0x1f);
+                unsigned phases = 0x1f, uint64_t* prof = nullptr);
     int grid(const LayerArgs& a, const LayerPlan& plan) const;
     // Whether a grid barrier gave up waiting since the last call (then clears the flag).
     // Synchronizes with the device.

@@ -24,7 +24,23 @@ struct LayerParams {
     int epi0;         // EPI_K_ROPE (layer 0) or EPI_K_LNROPE
     unsigned phases;  // bits 0-4
     uint32_t* bar;    // the barrier's words (BAR_WORDS, zero between launches)
+    uint64_t* prof;   // null, or PROF_WORDS per block: see stamp()
 };
+
+// Per-phase timestamps (the reference's kernels/src/prof.rs): thread 0 of each block writes the
+// GPU-wide constant-rate clock (100 MHz) at each phase's start (after the barrier before it)
+// into word 2p and at its end (after the block's last task, before the barrier after it) into
+// word 2p + 1, and its CU id into word 10.
+__device__ __forceinline__ void stamp(uint64_t* prof, int slot) {
+    if (prof && threadIdx.x == 0) prof[(size_t)blockIdx.x * PROF_WORDS + slot] = wall_clock64();
+}
+
+__device__ __forceinline__ void stamp_end(uint64_t* prof, int phase) {
+    if (prof) {
+        __syncthreads();  // the whole block is done with the phase (profiling only)
+        stamp(prof, 2 * phase + 1);
+    }
+}
 
 // The grid barrier's words, each on its own 128-byte line: eight group arrival counters, the
 // count of groups complete, the generation, and the time-out flag.
@@ -37,11 +53,11 @@ constexpr int BAR_GROUPS = 8 * BAR_LINE, BAR_GEN = 9 * BAR_LINE, BAR_TIMEOUT = 1
 // group advances the generation that every block waits on, and each counter is reset by its
 // last arrival, so the words are zero again at the end of every barrier.
 //
-// The phase outputs are stored device-coherent (XG), so the release is only each wave waiting
-// for its stores to complete; after the barrier every wave invalidates its L1/L2 view (the
-// acquire) before reading other blocks' outputs. The wait is bounded: past ~0.2 s (far beyond
-// any real barrier) it gives up and raises the time-out flag, which the host turns into an
-// error, so a broken launch cannot hang the GPU.
+// The phase outputs are stored device-coherent and read back through the coherent path (XG), so
+// the release is only each wave waiting for its stores to complete, and no cache needs
+// invalidating after the barrier (the weights other blocks share through L2 stay cached). The
+// wait is bounded: past ~0.2 s (far beyond any real barrier) it gives up and raises the time-out
+// flag, which the host turns into an error, so a broken launch cannot hang the GPU.
 __device__ __forceinline__ void grid_sync(uint32_t* bar) {
     release_wait();
     __syncthreads();
@@ -69,7 +85,6 @@ __device__ __forceinline__ void grid_sync(uint32_t* bar) {
         }
     }
     __syncthreads();
-    acquire_agent();
 }
 
 constexpr int LAYER_LDS_FLOATS = lat_lds_floats<32>();
@@ -94,31 +109,44 @@ __global__ __launch_bounds__(256) void layer_kernel(LayerParams P) {
     auto sync_if = [&](int next) {
         if (on(next)) grid_sync(P.bar);
     };
+    if (P.prof && threadIdx.x == 0) P.prof[(size_t)blockIdx.x * PROF_WORDS + 10] = __smid();
     if (on(0)) {
+        stamp(P.prof, 0);
         if (P.epi0 == EPI_K_LNROPE)
             gemm_phase<EPI_K_LNROPE>(P.g[0], P.bm[0], lds, &s_last);
         else
             gemm_phase<EPI_K_ROPE>(P.g[0], P.bm[0], lds, &s_last);
+        stamp_end(P.prof, 0);
         sync_if(1);
     }
     if (on(1)) {
+        stamp(P.prof, 2);
         const AttnParams& a = P.at;
         const int heads = a.d >> 6, T = ((a.n + 63) >> 6) * heads * a.chunks;
         for (int t = blockIdx.x; t < T; t += gridDim.x) {
             const int tile = t / a.chunks;
             attention_tile<true>(a, tile / heads, tile % heads, t % a.chunks, (f16*)lds, &s_last);
         }
+        stamp_end(P.prof, 1);
         sync_if(2);
     }
     if (on(2)) {
+        stamp(P.prof, 4);
         gemm_phase<EPI_K_RESSTATS>(P.g[1], P.bm[1], lds, &s_last);
+        stamp_end(P.prof, 2);
         sync_if(3);
     }
     if (on(3)) {
+        stamp(P.prof, 6);
         gemm_phase<EPI_K_LNGEGLU>(P.g[2], P.bm[2], lds, &s_last);
+        stamp_end(P.prof, 3);
         sync_if(4);
     }
-    if (on(4)) gemm_phase<EPI_K_RESSTATS>(P.g[3], P.bm[3], lds, &s_last);
+    if (on(4)) {
+        stamp(P.prof, 8);
+        gemm_phase<EPI_K_RESSTATS>(P.g[3], P.bm[3], lds, &s_last);
+        stamp_end(P.prof, 4);
+    }
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -209,7 +237,7 @@ int LayerKernel::grid(const LayerArgs& a, const LayerPlan& plan) const {
 }
 
 void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratch& s,
-                         hipStream_t stream, unsigned phases) {
+                         hipStream_t stream, unsigned phases, uint64_t* prof) {
     auto fail = [&](const std::string& m) { throw std::runtime_error("layer: " + m); };
     if (per_cu_ <= 0) fail("the layer kernel does not fit on a CU");
     if (!bar_) fail("no grid-barrier counter");
@@ -248,6 +276,7 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
     P.epi0 = g[0].epi;
     P.phases = phases;
     P.bar = bar_;
+    P.prof = prof;
 
     const int grid_blocks = grid(a, plan);
     // A barrier between two consecutive selected phases only (the kernel's sync_if).

@@ -3,6 +3,7 @@
 // (the scorer's last linear on the marker rows). The reference's are kernels/src/main.rs:47-200
 // (one 32-lane warp per row, D fixed at 384); here D is any multiple of 64 and a lane takes
 // 4 f16 (8 bytes) at a time, 64 lanes covering 512 contiguous bytes per step.
+#include <algorithm>
 #include <stdexcept>
 #include <string>
 
@@ -124,6 +125,25 @@ __global__ __launch_bounds__(256) void score_kernel(const f16* y, int n, int d, 
         for (int e = 0; e < 4; e++) acc += v[j][e] * u[j][e];
     acc = wave_sum(acc);
     if (lane == 0) logits[i] = acc + b;
+}
+
+// dst = src, 16 bytes per thread per step, grid-stride: the plain copy kernel the byte counters
+// (rocprofv3 FETCH_SIZE / WRITE_SIZE) are calibrated against, and the achievable-bandwidth
+// probe for the bandwidth-bound kernels.
+__global__ __launch_bounds__(256) void stream_copy_kernel(const uint4* src, uint4* dst, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+        dst[i] = src[i];
+}
+
+void stream_copy_launch(void* dst, const void* src, size_t bytes, hipStream_t st) {
+    if (bytes % 16 || ((uintptr_t)dst % 16) || ((uintptr_t)src % 16))
+        throw std::runtime_error("copy: 16-byte aligned buffers and sizes only");
+    const size_t n = bytes / 16;
+    const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 8192);
+    if (n) hipLaunchKernelGGL(stream_copy_kernel, dim3(blocks), dim3(256), 0, st, (const uint4*)src,
+                              (uint4*)dst, n);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) throw std::runtime_error(std::string("copy: ") + hipGetErrorString(e));
 }
 
 namespace {

@@ -78,12 +78,12 @@ EXPORTS = [
     "julia_cuda_tier", "julia_cuda_load", "julia_cuda_free", "julia_cuda_device", "julia_cuda_run",
     "julia_hip_scratch_new", "julia_hip_scratch_free", "julia_hip_gemm", "julia_hip_attention",
     "julia_hip_embed", "julia_hip_norm_add", "julia_hip_score", "julia_hip_time_gemm",
-    "julia_hip_time_attention", "julia_hip_copy", "julia_hip_device_count",
+    "julia_hip_time_attention", "julia_hip_time_copy", "julia_hip_copy", "julia_hip_device_count",
     "julia_hip_prep_fold_layernorm", "julia_hip_prep_fold_layernorm_bias",
     "julia_hip_prep_geglu_rows", "julia_hip_prep_rope_table", "julia_hip_synth",
     "julia_hip_round_f16", "julia_hip_gemm_choose", "julia_hip_gemm_plan_2080ti",
     "julia_hip_gemm_choose_2080ti", "julia_hip_engine_info_get", "julia_hip_engine_tensor",
-    "julia_hip_time_encoder_step", "julia_hip_run_trace",
+    "julia_hip_time_encoder_step", "julia_hip_profile_layer", "julia_hip_run_trace",
 ]
 
 _VP, _SZ, _I, _F, _CP = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_char_p
@@ -116,6 +116,8 @@ def lib():
                                      ctypes.POINTER(_F), ctypes.POINTER(_F), _CP, _SZ]),
         "julia_hip_time_attention": (_I, [_VP, _VP, _I, _I, _I, _I, _VP, _I, _I, _I,
                                           ctypes.POINTER(_F), ctypes.POINTER(_F), _CP, _SZ]),
+        "julia_hip_time_copy": (_I, [_SZ, _I, _I, _I, ctypes.POINTER(_F), ctypes.POINTER(_F),
+                                     _CP, _SZ]),
         "julia_hip_copy": (_I, [_VP, _VP, _SZ, _I, _CP, _SZ]),
         "julia_hip_device_count": (_I, []),
         "julia_hip_prep_fold_layernorm": (None, [_F32P, _F32P, _I, _I, _U16P, _F32P]),
@@ -134,6 +136,8 @@ def lib():
         "julia_hip_engine_tensor": (_VP, [_VP, _CP, _I, ctypes.POINTER(_SZ)]),
         "julia_hip_time_encoder_step": (_I, [_VP, _I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_F),
                                              ctypes.POINTER(_F), _CP, _SZ]),
+        "julia_hip_profile_layer": (_I, [_VP, _I, _I, _VP, _VP, _I, ctypes.POINTER(_I), _VP, _CP,
+                                         _SZ]),
         "julia_hip_run_trace": (_I, [_VP, _VP, _SZ, _VP, _SZ, ctypes.c_uint32, _I, _VP, _VP, _VP,
                                      _CP, _SZ]),
     }
@@ -243,6 +247,17 @@ class Engine:
               splits, warmup, batches, per_batch, ctypes.byref(mn), ctypes.byref(md))
         return mn.value, md.value
 
+    def profile_layer(self, n, layer=1, plan=None):
+        """The layer kernel's per-block phase stamps (src/profile.rs): returns (plan, stamps
+        [grid][16] u64 of a 100 MHz clock)."""
+        stamps = np.zeros((4096, 16), np.uint64)
+        grid = ctypes.c_int()
+        pin = None if plan is None else np.ascontiguousarray(plan, np.int32)
+        pout = np.zeros(10, np.int32)
+        _call(lib().julia_hip_profile_layer, self.ptr, n, layer, _np_ptr(pin), _np_ptr(stamps),
+              4096, ctypes.byref(grid), _np_ptr(pout))
+        return pout, stamps[: grid.value]
+
     def tensor(self, name, index=0):
         """(device address, bytes) of a prepared weight tensor."""
         nb = ctypes.c_size_t()
@@ -312,6 +327,14 @@ def time_attention(qkv, o, n, d, window=0, chunks=1, scratch=None, warmup=20, ba
     mn, md = ctypes.c_float(), ctypes.c_float()
     _call(lib().julia_hip_time_attention, qkv, o, n, d, window, chunks,
           scratch.ptr if scratch else None, warmup, batches, per_batch, ctypes.byref(mn),
+          ctypes.byref(md))
+    return mn.value, md.value
+
+
+def time_copy(nbytes, warmup=20, batches=10, per_batch=50):
+    """(min, median) microseconds of the library's plain device copy of nbytes."""
+    mn, md = ctypes.c_float(), ctypes.c_float()
+    _call(lib().julia_hip_time_copy, nbytes, warmup, batches, per_batch, ctypes.byref(mn),
           ctypes.byref(md))
     return mn.value, md.value
 

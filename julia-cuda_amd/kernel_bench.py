@@ -1,0 +1,41 @@
+"""Runs one encoder step of the engine repeatedly, for profilers (rocprofv3 --kernel-trace /
+--pmc): the same launches as the forward pass, rotating through the layers' weights, plus a
+plain device-to-device copy of a known size to calibrate byte counters against.
+
+    python julia-cuda_amd/kernel_bench.py --step wi --tokens 293 --iters 200 --copy-mb 64
+
+Prints the step's median time per call (HIP events) and the copy's bytes.
+"""
+
+import argparse
+import os
+import sys
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+import julia_hip as jh  # noqa: E402
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--step", default="qkv", choices=list(jh.Engine.STEPS))
+    ap.add_argument("--tokens", type=int, default=293)
+    ap.add_argument("--iters", type=int, default=200)
+    ap.add_argument("--bm", type=int, default=0)
+    ap.add_argument("--splits", type=int, default=1)
+    ap.add_argument("--copy-mb", type=int, default=64)
+    ap.add_argument("--spec", default="synthetic")
+    args = ap.parse_args()
+    e = jh.Engine(args.spec, max_length=max(1024, args.tokens))
+    mn, md = e.time_step(args.step, args.tokens, args.bm, args.splits, warmup=10, batches=1,
+                         per_batch=args.iters)
+    print(f"{args.step} at {args.tokens} tokens: {md:.2f} us per call", flush=True)
+    if args.copy_mb:
+        nbytes = args.copy_mb << 20
+        mn, md = jh.time_copy(nbytes, warmup=2, batches=1, per_batch=5)
+        print(f"stream_copy_kernel: {nbytes} bytes read and {nbytes} written per call, "
+              f"{md:.2f} us, {2 * nbytes / md / 1e3:.0f} GB/s", flush=True)
+    e.close()
+
+
+if __name__ == "__main__":
+    main()
