@@ -75,7 +75,8 @@ enum {
 };
 
 /* One GEMM (src/gemm.rs:226-245 `Gemm`): c = epilogue(a . w^T), a [m][k], w [n][k], c [m][n]
- * ([m][n/2] with GeGLU), all f16. Row statistics are (sum, sum of squares) f32 pairs per row and
+ * ([m][n/2] with GeGLU), all f16; w is passed packed in MFMA fragment order
+ * (julia_hip_prep_pack_frag; the engine's weights are stored so). Row statistics are (sum, sum of squares) f32 pairs per row and
  * 64-column group: stats_in [m][k/64][2] (the LayerNorm epilogues), stats_out [m][n/64][2]
  * (the residual epilogues; written, no clearing needed). colsum and bias have n floats, rope is
  * [rope_rows][32][2] (cos, sin), positions (nullable) gives each row's position. */
@@ -163,6 +164,12 @@ void julia_hip_prep_fold_layernorm_bias(const float *w, const float *gamma, cons
 /* The GeGLU row interleave of this library's epilogue (the reference's is src/prep.rs:61-77):
  * src[p] = the checkpoint row of Wi that packed row p holds. */
 void julia_hip_prep_geglu_rows(int inter, int32_t *src);
+/* w [n][k] f16 bits (n % 64 == 0, k % 32 == 0) <-> the GEMM kernels' fragment order: for
+ * 64-row group G, 32-column unit u, 16-row fragment j and lane l < 64, the 8 values
+ * w[64 G + 16 j + l % 16][32 u + 8 (l / 16) + e], e < 8, contiguous, in that nesting. A layout
+ * transform of this library's, like the reference's row permutations (src/prep.rs:61-101). */
+void julia_hip_prep_pack_frag(const uint16_t *w, int n, int k, uint16_t *out);
+void julia_hip_prep_unpack_frag(const uint16_t *packed, int n, int k, uint16_t *w);
 /* src/prep.rs:103-118: RoPE (cos, sin) [npos][32][2]. */
 void julia_hip_prep_rope_table(float theta, int npos, float *table);
 /* The synthetic generator: elements start..start+count of tensor `id`, mean + std * N(0, 1). */

@@ -186,40 +186,96 @@ __device__ __forceinline__ int xcd_task(int b, int T) {
 // gcol + 32 + c0 + e (hi), e < 4, where gcol is a multiple of 64 (the tile's 64-column group
 // `grp`) and c0 a multiple of 4 below 32. The 8 threads sharing a row are 8 consecutive lanes
 // (lane % 8 = c0 / 4), which the statistics reduce over. `valid` is row < m; every thread calls
-// this (the reduction needs the whole group).
+// this (the reductions need the whole group).
 //
 // Order as the reference's gemm_tile (kernels/src/main.rs:931-1038): LayerNorm from the input
 // statistics, bias, ReLU, GELU, RoPE, then GeGLU or the store with the residual and the output
 // statistics of the stored f16 values. XG: the outputs are read by other blocks of the same
 // kernel (the persistent layer kernel's next phase), so they are stored device-coherent.
-template <int EPI, bool XG = false>
-__device__ __forceinline__ void epilogue(const GemmParams& p, int row, int grp, int c0, float* v,
-                                         bool valid) {
+//
+// Everything the epilogue reads besides the accumulator (statistics, colsum, bias, the RoPE
+// table, the residual) is loaded by epi_load_* when the tile starts, so those loads overlap the
+// operand loads instead of costing dependent round trips after the K loop. The loads are
+// unconditional (rows past m read row m - 1, never stored) and masked in epi_apply: a guarded
+// load is a branch, where the compiler waits for every outstanding load.
+
+// Statistics slots one lane of a row's 8-lane group prefetches: j and j + 8 (j = lane % 8), all
+// of a row with k <= 1024; epi_apply loads the rest of a wider row itself.
+constexpr int EPI_PRE_SLOTS = 2;
+
+struct EpiCol {  // per column: colsum (LN) and bias, lo and hi halves
+    float4 cs[2], bs[2];
+};
+struct EpiRow {  // per row: statistics slots, RoPE (cos, sin) pairs, residual lo and hi
+    float2 st[EPI_PRE_SLOTS];
+    float4 rt[2];
+    half4 rl, rh;
+};
+
+template <int EPI>
+__device__ __forceinline__ void epi_load_col(const GemmParams& p, int grp, int c0, EpiCol& e) {
     const int gcol = grp * 64;
     if (EPI & EPI_LN) {
-        if (valid) {
-            const int slots = p.k >> 6;
-            const float* st = p.stats_in + (size_t)row * slots * 2;
-            float S = 0.0f, Q = 0.0f;
-            for (int s = 0; s < slots; s++) {
-                const float2 sq = load8f<XG>(st + 2 * s);
-                S += sq.x;
-                Q += sq.y;
-            }
-            const float mean = S / (float)p.k;
-            const float var = fmaxf(Q / (float)p.k - mean * mean, 0.0f);
-            const float rs = 1.0f / sqrtf(var + p.eps);
-            const float4 a = *(const float4*)(p.colsum + gcol + c0);
-            const float4 b = *(const float4*)(p.colsum + gcol + 32 + c0);
-            const float cs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = rs * (v[e] - mean * cs[e]);
-        }
+        e.cs[0] = *(const float4*)(p.colsum + gcol + c0);
+        e.cs[1] = *(const float4*)(p.colsum + gcol + 32 + c0);
     }
     if (EPI & EPI_BIAS) {
-        const float4 a = *(const float4*)(p.bias + gcol + c0);
-        const float4 b = *(const float4*)(p.bias + gcol + 32 + c0);
-        const float bs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        e.bs[0] = *(const float4*)(p.bias + gcol + c0);
+        e.bs[1] = *(const float4*)(p.bias + gcol + 32 + c0);
+    }
+}
+
+template <int EPI, bool XG>
+__device__ __forceinline__ void epi_load_row(const GemmParams& p, int row, int grp, int c0,
+                                             EpiRow& e) {
+    const int r = min(row, p.m - 1);
+    if (EPI & EPI_LN) {
+        const int slots = p.k >> 6, j = c0 >> 2;
+        const float* st = p.stats_in + (size_t)r * slots * 2;
+#pragma unroll
+        for (int i = 0; i < EPI_PRE_SLOTS; i++) e.st[i] = load8f<XG>(st + 2 * min(j + 8 * i, slots - 1));
+    }
+    if (EPI & EPI_ROPE) {
+        const int pos = min(p.pos ? max(p.pos[r], 0) : r, p.rope_rows - 1);
+        const float4* t = (const float4*)(p.rope + ((size_t)pos * 32 + c0) * 2);
+        e.rt[0] = t[0];
+        e.rt[1] = t[1];
+    }
+    if ((EPI & EPI_RES) && !(EPI & EPI_GEGLU)) {
+        const f16* x = (const f16*)p.c + (size_t)r * p.n + grp * 64 + c0;
+        e.rl = load8h<XG>(x);
+        e.rh = load8h<XG>(x + 32);
+    }
+}
+
+template <int EPI, bool XG = false>
+__device__ __forceinline__ void epi_apply(const GemmParams& p, int row, int grp, int c0, float* v,
+                                          bool valid, const EpiCol& ec, const EpiRow& er) {
+    const int gcol = grp * 64;
+    if (EPI & EPI_LN) {
+        const int slots = p.k >> 6, j = c0 >> 2;
+        float S = 0.0f, Q = 0.0f;
+#pragma unroll
+        for (int i = 0; i < EPI_PRE_SLOTS; i++)
+            if (j + 8 * i < slots) S += er.st[i].x, Q += er.st[i].y;
+        const float* st = p.stats_in + (size_t)min(row, p.m - 1) * slots * 2;
+        for (int s = j + 8 * EPI_PRE_SLOTS; s < slots; s += 8) {  // rows wider than 1024
+            const float2 sq = load8f<XG>(st + 2 * s);
+            S += sq.x, Q += sq.y;
+        }
+        S = group_sum<8>(S);
+        Q = group_sum<8>(Q);
+        const float mean = S / (float)p.k;
+        const float var = fmaxf(Q / (float)p.k - mean * mean, 0.0f);
+        const float rs = 1.0f / sqrtf(var + p.eps);
+        const float cs[8] = {ec.cs[0].x, ec.cs[0].y, ec.cs[0].z, ec.cs[0].w,
+                             ec.cs[1].x, ec.cs[1].y, ec.cs[1].z, ec.cs[1].w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = rs * (v[e] - mean * cs[e]);
+    }
+    if (EPI & EPI_BIAS) {
+        const float bs[8] = {ec.bs[0].x, ec.bs[0].y, ec.bs[0].z, ec.bs[0].w,
+                             ec.bs[1].x, ec.bs[1].y, ec.bs[1].z, ec.bs[1].w};
 #pragma unroll
         for (int e = 0; e < 8; e++) v[e] += bs[e];
     }
@@ -233,10 +289,8 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int row, int grp, 
     }
     if (EPI & EPI_ROPE) {
         // q and k heads: columns i and i + 32 of a head are the rotate-half pair of dimension i.
-        if (valid && gcol < p.rope_cols) {
-            const int pos = p.pos ? p.pos[row] : row;
-            const float4* t = (const float4*)(p.rope + ((size_t)pos * 32 + c0) * 2);
-            const float4 t0 = t[0], t1 = t[1];
+        if (gcol < p.rope_cols) {
+            const float4 t0 = er.rt[0], t1 = er.rt[1];
             const float cs[4] = {t0.x, t0.z, t1.x, t1.z}, sn[4] = {t0.y, t0.w, t1.y, t1.w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
@@ -257,32 +311,29 @@ __device__ __forceinline__ void epilogue(const GemmParams& p, int row, int grp, 
     } else {
         half4 lo, hi;
         f16* out = (f16*)p.c + (size_t)row * p.n + gcol + c0;
-        if (valid) {
-            if (EPI & EPI_RES) {
-                const half4 rl = load8h<XG>(out), rh = load8h<XG>(out + 32);
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    v[e] += (float)rl[e];
-                    v[4 + e] += (float)rh[e];
-                }
-            }
+        if (EPI & EPI_RES) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                lo[e] = (f16)v[e];
-                hi[e] = (f16)v[4 + e];
+                v[e] += (float)er.rl[e];
+                v[4 + e] += (float)er.rh[e];
             }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            lo[e] = (f16)v[e];
+            hi[e] = (f16)v[4 + e];
+        }
+        if (valid) {
             store8<XG>(out, lo);
             store8<XG>(out + 32, hi);
         }
         if (EPI & EPI_STATS) {
             float s = 0.0f, q = 0.0f;
-            if (valid) {
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const float a = (float)lo[e], b = (float)hi[e];
-                    s += a + b;
-                    q += a * a + b * b;
-                }
+            for (int e = 0; e < 4; e++) {
+                const float a = (float)lo[e], b = (float)hi[e];
+                s += a + b;
+                q += a * a + b * b;
             }
             s = group_sum<8>(s);
             q = group_sum<8>(q);

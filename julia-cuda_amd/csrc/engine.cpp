@@ -649,6 +649,14 @@ void julia_hip_prep_fold_layernorm_bias(const float* w, const float* gamma, cons
 
 void julia_hip_prep_geglu_rows(int inter, int32_t* src) { geglu_rows(inter, src); }
 
+void julia_hip_prep_pack_frag(const uint16_t* w, int n, int k, uint16_t* out) {
+    if (n > 0 && k > 0 && n % 64 == 0 && k % 32 == 0) pack_frag(w, n, k, out);
+}
+
+void julia_hip_prep_unpack_frag(const uint16_t* packed, int n, int k, uint16_t* w) {
+    if (n > 0 && k > 0 && n % 64 == 0 && k % 32 == 0) unpack_frag(packed, n, k, w);
+}
+
 void julia_hip_prep_rope_table(float theta, int npos, float* table) {
     rope_table(theta, npos, table);
 }

@@ -33,11 +33,12 @@ __global__ __launch_bounds__(256) void gemm_lat(GemmParams p) {
 
 // ---------------------------------------------------------------------------------------------
 // gemm_tput: BM x 128 tiles (BM = 128 or 256), BK = 64, 4 waves in a 2 x 2 grid, each owning
-// (BM/2) x 64 of the output. a and w tiles go global -> registers -> swizzled LDS, two stages;
-// the next stage's global loads are in flight while the current one feeds the MFMAs.
+// (BM/2) x 64 of the output. a and w tiles go global -> registers -> LDS, two stages; the next
+// stage's global loads are in flight while the current one feeds the MFMAs.
 //
-// LDS tile rows are 64 f16 (128 B) as eight 16-B chunks; chunk c of row r is stored at chunk
-// c ^ (r & 7), so the 16 rows one fragment load reads spread over all banks.
+// a tile rows are 64 f16 (128 B) as eight 16-B chunks; chunk c of row r is stored at chunk
+// c ^ (r & 7), so the 16 rows one fragment load reads spread over all banks. w arrives in
+// fragment order and stays so in LDS: a lane's fragment is 16 contiguous bytes.
 template <int BM>
 struct Tput {
     static constexpr int BN = 128, BK = 64;
@@ -79,17 +80,18 @@ __global__ __launch_bounds__(256) void gemm_tput(GemmParams p) {
         const int q = tid + 256 * h, r = q >> 3;
         ag[h] = (const f16*)p.a + (size_t)min(by * BM + r, p.m - 1) * p.k + (q & 7) * 8;
     }
+    // w in fragment order: the stage's four 2048-value blocks (64-row group 2 bx + h / 2, K unit
+    // 2 kt + h % 2) are copied as they are; thread tid takes value tid * 8 of each.
+    const int U = p.k >> 5;
 #pragma unroll
-    for (int h = 0; h < C::W_PER; h++) {
-        const int q = tid + 256 * h, r = q >> 3;
-        wg[h] = (const f16*)p.w + (size_t)(bx * C::BN + r) * p.k + (q & 7) * 8;
-    }
+    for (int h = 0; h < C::W_PER; h++)
+        wg[h] = (const f16*)p.w + ((size_t)(2 * bx + (h >> 1)) * U + (h & 1)) * 2048 + tid * 8;
     half8 ra[C::A_PER], rw[C::W_PER];
     auto gload = [&](int kt) {
 #pragma unroll
         for (int h = 0; h < C::A_PER; h++) ra[h] = *(const half8*)(ag[h] + kt * C::BK);
 #pragma unroll
-        for (int h = 0; h < C::W_PER; h++) rw[h] = *(const half8*)(wg[h] + kt * C::BK);
+        for (int h = 0; h < C::W_PER; h++) rw[h] = *(const half8*)(wg[h] + (size_t)kt * 4096);
     };
     auto lstore = [&](int stage) {
         f16* as = sm + stage * C::STAGE;
@@ -100,10 +102,7 @@ __global__ __launch_bounds__(256) void gemm_tput(GemmParams p) {
             *(half8*)(as + swz(q >> 3, q & 7)) = ra[h];
         }
 #pragma unroll
-        for (int h = 0; h < C::W_PER; h++) {
-            const int q = tid + 256 * h;
-            *(half8*)(ws + swz(q >> 3, q & 7)) = rw[h];
-        }
+        for (int h = 0; h < C::W_PER; h++) *(half8*)(ws + h * 2048 + tid * 8) = rw[h];
     };
 
     floatx4 acc[C::MI][4];
@@ -130,7 +129,7 @@ __global__ __launch_bounds__(256) void gemm_tput(GemmParams p) {
                 fa[i] = *(const half8*)(as + swz(wm * C::WM + 16 * i + r16, 4 * s + g));
 #pragma unroll
             for (int j = 0; j < 4; j++)
-                fw[j] = *(const half8*)(ws + swz(wn * 64 + 16 * j + r16, 4 * s + g));
+                fw[j] = *(const half8*)(ws + (wn * 2 + s) * 2048 + (j * 64 + l) * 8);
 #pragma unroll
             for (int i = 0; i < C::MI; i++)
 #pragma unroll
@@ -153,6 +152,12 @@ __global__ __launch_bounds__(256) void gemm_tput(GemmParams p) {
                 for (int j = 0; j < 4; j++)
                     *(floatx4*)&out[(wm * C::WM + 16 * i + r16) * 68 + 16 * j + 4 * g] = acc[i][j];
         }
+        EpiCol ec;
+        EpiRow er[NPASS];
+        epi_load_col<EPI>(p, bx * 2 + grp, c0, ec);
+#pragma unroll
+        for (int ps = 0; ps < NPASS; ps++)
+            epi_load_row<EPI, false>(p, by * BM + ps * 32 + (tid >> 3), bx * 2 + grp, c0, er[ps]);
         __syncthreads();
         float v[NPASS][8];
 #pragma unroll
@@ -165,7 +170,7 @@ __global__ __launch_bounds__(256) void gemm_tput(GemmParams p) {
         __syncthreads();  // every thread has read the group before the next one is written
         // Each 64-column group is its own split-K "tile" (two per block).
         finish<NPASS, EPI>(p, v, (bx * p.tiles_m + by) * 2 + grp, z, by * BM, bx * 2 + grp, BM,
-                           &s_last);
+                           &s_last, ec, er);
     }
 }
 
@@ -222,7 +227,8 @@ void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
         fail("colsum must be 16-byte and stats 8-byte aligned");
     const bool rope = g.epi & EPI_ROPE;
     if (rope != (g.rope != nullptr)) fail("a RoPE table goes with the rope epilogues");
-    if (rope && (g.n % 192 || (!g.pos && g.rope_rows < g.m) || !aligned(g.rope, 16)))
+    if (rope && (g.n % 192 || g.rope_rows < 1 || (!g.pos && g.rope_rows < g.m) ||
+                 !aligned(g.rope, 16)))
         fail("the RoPE table is too short for " + std::to_string(g.m) +
              " positions, or n = " + std::to_string(g.n) + " isn't qkv");
     const bool stats = g.epi & EPI_STATS;
@@ -264,6 +270,7 @@ void gemm_launch(const Gemm& g, GemmConfig cfg, const Scratch& s, hipStream_t st
     p.stats_out = g.stats_out, p.ws = s.ws, p.counters = s.counters;
     p.m = g.m, p.n = g.n, p.k = g.k, p.eps = g.eps;
     p.rope_cols = (g.epi & EPI_ROPE) ? 2 * (g.n / 3) : 0;
+    p.rope_rows = g.rope_rows;
     p.splits = cfg.splits;
     p.tiles_n = g.n / (cfg.bm >= 128 ? 128 : 64);
     p.tiles_m = (g.m + cfg.bm - 1) / cfg.bm;

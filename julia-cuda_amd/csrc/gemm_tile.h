@@ -22,7 +22,8 @@ constexpr int lat_lds_floats() { return 4 * BM * 68; }
 template <int NPASS, int EPI, bool XG = false>
 __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8], int tile_id,
                                        int z, int row0, int grp, int rows_in_tile,
-                                       uint32_t* s_last) {
+                                       uint32_t* s_last, const EpiCol& ec,
+                                       const EpiRow (&er)[NPASS]) {
     const int tid = threadIdx.x;
     if (p.splits > 1) {
         // [tile][split][pass][half][thread] float4s: coalesced stores and loads.
@@ -69,7 +70,7 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
     for (int ps = 0; ps < NPASS; ps++) {
         const int r = ps * 32 + (tid >> 3);
         const int row = row0 + r;
-        epilogue<EPI, XG>(p, row, grp, c0, v[ps], r < rows_in_tile && row < p.m);
+        epi_apply<EPI, XG>(p, row, grp, c0, v[ps], r < rows_in_tile && row < p.m, ec, er[ps]);
     }
 }
 
@@ -100,8 +101,18 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
         const int row = min(by * BM + 16 * i + r16, p.m - 1);  // rows past m: read, never stored
         ap[i] = (const f16*)p.a + (size_t)row * p.k + 8 * g;
     }
+    // w in fragment order: unit uu's fragment j is 512 values at ((bx U + uu) 4 + j) 512, and
+    // lane l's 8 of them at l * 8 (W rows bx 64 + 16 j + l % 16, K 32 uu + 8 (l / 16) + e).
 #pragma unroll
-    for (int j = 0; j < 4; j++) wp[j] = (const f16*)p.w + (size_t)(bx * 64 + 16 * j + r16) * p.k + 8 * g;
+    for (int j = 0; j < 4; j++) wp[j] = (const f16*)p.w + ((size_t)bx * U * 4 + j) * 512 + l * 8;
+
+    // The epilogue's other inputs, in flight with the first operand loads.
+    const int c0 = (tid & 7) * 4;
+    EpiCol ec;
+    EpiRow er[NPASS];
+    epi_load_col<EPI>(p, bx, c0, ec);
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ps++) epi_load_row<EPI, XG>(p, by * BM + ps * 32 + (tid >> 3), bx, c0, er[ps]);
 
     floatx4 acc[MI][4];
 #pragma unroll
@@ -123,7 +134,7 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
         for (int s = 0; s < UMAX; s++) {
             const int uu = min(u + s, u1 - 1);
 #pragma unroll
-            for (int j = 0; j < 4; j++) fw[s][j] = *(const half8*)(wp[j] + uu * 32);
+            for (int j = 0; j < 4; j++) fw[s][j] = *(const half8*)(wp[j] + (size_t)uu * 2048);
 #pragma unroll
             for (int i = 0; i < MI; i++) fa[s][i] = load16h<XG>(ap[i] + uu * 32);
         }
@@ -152,7 +163,6 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     __syncthreads();
 
     float v[NPASS][8];
-    const int c0 = (tid & 7) * 4;
 #pragma unroll
     for (int ps = 0; ps < NPASS; ps++) {
         const int r = ps * 32 + (tid >> 3);
@@ -169,7 +179,7 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
         }
     }
     __syncthreads();  // red is free again
-    finish<NPASS, EPI, XG>(p, v, bx * p.tiles_m + by, z, by * BM, bx, BM, s_last);
+    finish<NPASS, EPI, XG>(p, v, bx * p.tiles_m + by, z, by * BM, bx, BM, s_last, ec, er);
 }
 
 }  // namespace jh

@@ -54,6 +54,7 @@ struct GemmParams {
     int m, n, k;
     float eps;
     int rope_cols;          // RoPE applies to columns below this (2 d for qkv)
+    int rope_rows;          // positions in the RoPE table (positions are clamped to it)
     int splits;
     int tiles_n, tiles_m;
 };

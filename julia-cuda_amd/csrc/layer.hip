@@ -222,6 +222,7 @@ static void fill(GemmParams& p, const Gemm& g, GemmConfig c, const Scratch& s) {
     p.ws = s.ws, p.counters = s.counters;
     p.m = g.m, p.n = g.n, p.k = g.k, p.eps = g.eps;
     p.rope_cols = (g.epi & EPI_ROPE) ? 2 * (g.n / 3) : 0;
+    p.rope_rows = g.rope_rows;
     p.splits = c.splits, p.tiles_n = g.n / 64, p.tiles_m = (g.m + c.bm - 1) / c.bm;
 }
 
@@ -299,7 +300,8 @@ bool LayerKernel::barrier_timed_out() {
     if (!bar_) return false;
     uint32_t flag = 0;
     if (hipMemcpy(&flag, bar_ + BAR_TIMEOUT, 4, hipMemcpyDeviceToHost) != hipSuccess) return true;
-    if (flag) hipMemset(bar_, 0, BAR_WORDS * 4);  // a barrier gave up: its counts are stale
+    if (flag && hipMemset(bar_, 0, BAR_WORDS * 4) != hipSuccess)  // its counts are stale
+        return true;
     return flag != 0;
 }
 

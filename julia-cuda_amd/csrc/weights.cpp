@@ -117,6 +117,28 @@ void geglu_rows(int inter, int32_t* src) {
     }
 }
 
+// Each wave load of a GEMM tile's weights then reads 1 KB contiguous (16 rows x 64 bytes of the
+// row-major matrix otherwise, which costs the CU's memory pipeline about twice as long).
+void pack_frag(const uint16_t* w, int n, int k, uint16_t* out) {
+    const int U = k / 32;
+    size_t o = 0;
+    for (int G = 0; G < n / 64; G++)
+        for (int u = 0; u < U; u++)
+            for (int j = 0; j < 4; j++)
+                for (int l = 0; l < 64; l++, o += 8)
+                    memcpy(out + o, w + (size_t)(64 * G + 16 * j + l % 16) * k + 32 * u + 8 * (l / 16), 16);
+}
+
+void unpack_frag(const uint16_t* packed, int n, int k, uint16_t* w) {
+    const int U = k / 32;
+    size_t o = 0;
+    for (int G = 0; G < n / 64; G++)
+        for (int u = 0; u < U; u++)
+            for (int j = 0; j < 4; j++)
+                for (int l = 0; l < 64; l++, o += 8)
+                    memcpy(w + (size_t)(64 * G + 16 * j + l % 16) * k + 32 * u + 8 * (l / 16), packed + o, 16);
+}
+
 // src/prep.rs:103-118: cos and sin of p . theta^(-2j/64) for pairs j < 32, in f32.
 void rope_table(float theta, int npos, float* table) {
     float inv[32];
@@ -347,6 +369,28 @@ HostWeights prepare_synthetic(const ModelConfig& c) {
         });
         conv16(s.lin2, T_SCORER + 4);
     }
+    run_parallel(tasks);
+    // The GEMM matrices into fragment order, in place.
+    tasks.clear();
+    auto pack = [&](Span s, int n, int k) {
+        tasks.push_back([=] {
+            const std::vector<uint16_t> w(H + s.start, H + s.start + s.len);
+            pack_frag(w.data(), n, k, H + s.start);
+        });
+    };
+    for (const EncoderLayer& e : L.layers) {
+        pack(e.wqkv, (int)(3 * d), (int)d);
+        pack(e.wo, (int)d, (int)d);
+        pack(e.wi, (int)(2 * I), (int)d);
+        pack(e.wo_mlp, (int)d, (int)I);
+    }
+    for (const HeadLayer& h : L.head) {
+        pack(h.in_proj, (int)(3 * d), (int)d);
+        pack(h.out_proj, (int)d, (int)d);
+        pack(h.linear1, (int)F, (int)d);
+        pack(h.linear2, (int)d, (int)F);
+    }
+    pack(L.scorer.lin1, (int)d, (int)d);
     run_parallel(tasks);
     L.scorer.lin2_b = gen(seed, T_SCORER + 5, 1)[0];
     return hw;

@@ -1,5 +1,6 @@
 // The model's weights as the kernels read them (the reference's src/weights.rs): every matrix
-// (and the embedding table) f16 in one arena, every vector (LayerNorm weights, biases, column
+// (and the embedding table) f16 in one arena, the GEMM matrices in MFMA fragment order
+// (pack_frag), every vector (LayerNorm weights, biases, column
 // sums, type embeddings, RoPE tables) f32 in another; each tensor is a Span into one of the two,
 // 256-byte aligned. Prepared on the host once (`prepare`), uploaded with two copies.
 #pragma once
@@ -78,6 +79,11 @@ void fold_layernorm(const float* w, const float* gamma, int out, int k, uint16_t
 void fold_layernorm_bias(const float* w, const float* gamma, const float* beta, const float* b,
                          int out, int k, uint16_t* w16, float* colsum, float* bias);
 void geglu_rows(int inter, int32_t* src);
+// W [n][k] (n % 64 == 0, k % 32 == 0) <-> the GEMM kernels' MFMA fragment order: for 64-row
+// group G, 32-column unit u, 16-row fragment j and lane l < 64, the 8 values
+// W[64 G + 16 j + l % 16][32 u + 8 (l / 16) + e], e < 8, contiguous, in that nesting.
+void pack_frag(const uint16_t* w, int n, int k, uint16_t* out);
+void unpack_frag(const uint16_t* packed, int n, int k, uint16_t* w);
 void rope_table(float theta, int npos, float* table);
 
 // Tensor ids of the synthetic model (the generator's streams).

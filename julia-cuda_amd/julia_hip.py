@@ -80,7 +80,8 @@ EXPORTS = [
     "julia_hip_embed", "julia_hip_norm_add", "julia_hip_score", "julia_hip_time_gemm",
     "julia_hip_time_attention", "julia_hip_time_copy", "julia_hip_copy", "julia_hip_device_count",
     "julia_hip_prep_fold_layernorm", "julia_hip_prep_fold_layernorm_bias",
-    "julia_hip_prep_geglu_rows", "julia_hip_prep_rope_table", "julia_hip_synth",
+    "julia_hip_prep_geglu_rows", "julia_hip_prep_pack_frag", "julia_hip_prep_unpack_frag",
+    "julia_hip_prep_rope_table", "julia_hip_synth",
     "julia_hip_round_f16", "julia_hip_gemm_choose", "julia_hip_gemm_plan_2080ti",
     "julia_hip_gemm_choose_2080ti", "julia_hip_engine_info_get", "julia_hip_engine_tensor",
     "julia_hip_time_encoder_step", "julia_hip_profile_layer", "julia_hip_run_trace",
@@ -124,6 +125,8 @@ def lib():
         "julia_hip_prep_fold_layernorm_bias": (None, [_F32P, _F32P, _F32P, _F32P, _I, _I, _U16P,
                                                       _F32P, _F32P]),
         "julia_hip_prep_geglu_rows": (None, [_I, _I32P]),
+        "julia_hip_prep_pack_frag": (None, [_U16P, _I, _I, _U16P]),
+        "julia_hip_prep_unpack_frag": (None, [_U16P, _I, _I, _U16P]),
         "julia_hip_prep_rope_table": (None, [_F, _I, _F32P]),
         "julia_hip_synth": (None, [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint64,
                                    ctypes.c_uint64, ctypes.c_double, ctypes.c_double, _F32P]),
@@ -376,6 +379,25 @@ def geglu_rows(inter):
     src = np.empty(2 * inter, np.int32)
     lib().julia_hip_prep_geglu_rows(inter, src)
     return src
+
+
+def pack_frag(w16):
+    """w16 [n][k] f16 bits -> the GEMM kernels' MFMA fragment order (a flat array)."""
+    w16 = np.ascontiguousarray(w16, np.uint16)
+    n, k = w16.shape
+    if n % 64 or k % 32:
+        raise JuliaHipError(f"pack_frag: {n} x {k} is not a multiple of 64 x 32")
+    out = np.empty(n * k, np.uint16)
+    lib().julia_hip_prep_pack_frag(w16, n, k, out)
+    return out
+
+
+def unpack_frag(packed, n, k):
+    if n % 64 or k % 32 or packed.size != n * k:
+        raise JuliaHipError(f"unpack_frag: {packed.size} values for {n} x {k}")
+    w = np.empty((n, k), np.uint16)
+    lib().julia_hip_prep_unpack_frag(np.ascontiguousarray(packed, np.uint16).ravel(), n, k, w)
+    return w
 
 
 def rope_table(theta, npos):

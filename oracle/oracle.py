@@ -167,6 +167,17 @@ def geglu_rows(inter):
     return src
 
 
+def pack_frag(w16):
+    """The GEMM kernels' weight order (a layout of this library's, no counterpart in the
+    reference): w [n][k] as [n/64 groups][k/32 units][4 fragments][64 lanes][8], lane l holding
+    row 64 G + 16 j + l % 16, columns 32 u + 8 (l / 16) + e. Restated with numpy axes, not
+    by the library's loops."""
+    w16 = np.asarray(w16)
+    n, k = w16.shape
+    return np.ascontiguousarray(
+        w16.reshape(n // 64, 4, 16, k // 32, 4, 8).transpose(0, 3, 1, 4, 2, 5)).ravel()
+
+
 def rope_table(theta, npos):
     t = np.empty((npos, 32, 2), np.float32)
     lib().oracle_rope_table(theta, npos, t)

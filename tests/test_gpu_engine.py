@@ -55,18 +55,18 @@ def test_weights_match_the_oracle_preparation(small):
     seed = c["seed"]
     # layer 0: converted only; layer 1: folded; wi interleaved for GeGLU
     w0 = O.synth(seed, O.LAYER_BASE + O.L_WQKV, 3 * d * d).reshape(3 * d, d)
-    assert np.array_equal(e.tensor_host("wqkv", 0), O.to_f16_bits(w0).ravel())
+    assert np.array_equal(e.tensor_host("wqkv", 0), O.pack_frag(O.to_f16_bits(w0)))
     b = O.LAYER_BASE + 16
     w1 = O.synth(seed, b + O.L_WQKV, 3 * d * d).reshape(3 * d, d)
     g1 = O.synth(seed, b + O.L_ATTN_NORM, d)
     w16, cs = O.fold_layernorm(w1, g1)
-    assert np.array_equal(e.tensor_host("wqkv", 1), w16.ravel())
+    assert np.array_equal(e.tensor_host("wqkv", 1), O.pack_frag(w16))
     assert np.array_equal(e.tensor_host("qkv_colsum", 1, np.float32), cs)
     wi = O.synth(seed, b + O.L_WI, 2 * I * d).reshape(2 * I, d)
     gi = O.synth(seed, b + O.L_MLP_NORM, d)
     wi16, wcs = O.fold_layernorm(wi, gi)
     rows = O.geglu_rows(I)
-    assert np.array_equal(e.tensor_host("wi", 1), wi16[rows].ravel())
+    assert np.array_equal(e.tensor_host("wi", 1), O.pack_frag(wi16[rows]))
     assert np.array_equal(e.tensor_host("wi_colsum", 1, np.float32), wcs[rows])
     # the head's bias fold and the embedding table
     hb = O.HEAD_BASE + 32

@@ -99,8 +99,9 @@ def gemm_problem(kind, m, n, k, seed=1, theta=160000.0):
 
 def run_gemm(torch, P, bm, splits, scratch):
     m, n, k = P["m"], P["n"], P["k"]
-    dev = {key: to_dev(torch, P[key]) for key in ("a", "w", "stats_in", "colsum", "bias", "rope")
+    dev = {key: to_dev(torch, P[key]) for key in ("a", "stats_in", "colsum", "bias", "rope")
            if key in P}
+    dev["w"] = to_dev(torch, O.pack_frag(P["w"]))  # the kernels take w in fragment order
     ncols = n // 2 if P["kind"] == "lngeglu" else n
     c = to_dev(torch, P["res"]) if "res" in P else torch.zeros((m, ncols), dtype=torch.float16,
                                                                device="cuda")

@@ -148,6 +148,25 @@ def test_geglu_interleave_matches_the_epilogue():
     assert sorted(rows) == list(range(2 * inter))
 
 
+def test_fragment_order_packing():
+    """The GEMM weight layout: the library's packing equals the oracle's numpy restatement,
+    unpacking inverts it, and sampled elements sit where the MFMA lane map puts them (lane l of
+    16 x 16 x 32 fragment j holds row 16 j + l % 16, K values 8 (l / 16) .. + 7 of its unit)."""
+    rng = np.random.default_rng(7)
+    n, k = 192, 96
+    w = rng.integers(0, 1 << 16, (n, k), dtype=np.uint16)
+    p = jh.pack_frag(w)
+    assert np.array_equal(p, O.pack_frag(w))
+    assert np.array_equal(jh.unpack_frag(p, n, k), w)
+    U = k // 32
+    for _ in range(500):
+        G, u, j, l, e = (int(rng.integers(0, x)) for x in (n // 64, U, 4, 64, 8))
+        assert p[(((G * U + u) * 4 + j) * 64 + l) * 8 + e] == w[64 * G + 16 * j + l % 16,
+                                                                  32 * u + 8 * (l // 16) + e]
+    with pytest.raises(jh.JuliaHipError):
+        jh.pack_frag(w[:100])
+
+
 def test_rope_table_matches_the_oracle_and_closed_form():
     a = jh.rope_table(160000.0, 300)
     assert np.array_equal(a, O.rope_table(160000.0, 300))
