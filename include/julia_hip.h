@@ -210,12 +210,15 @@ int julia_hip_time_encoder_step(const Engine *e, int step, int m, int bm, int sp
                                 int batches, int per_batch, float *min_us, float *median_us,
                                 char *err, size_t err_len);
 /* src/profile.rs:84-241 with kernels/src/prof.rs's stamps: runs the encoder up to `layer` on n
- * tokens (per-step), then that layer with the persistent layer kernel recording, per block, the
- * 100 MHz clock at each phase's start and end (16 u64 per block: phase p at 2p, 2p + 1; the CU
- * at 10). plan: NULL for the default, else 10 ints (bm[4], splits[4], kv[2]); plan_out (nullable)
- * receives the plan used, grid the block count. */
+ * tokens (per-step), then that layer with the persistent encoder kernel recording, per block,
+ * the 100 MHz clock at each phase's start and end (32 u64 per block: phase p at 2p, 2p + 1; the
+ * CU at 10; the stages of the block's first task of GEMM g at 16 + 4 g .. + 3: inputs in place,
+ * MFMAs done, partials reduced, epilogue done). layer -1: the whole encoder as the forward pass
+ * runs it, one launch, stamps [block][layer][32]. plan: NULL for the default, else 10 ints
+ * (bm[4], splits[4], kv[2]); plan_out (nullable) receives the plan used, grid the block count;
+ * stamps holds max_rows rows of 32. */
 int julia_hip_profile_layer(const Engine *e, int n, int layer, const int *plan, uint64_t *stamps,
-                            int max_blocks, int *grid, int *plan_out, char *err, size_t err_len);
+                            int max_rows, int *grid, int *plan_out, char *err, size_t err_len);
 /* One request with the residual stream copied out after every encoder layer (x_trace, f16 bits
  * [layers][n][d], nullable) and the head's stream after its last layer (head_x, [n][d],
  * nullable): for step-by-step parity checks. */

@@ -13,6 +13,9 @@
 // With `chunks` > 1 the key blocks of each (query block, head) tile are split into ranges, one
 // block each; every range writes its unnormalised output, max and sum to the scratch and the
 // last one of the tile to arrive merges them in range order (kernels/src/attn.rs:92-204).
+// With one range the LDS-resident tile runs (attn_tile.h: the key range staged at once, V^T
+// fragments from the transposing LDS read).
+#include <algorithm>
 #include <stdexcept>
 #include <string>
 
@@ -26,6 +29,28 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
     attention_tile(p, blockIdx.x, blockIdx.y, blockIdx.z, lds, &s_last);
 }
 
+// One block per (query block, head), the key range staged in LDS (dynamic, att_lds_bytes(gmax)).
+__global__ __launch_bounds__(256) void attention_lds_kernel(AttnParams p, int gmax) {
+    extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
+    attention_lds_tile(p, blockIdx.x, blockIdx.y, lds_dyn, gmax);
+}
+
+// Lets the LDS-resident kernel have its dynamic LDS (once per process; the engine calls it at
+// load, before any graph capture).
+bool attention_prepare() {
+    static const bool ok =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(attention_lds_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, att_lds_bytes(8)) == hipSuccess;
+    return ok;
+}
+
+// Key blocks the LDS holds at once for an attention over n rows: all a tile reaches, up to 8.
+int attention_gmax(int n, int window) {
+    const int blocks = (n + 63) / 64;
+    const int reach = window > 0 ? 2 * ((window + 63) / 64) + 1 : blocks;
+    return std::max(1, std::min({8, blocks, reach}));
+}
+
 size_t attention_ws_floats(int n, int d, int chunks) {
     if (chunks <= 1) return 0;
     return (size_t)((n + 63) / 64) * (d / 64) * chunks * ATT_PART * 256;
@@ -33,14 +58,13 @@ size_t attention_ws_floats(int n, int d, int chunks) {
 
 size_t attention_counters(int n, int d) { return (size_t)((n + 63) / 64) * (d / 64); }
 
-// Key ranges per tile: split while the tiles don't fill the GPU, at least two key blocks a range
-// (the reference's default_plan rule, src/forward.rs:186-187, refit for a 256-CU GPU).
+// Key ranges per tile (the reference's default_plan splits global attention, src/forward.rs:
+// 186-187). With the key range staged in LDS in one round trip, a tile's key loop is short and
+// a split's merge (two more round trips through memory) costs more than it saves up to the
+// longest requests: one range. Longer ranges go through LDS in groups of 8 key blocks.
 int attention_chunks(int n, int d, int window, int cus) {
-    if (window > 0) return 1;  // a window tile reaches 3 key blocks: splitting doesn't pay
-    const int blocks = (n + 63) / 64, tiles = blocks * (d / 64);
-    int c = (cus > 0 ? cus : 256) / (tiles > 0 ? tiles : 1);
-    c = std::min(c, (blocks + 1) / 2);
-    return std::max(1, std::min(c, 8));
+    (void)n, (void)d, (void)window, (void)cus;
+    return 1;
 }
 
 void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, int chunks,
@@ -55,7 +79,14 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
                        attention_counters(n, d) > s.n_counters || !s.ws || !s.counters))
         fail("the key-range scratch is too small for " + std::to_string(n) + " tokens");
     AttnParams p{qkv, o, n, d, window, chunks, s.ws, s.counters};
-    hipLaunchKernelGGL(attention_kernel, dim3((n + 63) / 64, d / 64, chunks), dim3(256), 0, st, p);
+    if (chunks == 1) {
+        if (!attention_prepare()) fail("the LDS-resident kernel cannot have its LDS");
+        const int gmax = attention_gmax(n, window);
+        hipLaunchKernelGGL(attention_lds_kernel, dim3((n + 63) / 64, d / 64), dim3(256),
+                           att_lds_bytes(gmax), st, p, gmax);
+    } else {
+        hipLaunchKernelGGL(attention_kernel, dim3((n + 63) / 64, d / 64, chunks), dim3(256), 0, st, p);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) throw std::runtime_error(std::string("attention: ") + hipGetErrorString(e));
 }

@@ -207,4 +207,149 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
     __syncthreads();  // the tiles are free again
 }
 
+// ---- the LDS-resident tile ----------------------------------------------------------------
+// The same arithmetic as attention_tile with the tile's whole key range staged at once: Q (64
+// queries) and K and V of up to `gmax` key blocks go into LDS with direct global -> LDS loads in
+// one round trip, so the key loop never waits for memory (ranges longer than gmax blocks go in
+// groups). K and V stay row-major ([key][d], 128-byte rows, the 16-byte chunks of row r stored at
+// chunk ^ (r % 8) so a fragment's 16 rows spread over the banks); V^T fragments come from the
+// transposing LDS read. No key ranges: one block per (query block, head).
+
+// LDS bytes of attention_lds_tile with gmax key blocks per group.
+__host__ __device__ constexpr int att_lds_bytes(int gmax) { return 8192 * (1 + 2 * gmax); }
+
+// Byte offset of 16-byte chunk `ch` of row `r` in a swizzled [rows][64 f16] LDS tile.
+__device__ __forceinline__ int att_swz(int r, int ch) { return (r * 8 + (ch ^ (r & 7))) * 16; }
+
+template <bool XG = false>
+__device__ __forceinline__ void attention_lds_tile(const AttnParams& p, int qb, int h, char* lds,
+                                                   int gmax) {
+    const int n = p.n, d = p.d, ld = 3 * d;
+    const int q0 = qb * 64;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g = l >> 4;
+    char* qs = lds;
+    char* ks = lds + 8192;
+    char* vs = ks + gmax * 8192;
+
+    const int nb = (n + 63) >> 6;
+    int kb0 = 0, kb1 = nb;
+    if (p.window > 0) {
+        kb0 = max(q0 - p.window, 0) >> 6;
+        kb1 = (min(q0 + 63 + p.window, n - 1) >> 6) + 1;
+    }
+
+    // rows [r0, r0 + rows) of qkv's columns col.. col + 63 (clamped to row n - 1) into `dst`:
+    // wave load I of the copy fills LDS chunks 64 I .. 64 I + 63, lane l chunk 64 I + l, which
+    // is row c / 8, logical chunk (c % 8) ^ (row % 8).
+    auto stage = [&](char* dst, int r0, int rows, int col) {
+        for (int I = w; I * 64 < rows * 8; I += 4) {
+            const int c = I * 64 + l, row = c >> 3, ch = (c & 7) ^ (row & 7);
+            const f16* src = (const f16*)p.qkv + (size_t)min(r0 + row, n - 1) * ld + col + ch * 8;
+            lds_dma16<XG>(src, dst + I * 1024);
+        }
+    };
+
+    const int qi = q0 + 16 * w + r16;  // this lane's query
+    const float scale = 1.4426950408889634f / 8.0f;  // log2(e) / sqrt(64)
+    float mx = -INFINITY, lsum = 0.0f;
+    floatx4 oacc[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) oacc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    half8 qf[2];
+
+    for (int gb = kb0; gb < kb1; gb += gmax) {
+        const int nbk = min(gmax, kb1 - gb);
+        if (gb == kb0) stage(qs, q0, 64, h * 64);
+        stage(ks, gb * 64, nbk * 64, d + h * 64);
+        stage(vs, gb * 64, nbk * 64, 2 * d + h * 64);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // the group is in LDS
+        if (gb == kb0) {
+            const int qr = 16 * w + r16;
+#pragma unroll
+            for (int k2 = 0; k2 < 2; k2++) qf[k2] = *(const half8*)(qs + att_swz(qr, 4 * k2 + g));
+        }
+        for (int b = 0; b < nbk; b++) {
+            const int kbase = (gb + b) * 64;
+            // S^T for keys 16 t + 4 g + e of this block, query qi.
+            floatx4 sc[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                sc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+                const int kr = b * 64 + 16 * t + r16;
+#pragma unroll
+                for (int k2 = 0; k2 < 2; k2++)
+                    sc[t] = mfma16(*(const half8*)(ks + att_swz(kr, 4 * k2 + g)), qf[k2], sc[t]);
+            }
+            float bm = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int key = kbase + 16 * t + 4 * g + e;
+                    const int dist = qi > key ? qi - key : key - qi;
+                    const bool ok = key < n && (p.window == 0 || dist <= p.window);
+                    sc[t][e] = ok ? sc[t][e] * scale : -INFINITY;
+                    bm = fmaxf(bm, sc[t][e]);
+                }
+            bm = fmaxf(bm, __shfl_xor(bm, 16));
+            bm = fmaxf(bm, __shfl_xor(bm, 32));
+            const float mnew = fmaxf(mx, bm);
+            const float base = mnew == -INFINITY ? 0.0f : mnew;  // no valid key yet: exp2(-inf) = 0
+            const float alpha = exp2f(mx - base);
+            mx = mnew;
+            float rs = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    sc[t][e] = exp2f(sc[t][e] - base);
+                    rs += sc[t][e];
+                }
+            lsum = lsum * alpha + rs;
+#pragma unroll
+            for (int t = 0; t < 4; t++) oacc[t] *= alpha;
+
+            // O^T += V^T . P^T over K steps k2 of 32 keys: lane group g holds (as its P^T values)
+            // keys 32 k2 + 4 g + (0..3) and 32 k2 + 16 + 4 g + (0..3). Its V^T fragment for d rows
+            // 16 dt + r16 comes from two transposing reads: lane (g, 4 j + q) addresses key
+            // 32 k2 + 4 g + j (+ 16), d 16 dt + 4 q .. + 3.
+            const int j = r16 >> 2, q = r16 & 3;
+#pragma unroll
+            for (int k2 = 0; k2 < 2; k2++) {
+                half8 pf;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    pf[e] = (f16)sc[2 * k2][e];
+                    pf[4 + e] = (f16)sc[2 * k2 + 1][e];
+                }
+                const int vr = b * 64 + 32 * k2 + 4 * g + j;
+#pragma unroll
+                for (int dt = 0; dt < 4; dt++) {
+                    const int ch = 2 * dt + (q >> 1), off = (q & 1) * 8;
+                    const half4 lo = lds_read_tr16(vs + att_swz(vr, ch) + off);
+                    const half4 hi = lds_read_tr16(vs + att_swz(vr + 16, ch) + off);
+                    const half8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    oacc[dt] = mfma16(vf, pf, oacc[dt]);
+                }
+            }
+        }
+        __syncthreads();  // the group's tiles are no longer read
+    }
+
+    float tot = lsum + __shfl_xor(lsum, 16);
+    tot += __shfl_xor(tot, 32);
+    const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+    if (qi < n) {
+        f16* op = (f16*)p.o + (size_t)qi * d + h * 64 + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            half4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = (f16)(oacc[dt][e] * inv);
+            store8<XG>(op + 16 * dt, o);
+        }
+    }
+}
+
 }  // namespace jh

@@ -161,6 +161,38 @@ __device__ __forceinline__ void xstore16(void* p, float4 v) {
     xstore64((char*)p + 8, u[1]);
 }
 
+// Raw buffer access (gfx9 buffer descriptor: base, byte size, no stride): reads past `bytes`
+// return zeros. With XG the 16-byte load is device-coherent (sc1), like xload64 but in one
+// instruction.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+template <bool XG>
+__device__ __forceinline__ half8 bload16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, XG ? 16 : 0));
+}
+
+// gfx950's direct global -> LDS load: each lane's 16 bytes at `src` land at LDS `base` + 16 lane
+// (base is wave-uniform). Counted like any vector load: s_waitcnt vmcnt covers it. XG: the read
+// is device-coherent (sc1), for data another block wrote in this kernel.
+template <bool XG = false>
+__device__ __forceinline__ void lds_dma16(const void* src, void* base) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)base, 16, 0,
+                                     XG ? 16 : 0);
+}
+
+// gfx950's transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group, lane i receives
+// element i % 4 of the 8 bytes lanes 4 j + i / 4 address, as its element j (j < 4). Loading a
+// row-major [key][d] tile this way hands a lane 4 consecutive keys of one d column.
+__device__ __forceinline__ half4 lds_read_tr16(const void* p) {
+    typedef short short4_t __attribute__((ext_vector_type(4)));
+    const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) short4_t*)p);
+    return __builtin_bit_cast(half4, v);
+}
+
 __device__ __forceinline__ uint32_t atomic_add_agent(uint32_t* p, uint32_t v) {
     return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

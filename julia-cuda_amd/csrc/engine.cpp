@@ -60,6 +60,9 @@ struct Engine {
     hipEvent_t ev_start[QUEUE] = {}, ev_end[QUEUE] = {};
     Scratch scratch{};
     LayerKernel layer_kernel;
+    // Every layer's weights for the persistent encoder kernel, on the device and the host.
+    LayerDesc* layers_d = nullptr;
+    std::vector<LayerDesc> layers_h;
     // The per-step forward pass as HIP graphs, one per (tokens, markers, question type): 124
     // launches submitted as one. They read the request from fixed buffers (gin: ids, then
     // markers at max_length) and write glogits; stream order keeps queued requests apart.
@@ -84,7 +87,7 @@ struct Engine {
         for (void* p : {(void*)w16, (void*)w32, (void*)x, (void*)qkv, (void*)o, (void*)mid,
                         (void*)hx, (void*)stats_a, (void*)stats_b, (void*)ids_d,
                         (void*)markers_d, (void*)logits_d, (void*)scratch.ws,
-                        (void*)scratch.counters})
+                        (void*)scratch.counters, (void*)layers_d})
             if (p) hipFree(p);
         if (ids_h) hipHostFree(ids_h);
         if (markers_h) hipHostFree(markers_h);
@@ -126,19 +129,19 @@ struct Engine {
              stats_b);
     }
 
-    // The persistent layer kernel: one cooperative launch per layer.
-    void launch_layer_fused(int l, int n) {
-        const EncoderLayer& L = layout.layers[l];
+    // The persistent encoder kernel: layers [first, first + count) as one cooperative launch.
+    LayerArgs layer_args(int first, int count, int n) const {
         LayerArgs a{};
         a.x = x, a.qkv = qkv, a.o = o, a.mid = mid, a.stats_attn = stats_a, a.stats_mlp = stats_b;
-        a.wqkv = h(L.wqkv), a.qkv_colsum = f(L.qkv_colsum);
-        a.rope = f(L.global ? layout.rope_global : layout.rope_local);
-        a.wo = h(L.wo), a.wi = h(L.wi), a.wi_colsum = f(L.wi_colsum), a.wo_mlp = h(L.wo_mlp);
+        a.layers = layers_d, a.host_layers = layers_h.data(), a.first = first, a.count = count;
         a.m = n, a.d = cfg.d, a.inter = cfg.inter, a.eps = cfg.norm_eps;
-        a.window = L.global ? 0 : cfg.window;
         a.rope_rows = cfg.max_positions;
-        layer_kernel.launch(a, layer_kernel.default_plan(n, cfg.d, cfg.inter, a.window), scratch,
-                            stream);
+        return a;
+    }
+
+    void launch_encoder_fused(int first, int count, int n) {
+        layer_kernel.launch(layer_args(first, count, n), layer_kernel.default_plan(n, cfg.d, cfg.inter),
+                            scratch, stream);
     }
 
     // ---- the head (src/forward.rs GpuHead) -------------------------------------------------
@@ -201,12 +204,10 @@ struct Engine {
                 float* logits, bool fused) {
         embed_launch(ids, n, h(layout.tok_embeddings), cfg.vocab, cfg.d, f(layout.emb_norm),
                      cfg.norm_eps, x, stream);
-        for (int l = 0; l < cfg.layers; l++) {
-            if (fused)
-                launch_layer_fused(l, n);
-            else
-                launch_layer(l, n);
-        }
+        if (fused)
+            launch_encoder_fused(0, cfg.layers, n);
+        else
+            for (int l = 0; l < cfg.layers; l++) launch_layer(l, n);
         launch_head(n, qtype, markers, nm, logits);
     }
 };
@@ -282,7 +283,20 @@ Engine* load_engine(const char* dir, size_t max_length) {
         ws = std::max(ws, attention_ws_floats(m, (int)d, ch));
         counters = std::max(counters, attention_counters(m, (int)d));
     }
-    e->layer_kernel.init(e->cus);
+    // The per-layer weight table of the persistent kernel.
+    for (const EncoderLayer& L : e->layout.layers) {
+        LayerDesc ld{};
+        ld.wqkv = e->h(L.wqkv), ld.wo = e->h(L.wo), ld.wi = e->h(L.wi), ld.wo_mlp = e->h(L.wo_mlp);
+        ld.qkv_colsum = e->f(L.qkv_colsum), ld.wi_colsum = e->f(L.wi_colsum);
+        ld.rope = e->f(L.global ? e->layout.rope_global : e->layout.rope_local);
+        ld.window = L.global ? 0 : c.window;
+        e->layers_h.push_back(ld);
+    }
+    e->layers_d = dalloc<LayerDesc>(e->layers_h.size(), "layer table");
+    hip_check(hipMemcpy(e->layers_d, e->layers_h.data(), e->layers_h.size() * sizeof(LayerDesc),
+                        hipMemcpyHostToDevice), "layer table");
+    e->layer_kernel.init(e->cus, (int)prop.sharedMemPerBlock);
+    if (!attention_prepare()) throw std::runtime_error("attention: cannot set the kernel's LDS size");
     ws = std::max(ws, e->layer_kernel.ws_floats((int)ml, (int)d, c.inter));
     counters = std::max(counters, e->layer_kernel.counters((int)ml, (int)d, c.inter));
     e->scratch.ws = dalloc<float>(ws, "scratch");
@@ -841,28 +855,23 @@ int julia_hip_time_encoder_step(const Engine* ce, int step, int m, int bm, int s
 }
 
 int julia_hip_profile_layer(const Engine* ce, int n, int layer, const int* plan, uint64_t* stamps,
-                            int max_blocks, int* grid, int* plan_out, char* err, size_t err_len) {
+                            int max_rows, int* grid, int* plan_out, char* err, size_t err_len) {
     return guarded(err, err_len, [&] {
         if (!ce) throw std::runtime_error("no engine");
         Engine& e = *const_cast<Engine*>(ce);
         hip_check(hipSetDevice(e.device), "hipSetDevice");
         if (n <= 0 || n > e.max_length) throw std::runtime_error("profile: n out of range");
-        if (layer < 0 || layer >= e.cfg.layers) throw std::runtime_error("profile: no such layer");
+        if (layer < -1 || layer >= e.cfg.layers) throw std::runtime_error("profile: no such layer");
         std::vector<uint32_t> ids(n);
         for (int i = 0; i < n; i++) ids[i] = (uint32_t)(i * 7919 % e.cfg.vocab);
         hip_check(hipMemcpy(e.ids_d, ids.data(), n * 4, hipMemcpyHostToDevice), "ids");
         embed_launch(e.ids_d, n, e.h(e.layout.tok_embeddings), e.cfg.vocab, e.cfg.d,
                      e.f(e.layout.emb_norm), e.cfg.norm_eps, e.x, e.stream);
-        for (int l = 0; l < layer; l++) e.launch_layer(l, n);
-        const EncoderLayer& L = e.layout.layers[layer];
-        LayerArgs a{};
-        a.x = e.x, a.qkv = e.qkv, a.o = e.o, a.mid = e.mid, a.stats_attn = e.stats_a;
-        a.stats_mlp = e.stats_b, a.wqkv = e.h(L.wqkv), a.qkv_colsum = e.f(L.qkv_colsum);
-        a.rope = e.f(L.global ? e.layout.rope_global : e.layout.rope_local);
-        a.wo = e.h(L.wo), a.wi = e.h(L.wi), a.wi_colsum = e.f(L.wi_colsum), a.wo_mlp = e.h(L.wo_mlp);
-        a.m = n, a.d = e.cfg.d, a.inter = e.cfg.inter, a.eps = e.cfg.norm_eps;
-        a.window = L.global ? 0 : e.cfg.window, a.rope_rows = e.cfg.max_positions;
-        LayerPlan p = e.layer_kernel.default_plan(n, e.cfg.d, e.cfg.inter, a.window);
+        // One layer (after the ones before it, per step) or, with layer -1, the whole encoder.
+        const int first = layer < 0 ? 0 : layer, count = layer < 0 ? e.cfg.layers : 1;
+        for (int l = 0; l < first; l++) e.launch_layer(l, n);
+        const LayerArgs a = e.layer_args(first, count, n);
+        LayerPlan p = e.layer_kernel.default_plan(n, e.cfg.d, e.cfg.inter);
         if (plan) {
             for (int g = 0; g < 4; g++) p.bm[g] = plan[g], p.splits[g] = plan[4 + g];
             p.kv[0] = plan[8], p.kv[1] = plan[9];
@@ -873,15 +882,17 @@ int julia_hip_profile_layer(const Engine* ce, int n, int layer, const int* plan,
             for (int g = 0; g < 4; g++) plan_out[g] = p.bm[g], plan_out[4 + g] = p.splits[g];
             plan_out[8] = p.kv[0], plan_out[9] = p.kv[1];
         }
-        if (gb > max_blocks) throw std::runtime_error("profile: the stamps buffer is too small");
-        uint64_t* prof = dalloc<uint64_t>((size_t)gb * PROF_WORDS, "profile");
+        const size_t rows = (size_t)gb * count;
+        if (rows > (size_t)std::max(max_rows, 0))
+            throw std::runtime_error("profile: the stamps buffer is too small");
+        uint64_t* prof = dalloc<uint64_t>(rows * PROF_WORDS, "profile");
         try {
-            hip_check(hipMemset(prof, 0, (size_t)gb * PROF_WORDS * 8), "hipMemset");
+            hip_check(hipMemset(prof, 0, rows * PROF_WORDS * 8), "hipMemset");
             e.layer_kernel.launch(a, p, e.scratch, e.stream, 0x1f, prof);
             hip_check(hipStreamSynchronize(e.stream), "profile");
             if (e.layer_kernel.barrier_timed_out())
                 throw std::runtime_error("layer: a grid barrier timed out");
-            hip_check(hipMemcpy(stamps, prof, (size_t)gb * PROF_WORDS * 8, hipMemcpyDeviceToHost),
+            hip_check(hipMemcpy(stamps, prof, rows * PROF_WORDS * 8, hipMemcpyDeviceToHost),
                       "profile");
         } catch (...) {
             hipFree(prof);
@@ -907,7 +918,7 @@ int julia_hip_run_trace(const Engine* ce, const uint32_t* ids, size_t n, const u
                      e.f(e.layout.emb_norm), e.cfg.norm_eps, e.x, e.stream);
         for (int l = 0; l < e.cfg.layers; l++) {
             if (layer_fused)
-                e.launch_layer_fused(l, (int)n);
+                e.launch_encoder_fused(l, 1, (int)n);
             else
                 e.launch_layer(l, (int)n);
             if (x_trace) {

@@ -182,4 +182,158 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     finish<NPASS, EPI, XG>(p, v, bx * p.tiles_m + by, z, by * BM, bx, BM, s_last, ec, er);
 }
 
+// ---- the persistent kernel's tile: weights staged in LDS --------------------------------------
+// The weight tile of a task (64 columns x one split's K units, fragment order) is one contiguous
+// run of the packed matrix, nu * 4 KB. The persistent kernel copies it into LDS with direct
+// global -> LDS loads, if it can before the barrier that precedes the task's phase (the weights
+// do not depend on the previous phase), so that after the barrier only the activation loads
+// stand between the block and its MFMAs.
+
+struct WTile {
+    int bx, ub, nu;  // 64-column group, first K unit, units
+};
+
+__device__ __forceinline__ WTile w_tile_of(const GemmParams& p, int task) {
+    const int T = p.tiles_n * p.tiles_m * p.splits;
+    const int L = xcd_task(task, T);
+    const int z = L % p.splits, bx = (L / p.splits) / p.tiles_m;
+    const int U = p.k >> 5;
+    const int ub = z * U / p.splits;
+    return WTile{bx, ub, (z + 1) * U / p.splits - ub};
+}
+
+// LDS bytes of the weight tile for splits of a k-wide GEMM (the largest split).
+__host__ __device__ constexpr int w_tile_bytes(int k, int splits) {
+    return ((k / 32 + splits - 1) / splits) * 4096;
+}
+
+// Waves [w_first, 4) copy task's weight tile to `lds` (1 KB per wave load).
+__device__ __forceinline__ void w_tile_fetch(const GemmParams& p, WTile t, f16* lds, int w_first) {
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    if (w < w_first) return;
+    const f16* src = (const f16*)p.w + (size_t)(t.bx * (p.k >> 5) + t.ub) * 2048 + l * 8;
+    for (int c = w - w_first; c < 4 * t.nu; c += 4 - w_first) lds_dma16(src + (size_t)c * 512, lds + c * 512);
+}
+
+// LDS floats the cross-wave reduction of a BM-row tile needs (aliases the weight tile).
+template <int BM>
+constexpr int w_red_floats() { return 4 * BM * 68; }
+
+// Task `task` of c = epilogue(a . w^T) in the persistent kernel. The weight tile is in `lds`
+// already (w_ready: its loads were issued earlier by this block, maybe still in flight) or is
+// fetched here. a is read device-coherent (another block wrote it in this kernel) with 16-byte
+// buffer loads, rows past m reading zeros. The four waves split the tile's K units; their partial
+// tiles are summed through LDS, in the weight tile's space. Every thread calls this; it ends
+// with a block barrier after the last LDS access.
+template <int BM, int EPI>
+__device__ __forceinline__ void gemm_w_tile(const GemmParams& p, int task, char* lds, bool w_ready,
+                                            uint32_t* s_last, uint64_t* sub = nullptr) {
+    auto mark = [&](int i) {  // profiling: thread 0's view of the task's stages
+        if (sub && threadIdx.x == 0) sub[i] = wall_clock64();
+    };
+    constexpr int MI = BM / 16;
+    constexpr int NPASS = (BM + 31) / 32;
+    constexpr int UMAX = MI == 4 ? 6 : 9;  // a fragments one wave holds: 96 or 36-72 VGPRs
+    const int T = p.tiles_n * p.tiles_m * p.splits;
+    const int L = xcd_task(task, T);
+    const int z = L % p.splits, t2 = L / p.splits;
+    const int by = t2 % p.tiles_m, bx = t2 / p.tiles_m;
+    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g = l >> 4;
+    const int U = p.k >> 5;
+    const int ub = z * U / p.splits, nu = (z + 1) * U / p.splits - ub;
+    const int u0 = w * nu / 4, u1 = (w + 1) * nu / 4;  // this wave's units, relative to ub
+    f16* wl = (f16*)lds;
+    if (!w_ready) w_tile_fetch(p, WTile{bx, ub, nu}, wl, 0);
+
+    const int c0 = (tid & 7) * 4;
+    EpiCol ec;
+    EpiRow er[NPASS];
+    epi_load_col<EPI>(p, bx, c0, ec);
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ps++) epi_load_row<EPI, true>(p, by * BM + ps * 32 + (tid >> 3), bx, c0, er[ps]);
+
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(p.a, (uint32_t)p.m * (uint32_t)p.k * 2u);
+    uint32_t aoff[MI];
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+        aoff[i] = ((uint32_t)(by * BM + 16 * i + r16) * (uint32_t)p.k + (uint32_t)(ub + u0) * 32u + 8u * g) * 2u;
+
+    floatx4 acc[MI][4];
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    half8 fa[UMAX][MI];
+    auto load_a = [&](int u) {
+#pragma unroll
+        for (int s = 0; s < UMAX; s++) {
+            const uint32_t du = (uint32_t)(min(u + s, u1 - 1) - u0) * 64u;
+#pragma unroll
+            for (int i = 0; i < MI; i++) fa[s][i] = bload16<true>(ra, aoff[i] + du);
+        }
+    };
+    // The weight fragments of unit s + 1 are read from LDS while unit s's MFMAs run (the reads
+    // are unconditional, clamped to the wave's last unit; only the MFMAs are skipped).
+    auto mma = [&](int u) {
+        half8 fw[2][4];
+        auto rd = [&](half8 (&f)[4], int uu) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) f[j] = *(const half8*)(wl + (uu * 4 + j) * 512 + l * 8);
+        };
+        rd(fw[0], u);
+#pragma unroll
+        for (int s = 0; s < UMAX; s++) {
+            if (s + 1 < UMAX) rd(fw[(s + 1) & 1], min(u + s + 1, u1 - 1));
+            if (u + s < u1) {  // wave-uniform
+#pragma unroll
+                for (int i = 0; i < MI; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) acc[i][j] = mfma16(fw[s & 1][j], fa[s][i], acc[i][j]);
+            }
+        }
+    };
+    if (u0 < u1) load_a(u0);
+    __builtin_amdgcn_s_waitcnt(0);  // the weight tile's loads (and the first a chunk) are done
+    __syncthreads();                // ... for every wave: the whole tile is in LDS
+    mark(0);
+    for (int u = u0; u < u1; u += UMAX) {
+        if (u != u0) load_a(u);
+        mma(u);
+    }
+    __syncthreads();  // every wave is done with the weight tile: the reduction reuses its space
+    mark(1);
+
+    float* red = (float*)lds;
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            *(floatx4*)&red[(w * BM + 16 * i + r16) * 68 + 16 * j + 4 * g] = acc[i][j];
+    __syncthreads();
+    float v[NPASS][8];
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ps++) {
+        const int r = ps * 32 + (tid >> 3);
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[ps][e] = 0.0f;
+        if (r < BM) {
+#pragma unroll
+            for (int ww = 0; ww < 4; ww++) {
+                const float4 lo = *(const float4*)&red[(ww * BM + r) * 68 + c0];
+                const float4 hi = *(const float4*)&red[(ww * BM + r) * 68 + 32 + c0];
+                v[ps][0] += lo.x, v[ps][1] += lo.y, v[ps][2] += lo.z, v[ps][3] += lo.w;
+                v[ps][4] += hi.x, v[ps][5] += hi.y, v[ps][6] += hi.z, v[ps][7] += hi.w;
+            }
+        }
+    }
+    __syncthreads();  // LDS is free again
+    mark(2);
+    finish<NPASS, EPI, true>(p, v, bx * p.tiles_m + by, z, by * BM, bx, BM, s_last, ec, er);
+    if (sub) {
+        release_wait();
+        mark(3);
+    }
+}
+
 }  // namespace jh

@@ -115,6 +115,8 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
 size_t attention_ws_floats(int n, int d, int chunks);
 size_t attention_counters(int n, int d);
 int attention_chunks(int n, int d, int window, int cus);
+int attention_gmax(int n, int window);
+bool attention_prepare();
 
 void embed_launch(const uint32_t* ids, int n, const jh_half* table, int vocab, int d,
                   const float* gamma, float eps, jh_half* x, hipStream_t stream);

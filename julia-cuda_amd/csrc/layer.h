@@ -1,7 +1,8 @@
-// The persistent layer kernel's host side (the reference's `layer` launch, src/forward.rs:
-// 167-359, and `LayerPlan`, :737-757): one encoder layer as one cooperative launch, its five
-// steps as phases separated by grid barriers, each phase a list of tasks the resident blocks
-// stride over.
+// The persistent encoder kernel's host side (the reference's `layer` launch, src/forward.rs:
+// 167-359, and `LayerPlan`, :737-757). The reference launches one cooperative kernel per layer;
+// here one cooperative launch runs a range of layers (the whole encoder in the forward pass),
+// each layer's five steps as phases separated by grid barriers, each phase a list of tasks the
+// resident blocks stride over.
 #pragma once
 
 #include <stdint.h>
@@ -12,21 +13,32 @@
 
 namespace jh {
 
-// u32 words of device memory the grid barrier needs (zeroed once; every barrier leaves them zero).
+// u32 words of device memory the grid barrier needs (zero between launches; a launch leaves
+// them zero, and the host clears them after a barrier time-out).
 constexpr int BAR_WORDS = 11 * 32;
-// u64 words per block of the layer kernel's timestamps: (start, end) of phase p at 2p, 2p + 1
-// (100 MHz clock), the block's CU id at 10.
-constexpr int PROF_WORDS = 16;
+// u64 words per block and layer of the kernel's timestamps: (start, end) of phase p at 2p,
+// 2p + 1 (100 MHz clock), the block's CU id at 10, and for the block's first task of GEMM g
+// (qkv, wo, wi, wo_mlp) at 16 + 4 g + i: its inputs in place (weights in LDS, activations in
+// registers), its MFMAs done, its partial tiles reduced, its epilogue done.
+constexpr int PROF_WORDS = 32;
+
+// One layer's weights, as the kernel reads them (an array of these lives in device memory).
+struct LayerDesc {
+    const jh_half *wqkv, *wo, *wi, *wo_mlp;  // fragment order
+    const float *qkv_colsum;                 // null in layer 0: no LayerNorm before qkv
+    const float *wi_colsum, *rope;
+    int window;                              // 0: global attention
+    int pad_;
+};
 
 struct LayerArgs {
     jh_half *x, *qkv, *o, *mid;
     float *stats_attn, *stats_mlp;  // wo writes stats_attn (wi reads it), wo_mlp stats_mlp
-    const jh_half *wqkv, *wo, *wi, *wo_mlp;
-    const float *qkv_colsum;  // null in layer 0: no LayerNorm before qkv
-    const float *rope, *wi_colsum;
+    const LayerDesc* layers;        // device array, indexed by layer
+    const LayerDesc* host_layers;   // the same on the host (for the plan and the checks)
+    int first, count;               // the layers this launch runs
     int m, d, inter;
     float eps;
-    int window;
     int rope_rows;
 };
 
@@ -36,29 +48,31 @@ struct LayerPlan {
     int bm[4];
     int splits[4];
     int kv[2];
-    std::string str() const;  // "qkv 32/1 wo 16/2 wi 32/1 wo_mlp 16/2 kv 3/1"
+    std::string str() const;  // "qkv 64/1 wo 16/1 wi 64/1 wo_mlp 16/1 kv 4/1"
 };
 
 class LayerKernel {
 public:
-    void init(int cus);
+    void init(int cus, int lds_bytes);
     void bind(uint32_t* barrier) { bar_ = barrier; }
-    LayerPlan default_plan(int m, int d, int inter, int window) const;
+    LayerPlan default_plan(int m, int d, int inter) const;
     size_t ws_floats(int max_m, int d, int inter) const;
     size_t counters(int max_m, int d, int inter) const;
-    // Phases: bits 0-4 select qkv, attention, wo, wi, wo_mlp (0x1f: the whole layer).
-    // prof: null, or PROF_WORDS u64 per block of the grid (grid()).
+    // Phases: bits 0-4 select qkv, attention, wo, wi, wo_mlp (0x1f: whole layers; a subset only
+    // with one layer). prof: null, or PROF_WORDS u64 per block of the grid and layer run.
     void launch(const LayerArgs& a, const LayerPlan& plan, const Scratch& s, hipStream_t stream,
                 unsigned phases = 0x1f, uint64_t* prof = nullptr);
     int grid(const LayerArgs& a, const LayerPlan& plan) const;
-    // Whether a grid barrier gave up waiting since the last call (then clears the flag).
+    // LDS bytes a plan needs on m rows (weight tile, reduction and attention share it).
+    static int lds_bytes(const LayerPlan& plan, int d, int inter, int m, int window);
+    // Whether a grid barrier gave up waiting since the last call (then clears the words).
     // Synchronizes with the device.
     bool barrier_timed_out();
     int per_cu() const { return per_cu_; }
     bool available() const { return per_cu_ > 0; }
 
 private:
-    int cus_ = 0, per_cu_ = 0;
+    int cus_ = 0, per_cu_ = 0, lds_max_ = 0;
     uint32_t* bar_ = nullptr;  // BAR_WORDS words
 };
 

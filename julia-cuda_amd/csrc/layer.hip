@@ -1,12 +1,16 @@
-// The persistent layer kernel (the reference's `layer`, kernels/src/main.rs:578-842): one
-// encoder layer as one cooperative launch. Its five steps are phases (qkv, attention, wo, wi,
-// wo_mlp); every block strides over a phase's tasks (the per-step kernels' own tile functions,
-// so the arithmetic is theirs), with a grid barrier between two selected phases. The grid is at
-// most the number of blocks resident at once (the cooperative launch checks it), a multiple of
-// 8 so that task t runs on XCD t % 8 as in the per-step kernels.
+// The persistent encoder kernel (the reference's `layer`, kernels/src/main.rs:578-842, which runs
+// one layer per cooperative launch): here one cooperative launch runs a range of layers, the
+// whole encoder in the forward pass. Each layer's five steps are phases (qkv, attention, wo, wi,
+// wo_mlp) with a grid barrier between two phases; every block strides over a phase's tasks. The
+// grid is at most the number of blocks resident at once (the cooperative launch checks it).
 //
-// The row statistics need no clearing phase here: the resstats epilogue writes (not adds) one
-// partial per row and 64-column group.
+// A GEMM task stages its weight tile in LDS (gemm_w_tile). The weights do not depend on the
+// previous phase, so a block copies the weight tile of its first task in the next GEMM phase
+// while it waits at the barrier (waves 1-3 issue the copy after the block has arrived, wave 0
+// waits), and after the barrier only the activation loads stand before its MFMAs.
+//
+// The row statistics need no clearing phase: the resstats epilogue writes (not adds) one partial
+// per row and 64-column group.
 #include <algorithm>
 #include <stdexcept>
 #include <string>
@@ -17,14 +21,22 @@
 
 namespace jh {
 
-struct LayerParams {
-    GemmParams g[4];  // qkv, wo, wi, wo_mlp
-    AttnParams at;
-    int bm[4];
-    int epi0;         // EPI_K_ROPE (layer 0) or EPI_K_LNROPE
+struct EncParams {
+    const LayerDesc* layers;
+    int first, count;
+    jh_half *x, *qkv, *o, *mid;
+    float *stats_attn, *stats_mlp;
+    int m, d, inter, rope_rows;
+    float eps;
+    int bm[4], splits[4], kv[2];
+    float* ws;
+    uint32_t* counters;
     unsigned phases;  // bits 0-4
+    int barriers;     // grid barriers in this launch
+    int lds_main;     // dynamic LDS bytes before the block's split-K flag
+    int att_gmax[2];  // key blocks the attention tile stages at once: global, window layers
     uint32_t* bar;    // the barrier's words (BAR_WORDS, zero between launches)
-    uint64_t* prof;   // null, or PROF_WORDS per block: see stamp()
+    uint64_t* prof;   // null, or PROF_WORDS per block and layer: see stamp()
 };
 
 // Per-phase timestamps (the reference's kernels/src/prof.rs): thread 0 of each block writes the
@@ -32,7 +44,7 @@ struct LayerParams {
 // into word 2p and at its end (after the block's last task, before the barrier after it) into
 // word 2p + 1, and its CU id into word 10.
 __device__ __forceinline__ void stamp(uint64_t* prof, int slot) {
-    if (prof && threadIdx.x == 0) prof[(size_t)blockIdx.x * PROF_WORDS + slot] = wall_clock64();
+    if (prof && threadIdx.x == 0) prof[slot] = wall_clock64();
 }
 
 __device__ __forceinline__ void stamp_end(uint64_t* prof, int phase) {
@@ -47,105 +59,183 @@ __device__ __forceinline__ void stamp_end(uint64_t* prof, int phase) {
 constexpr int BAR_LINE = 32;
 constexpr int BAR_GROUPS = 8 * BAR_LINE, BAR_GEN = 9 * BAR_LINE, BAR_TIMEOUT = 10 * BAR_LINE;
 
-// A barrier across the grid (the reference's is kernels/src/gemm.rs:435-489): blocks arrive in
-// eight groups (block b in group b % 8, which is the XCD it is dispatched to), so no counter sees
-// more than an eighth of the arrivals; the last arrival of a group counts the group, the last
-// group advances the generation that every block waits on, and each counter is reset by its
-// last arrival, so the words are zero again at the end of every barrier.
+// Barrier nb (1, 2, ... within the launch) across the grid (the reference's is
+// kernels/src/gemm.rs:435-489). Blocks arrive in eight groups (block b in group b % 8, the XCD
+// it is dispatched to), so no counter sees more than an eighth of the arrivals; the arrival that
+// completes group x's count for barrier nb counts the group, the one that completes the groups'
+// count advances the generation. The counters only grow within a launch (targets nb * size),
+// so an arrival is two dependent atomics at most and nobody resets anything on the way; block 0
+// zeroes the counters after the launch's last barrier, when no arrival is left. The generation
+// keeps growing across launches: each block reads it once at its start (before it arrives
+// anywhere, so before any barrier of this launch can complete) and waits for g0 + nb.
 //
-// The phase outputs are stored device-coherent and read back through the coherent path (XG), so
-// the release is only each wave waiting for its stores to complete, and no cache needs
-// invalidating after the barrier (the weights other blocks share through L2 stay cached). The
-// wait is bounded: past ~0.2 s (far beyond any real barrier) it gives up and raises the time-out
-// flag, which the host turns into an error, so a broken launch cannot hang the GPU.
-__device__ __forceinline__ void grid_sync(uint32_t* bar) {
+// The phase outputs are stored device-coherent and read back through the coherent path, so the
+// release is only each wave waiting for its stores to complete, and no cache needs invalidating
+// after the barrier. `during` runs on waves 1-3 after the block has arrived (wave 0 waits): work
+// that does not depend on the other blocks, the next phase's weight copy. The wait is bounded:
+// past ~0.2 s (far beyond any real barrier) it gives up and raises the time-out flag, which the
+// host turns into an error, so a broken launch cannot hang the GPU.
+template <class F>
+__device__ __forceinline__ void grid_sync(uint32_t* bar, uint32_t g0, uint32_t nb, bool last,
+                                          bool& timed_out, F&& during) {
     release_wait();
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t grid = gridDim.x, x = blockIdx.x & 7;
-        const uint32_t groups = grid < 8 ? grid : 8, in_group = (grid - x + 7) / 8;
-        uint32_t* gen = bar + BAR_GEN;
-        const uint32_t g0 = atomic_load_agent(gen);  // before arriving: it cannot move yet
-        release_wait();
-        if (atomic_add_agent(bar + x * BAR_LINE, 1u) == in_group - 1) {
-            atomic_store_agent(bar + x * BAR_LINE, 0u);
-            if (atomic_add_agent(bar + BAR_GROUPS, 1u) == groups - 1) {
-                atomic_store_agent(bar + BAR_GROUPS, 0u);
-                release_wait();  // the resets land before anyone can pass
-                atomic_add_agent(gen, 1u);
+    if (threadIdx.x < 64) {
+        if (threadIdx.x == 0) {
+            const uint32_t grid = gridDim.x, x = blockIdx.x & 7;
+            const uint32_t groups = grid < 8 ? grid : 8, in_group = (grid - x + 7) / 8;
+            if (atomic_add_agent(bar + x * BAR_LINE, 1u) == nb * in_group - 1)
+                if (atomic_add_agent(bar + BAR_GROUPS, 1u) == nb * groups - 1)
+                    atomic_add_agent(bar + BAR_GEN, 1u);
+            const uint32_t target = g0 + nb;
+            const uint64_t t0 = wall_clock64();
+            while (!timed_out && (int)(atomic_load_agent(bar + BAR_GEN) - target) < 0) {
+                __builtin_amdgcn_s_sleep(1);
+                if (wall_clock64() - t0 > 20000000ull) {
+                    atomic_store_agent(bar + BAR_TIMEOUT, 1u);
+                    timed_out = true;  // the launch is lost: the remaining barriers do not wait
+                }
+            }
+            if (last && blockIdx.x == 0) {
+                for (int i = 0; i < 9; i++) atomic_store_agent(bar + i * BAR_LINE, 0u);
             }
         }
-        const uint64_t t0 = wall_clock64();
-        while (atomic_load_agent(gen) == g0) {
-            __builtin_amdgcn_s_sleep(1);
-            if (wall_clock64() - t0 > 20000000ull) {
-                atomic_store_agent(bar + BAR_TIMEOUT, 1u);
-                break;
-            }
-        }
+    } else {
+        during();
     }
     __syncthreads();
 }
 
-constexpr int LAYER_LDS_FLOATS = lat_lds_floats<32>();
-static_assert(ATT_LDS_F16 / 2 <= LAYER_LDS_FLOATS, "attention tiles fit the GEMM's LDS");
+__device__ __forceinline__ GemmParams make_gemm(const EncParams& P, int g, const LayerDesc& L) {
+    GemmParams p{};
+    p.m = P.m, p.eps = P.eps, p.ws = P.ws, p.counters = P.counters;
+    p.splits = P.splits[g];
+    if (g == 0) {
+        p.a = P.x, p.w = L.wqkv, p.c = P.qkv, p.n = 3 * P.d, p.k = P.d;
+        p.rope = L.rope, p.rope_cols = 2 * P.d, p.rope_rows = P.rope_rows;
+        if (L.qkv_colsum) p.stats_in = P.stats_mlp, p.colsum = L.qkv_colsum;
+    } else if (g == 1) {
+        p.a = P.o, p.w = L.wo, p.c = P.x, p.n = P.d, p.k = P.d, p.stats_out = P.stats_attn;
+    } else if (g == 2) {
+        p.a = P.x, p.w = L.wi, p.c = P.mid, p.n = 2 * P.inter, p.k = P.d;
+        p.stats_in = P.stats_attn, p.colsum = L.wi_colsum;
+    } else {
+        p.a = P.mid, p.w = L.wo_mlp, p.c = P.x, p.n = P.d, p.k = P.inter, p.stats_out = P.stats_mlp;
+    }
+    p.tiles_n = p.n >> 6;
+    p.tiles_m = (P.m + P.bm[g] - 1) / P.bm[g];
+    return p;
+}
+
+__device__ __forceinline__ int gemm_tasks(const GemmParams& g) {
+    return g.tiles_n * g.tiles_m * g.splits;
+}
 
 template <int EPI>
-__device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, float* lds,
-                                           uint32_t* s_last) {
-    const int T = g.tiles_n * g.tiles_m * g.splits;
+__device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* lds, bool pre,
+                                           uint32_t* s_last, uint64_t* sub) {
+    const int T = gemm_tasks(g);
     for (int t = blockIdx.x; t < T; t += gridDim.x) {
+        const bool first = t == (int)blockIdx.x;
+        const bool ready = pre && first;
+        uint64_t* su = first ? sub : nullptr;
         if (bm == 16)
-            gemm_lat_tile<16, EPI, true>(g, t, lds, s_last);
+            gemm_w_tile<16, EPI>(g, t, lds, ready, s_last, su);
+        else if (bm == 32)
+            gemm_w_tile<32, EPI>(g, t, lds, ready, s_last, su);
         else
-            gemm_lat_tile<32, EPI, true>(g, t, lds, s_last);
+            gemm_w_tile<64, EPI>(g, t, lds, ready, s_last, su);
     }
 }
 
-__global__ __launch_bounds__(256) void layer_kernel(LayerParams P) {
-    __shared__ __attribute__((aligned(16))) float lds[LAYER_LDS_FLOATS];
-    __shared__ uint32_t s_last;
-    auto on = [&](int ph) { return (P.phases >> ph) & 1u; };
-    auto sync_if = [&](int next) {
-        if (on(next)) grid_sync(P.bar);
+__global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    uint32_t* s_last = (uint32_t*)(lds + P.lds_main);
+    uint32_t g0 = 0, nb = 0;
+    bool timed_out = false;
+    if (threadIdx.x == 0) g0 = atomic_load_agent(P.bar + BAR_GEN);
+    auto on = [&](int ph) { return ((P.phases >> ph) & 1u) != 0; };
+    auto sync = [&](auto&& during) {
+        nb++;
+        grid_sync(P.bar, g0, nb, (int)nb == P.barriers, timed_out, during);
     };
-    if (P.prof && threadIdx.x == 0) P.prof[(size_t)blockIdx.x * PROF_WORDS + 10] = __smid();
-    if (on(0)) {
-        stamp(P.prof, 0);
-        if (P.epi0 == EPI_K_LNROPE)
-            gemm_phase<EPI_K_LNROPE>(P.g[0], P.bm[0], lds, &s_last);
-        else
-            gemm_phase<EPI_K_ROPE>(P.g[0], P.bm[0], lds, &s_last);
-        stamp_end(P.prof, 0);
-        sync_if(1);
-    }
-    if (on(1)) {
-        stamp(P.prof, 2);
-        const AttnParams& a = P.at;
-        const int heads = a.d >> 6, T = ((a.n + 63) >> 6) * heads * a.chunks;
-        for (int t = blockIdx.x; t < T; t += gridDim.x) {
-            const int tile = t / a.chunks;
-            attention_tile<true>(a, tile / heads, tile % heads, t % a.chunks, (f16*)lds, &s_last);
+    auto nothing = [] {};
+    // The next GEMM phase's weight copy for this block's first task in it (if it has one): the
+    // barrier's `during`, issued by waves 1-3.
+    f16* const wl = (f16*)lds;
+    auto fetch_first = [wl](const GemmParams& g) {
+        return [&g, wl] { w_tile_fetch(g, w_tile_of(g, blockIdx.x), wl, 1); };
+    };
+
+    LayerDesc L = P.layers[P.first];
+    GemmParams gq = make_gemm(P, 0, L);
+    bool pre = false;  // the weight tile of this block's first task in the coming phase is fetched
+    for (int li = 0; li < P.count; li++) {
+        uint64_t* prof = P.prof ? P.prof + ((size_t)blockIdx.x * P.count + li) * PROF_WORDS : nullptr;
+        if (prof && threadIdx.x == 0) prof[10] = __smid();
+        auto sub = [prof](int g) { return prof ? prof + 16 + 4 * g : nullptr; };
+        const GemmParams go = make_gemm(P, 1, L), gi = make_gemm(P, 2, L), gm = make_gemm(P, 3, L);
+        if (on(0)) {
+            stamp(prof, 0);
+            if (gq.colsum)
+                gemm_phase<EPI_K_LNROPE>(gq, P.bm[0], lds, pre, s_last, sub(0));
+            else
+                gemm_phase<EPI_K_ROPE>(gq, P.bm[0], lds, pre, s_last, sub(0));
+            pre = false;
+            stamp_end(prof, 0);
+            if (on(1)) sync(nothing);
         }
-        stamp_end(P.prof, 1);
-        sync_if(2);
-    }
-    if (on(2)) {
-        stamp(P.prof, 4);
-        gemm_phase<EPI_K_RESSTATS>(P.g[1], P.bm[1], lds, &s_last);
-        stamp_end(P.prof, 2);
-        sync_if(3);
-    }
-    if (on(3)) {
-        stamp(P.prof, 6);
-        gemm_phase<EPI_K_LNGEGLU>(P.g[2], P.bm[2], lds, &s_last);
-        stamp_end(P.prof, 3);
-        sync_if(4);
-    }
-    if (on(4)) {
-        stamp(P.prof, 8);
-        gemm_phase<EPI_K_RESSTATS>(P.g[3], P.bm[3], lds, &s_last);
-        stamp_end(P.prof, 4);
+        if (on(1)) {
+            stamp(prof, 2);
+            const int chunks = L.window > 0 ? P.kv[1] : P.kv[0];
+            const AttnParams at{P.qkv, P.o, P.m, P.d, L.window, chunks, P.ws, P.counters};
+            const int heads = P.d >> 6, T = ((P.m + 63) >> 6) * heads * chunks;
+            const int gmax = P.att_gmax[L.window > 0 ? 1 : 0];
+            for (int t = blockIdx.x; t < T; t += gridDim.x) {
+                const int tile = t / chunks;
+                if (chunks == 1)
+                    attention_lds_tile<true>(at, tile / heads, tile % heads, lds, gmax);
+                else
+                    attention_tile<true>(at, tile / heads, tile % heads, t % chunks, (f16*)lds, s_last);
+            }
+            stamp_end(prof, 1);
+            if (on(2)) {
+                pre = (int)blockIdx.x < gemm_tasks(go);
+                if (pre) sync(fetch_first(go)); else sync(nothing);
+            }
+        }
+        if (on(2)) {
+            stamp(prof, 4);
+            gemm_phase<EPI_K_RESSTATS>(go, P.bm[1], lds, pre, s_last, sub(1));
+            pre = false;
+            stamp_end(prof, 2);
+            if (on(3)) {
+                pre = (int)blockIdx.x < gemm_tasks(gi);
+                if (pre) sync(fetch_first(gi)); else sync(nothing);
+            }
+        }
+        if (on(3)) {
+            stamp(prof, 6);
+            gemm_phase<EPI_K_LNGEGLU>(gi, P.bm[2], lds, pre, s_last, sub(2));
+            pre = false;
+            stamp_end(prof, 3);
+            if (on(4)) {
+                pre = (int)blockIdx.x < gemm_tasks(gm);
+                if (pre) sync(fetch_first(gm)); else sync(nothing);
+            }
+        }
+        if (on(4)) {
+            stamp(prof, 8);
+            gemm_phase<EPI_K_RESSTATS>(gm, P.bm[3], lds, pre, s_last, sub(3));
+            pre = false;
+            stamp_end(prof, 4);
+        }
+        if (li + 1 < P.count) {  // whole layers only (the host checks)
+            L = P.layers[P.first + li + 1];
+            gq = make_gemm(P, 0, L);
+            pre = (int)blockIdx.x < gemm_tasks(gq);
+            if (pre) sync(fetch_first(gq)); else sync(nothing);
+        }
     }
 }
 
@@ -160,15 +250,6 @@ std::string LayerPlan::str() const {
     return s + "kv " + std::to_string(kv[0]) + "/" + std::to_string(kv[1]);
 }
 
-void LayerKernel::init(int cus) {
-    cus_ = cus > 0 ? cus : 256;
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(layer_kernel),
-                                                     256, 0) != hipSuccess)
-        n = 0;
-    per_cu_ = n;
-}
-
 static void shapes(int d, int inter, int cols[4], int ks[4]) {
     cols[0] = 3 * d, ks[0] = d;
     cols[1] = d, ks[1] = d;
@@ -176,21 +257,65 @@ static void shapes(int d, int inter, int cols[4], int ks[4]) {
     cols[3] = d, ks[3] = inter;
 }
 
-// Per GEMM the latency chooser's pick, limited to the layer kernel's tile heights (16 and 32
-// rows, which keep the kernel's LDS at 34.8 KB); key ranges for global attention as the
+static int red_bytes(int bm) { return 4 * bm * 68 * 4; }
+
+int LayerKernel::lds_bytes(const LayerPlan& plan, int d, int inter, int m, int window) {
+    int cols[4], ks[4];
+    shapes(d, inter, cols, ks);
+    int b = std::max({ATT_LDS_F16 * 2, att_lds_bytes(attention_gmax(m, 0)),
+                      att_lds_bytes(attention_gmax(m, window))});
+    for (int g = 0; g < 4; g++)
+        b = std::max({b, w_tile_bytes(ks[g], plan.splits[g]), red_bytes(plan.bm[g])});
+    return (b + 15) / 16 * 16;
+}
+
+void LayerKernel::init(int cus, int lds_max) {
+    cus_ = cus > 0 ? cus : 256;
+    lds_max_ = lds_max - 16;  // the split-K flag after the main area
+    per_cu_ = 0;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(encoder_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, lds_max) != hipSuccess) {
+        (void)hipGetLastError();
+        return;
+    }
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(encoder_kernel),
+                                                     256, lds_max) != hipSuccess)
+        n = 0;
+    per_cu_ = n;  // with the largest LDS a plan may use: one block per CU
+}
+
+// Per GEMM the tile height and split-K with the least modelled time on a grid of one block per
+// CU: a task waits for its activation tile (about 67 KB per us into one CU), its MFMAs, the
+// cross-wave reduction and the epilogue; tasks run in rounds over the grid; the first round's
+// weight tile is fetched during the barrier, later rounds fetch their own; a split costs a
+// partial exchange. The weight tile must fit the LDS. Key ranges for global attention as the
 // per-step attention's, none for sliding-window layers (src/forward.rs:173-189's rule).
-LayerPlan LayerKernel::default_plan(int m, int d, int inter, int window) const {
+LayerPlan LayerKernel::default_plan(int m, int d, int inter) const {
     LayerPlan p{};
     int cols[4], ks[4];
     shapes(d, inter, cols, ks);
+    const double bw = 67e3;  // bytes per us into one CU
     for (int g = 0; g < 4; g++) {
-        GemmConfig c = gemm_choose(std::min(m, 1024), cols[g], ks[g], cus_);
-        if (c.bm > 32) c = GemmConfig{32, c.bm >= 128 ? 1 : c.splits};
-        p.bm[g] = c.bm, p.splits[g] = c.splits;
+        double best = 1e30;
+        p.bm[g] = 16, p.splits[g] = ks[g] / 32 >= 8 ? 2 : 1;
+        for (int bm : {16, 32, 64}) {
+            for (int s = 1; s <= 4; s++) {
+                if (ks[g] / 32 < 4 * s) continue;  // every wave needs a K unit
+                if (w_tile_bytes(ks[g], s) > lds_max_) continue;
+                const long tasks = (long)(cols[g] / 64) * ((m + bm - 1) / bm) * s;
+                const long rounds = (tasks + cus_ - 1) / cus_;
+                const double a_us = (double)bm * (ks[g] / s) * 2 / bw;
+                const double w_us = (double)w_tile_bytes(ks[g], s) / bw;
+                const double mma_us = (bm / 16) * (ks[g] / s / 32 / 4.0) * 4 * 16 / 2400.0;
+                const double task = 1.2 + a_us + mma_us + 0.1 * (bm / 16) + 0.4;
+                const double cost = rounds * task + (rounds - 1) * w_us + (s > 1 ? 1.5 : 0.0);
+                if (cost < best - 1e-9) best = cost, p.bm[g] = bm, p.splits[g] = s;
+            }
+        }
     }
     p.kv[0] = attention_chunks(m, d, 0, cus_);
     p.kv[1] = 1;
-    (void)window;
     return p;
 }
 
@@ -199,7 +324,7 @@ size_t LayerKernel::ws_floats(int max_m, int d, int inter) const {
     int cols[4], ks[4];
     shapes(d, inter, cols, ks);
     for (int m = 1; m <= max_m; m++) {
-        const LayerPlan p = default_plan(m, d, inter, 0);
+        const LayerPlan p = default_plan(m, d, inter);
         for (int g = 0; g < 4; g++)
             ws = std::max(ws, gemm_ws_floats(m, cols[g], GemmConfig{p.bm[g], p.splits[g]}));
         ws = std::max(ws, attention_ws_floats(m, d, p.kv[0]));
@@ -215,83 +340,84 @@ size_t LayerKernel::counters(int max_m, int d, int inter) const {
     return c;
 }
 
-static void fill(GemmParams& p, const Gemm& g, GemmConfig c, const Scratch& s) {
-    p = GemmParams{};
-    p.a = g.a, p.w = g.w, p.c = g.c, p.stats_in = g.stats_in, p.colsum = g.colsum;
-    p.bias = g.bias, p.rope = g.rope, p.pos = g.pos, p.stats_out = g.stats_out;
-    p.ws = s.ws, p.counters = s.counters;
-    p.m = g.m, p.n = g.n, p.k = g.k, p.eps = g.eps;
-    p.rope_cols = (g.epi & EPI_ROPE) ? 2 * (g.n / 3) : 0;
-    p.rope_rows = g.rope_rows;
-    p.splits = c.splits, p.tiles_n = g.n / 64, p.tiles_m = (g.m + c.bm - 1) / c.bm;
-}
-
 int LayerKernel::grid(const LayerArgs& a, const LayerPlan& plan) const {
     int cols[4], ks[4];
     shapes(a.d, a.inter, cols, ks);
-    long most = (long)((a.m + 63) / 64) * (a.d / 64) * plan.kv[a.window > 0 ? 1 : 0];
+    long most = (long)((a.m + 63) / 64) * (a.d / 64) * std::max(plan.kv[0], plan.kv[1]);
     for (int g = 0; g < 4; g++)
         most = std::max(most, (long)(cols[g] / 64) * ((a.m + plan.bm[g] - 1) / plan.bm[g]) * plan.splits[g]);
-    long grid = std::min<long>((long)per_cu_ * cus_, most);
-    if (grid > 8) grid -= grid % 8;
+    // Enough blocks for the largest phase's tasks in one round if they fit (a multiple of 8, so
+    // that the task-to-XCD map is even), else every resident block.
+    const long grid = std::min<long>((long)per_cu_ * cus_, (most + 7) / 8 * 8);
     return (int)std::max<long>(grid, 1);
 }
 
 void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratch& s,
                          hipStream_t stream, unsigned phases, uint64_t* prof) {
     auto fail = [&](const std::string& m) { throw std::runtime_error("layer: " + m); };
-    if (per_cu_ <= 0) fail("the layer kernel does not fit on a CU");
+    if (per_cu_ <= 0) fail("the encoder kernel does not fit on a CU");
     if (!bar_) fail("no grid-barrier counter");
-    for (int g = 0; g < 4; g++)
-        if (!(plan.bm[g] == 16 || plan.bm[g] == 32) || plan.splits[g] < 1 || plan.splits[g] > 4)
-            fail("no such plan: " + plan.str());
-    const int kv = plan.kv[a.window > 0 ? 1 : 0];
-    if (kv < 1 || kv > 8) fail("no such plan: " + plan.str());
+    if (!a.layers || !a.host_layers || a.count < 1) fail("no layers");
     if (phases == 0 || phases > 0x1f) fail("no phases selected");
+    if (phases != 0x1f && a.count != 1) fail("a subset of the phases runs one layer only");
+    for (int g = 0; g < 4; g++)
+        if (!(plan.bm[g] == 16 || plan.bm[g] == 32 || plan.bm[g] == 64) || plan.splits[g] < 1 ||
+            plan.splits[g] > 4)
+            fail("no such plan: " + plan.str());
+    if (plan.kv[0] < 1 || plan.kv[0] > 8 || plan.kv[1] < 1 || plan.kv[1] > 8)
+        fail("no such plan: " + plan.str());
+    int window = 0;
+    for (int li = 0; li < a.count; li++) window = std::max(window, a.host_layers[a.first + li].window);
+    const int lds = lds_bytes(plan, a.d, a.inter, a.m, window);
+    if (lds > lds_max_) fail("the plan's weight tiles do not fit the LDS: " + plan.str());
 
-    const bool ln0 = a.qkv_colsum != nullptr;
-    Gemm g[4] = {};
-    g[0].epi = ln0 ? EPI_K_LNROPE : EPI_K_ROPE, g[0].a = a.x, g[0].w = a.wqkv, g[0].c = a.qkv;
-    g[0].m = a.m, g[0].n = 3 * a.d, g[0].k = a.d, g[0].eps = a.eps, g[0].rope = a.rope;
-    g[0].rope_rows = a.rope_rows;
-    if (ln0) g[0].stats_in = a.stats_mlp, g[0].colsum = a.qkv_colsum;
-    g[1].epi = EPI_K_RESSTATS, g[1].a = a.o, g[1].w = a.wo, g[1].c = a.x, g[1].m = a.m;
-    g[1].n = a.d, g[1].k = a.d, g[1].stats_out = a.stats_attn;
-    g[2].epi = EPI_K_LNGEGLU, g[2].a = a.x, g[2].w = a.wi, g[2].c = a.mid, g[2].m = a.m;
-    g[2].n = 2 * a.inter, g[2].k = a.d, g[2].stats_in = a.stats_attn, g[2].colsum = a.wi_colsum;
-    g[2].eps = a.eps;
-    g[3].epi = EPI_K_RESSTATS, g[3].a = a.mid, g[3].w = a.wo_mlp, g[3].c = a.x, g[3].m = a.m;
-    g[3].n = a.d, g[3].k = a.inter, g[3].stats_out = a.stats_mlp;
-
-    LayerParams P{};
-    for (int i = 0; i < 4; i++) {
-        const GemmConfig c{plan.bm[i], plan.splits[i]};
-        gemm_check(g[i], c, s);
-        fill(P.g[i], g[i], c, s);
-        P.bm[i] = plan.bm[i];
+    // Every layer's GEMMs pass the per-step launcher's checks (the kernel builds the same ones).
+    int cols[4], ks[4];
+    shapes(a.d, a.inter, cols, ks);
+    for (int li = 0; li < a.count; li++) {
+        const LayerDesc& L = a.host_layers[a.first + li];
+        Gemm g[4] = {};
+        const bool ln0 = L.qkv_colsum != nullptr;
+        g[0].epi = ln0 ? EPI_K_LNROPE : EPI_K_ROPE, g[0].a = a.x, g[0].w = L.wqkv, g[0].c = a.qkv;
+        g[0].rope = L.rope, g[0].rope_rows = a.rope_rows;
+        if (ln0) g[0].stats_in = a.stats_mlp, g[0].colsum = L.qkv_colsum;
+        g[1].epi = EPI_K_RESSTATS, g[1].a = a.o, g[1].w = L.wo, g[1].c = a.x, g[1].stats_out = a.stats_attn;
+        g[2].epi = EPI_K_LNGEGLU, g[2].a = a.x, g[2].w = L.wi, g[2].c = a.mid;
+        g[2].stats_in = a.stats_attn, g[2].colsum = L.wi_colsum;
+        g[3].epi = EPI_K_RESSTATS, g[3].a = a.mid, g[3].w = L.wo_mlp, g[3].c = a.x, g[3].stats_out = a.stats_mlp;
+        for (int i = 0; i < 4; i++) {
+            g[i].m = a.m, g[i].n = cols[i], g[i].k = ks[i], g[i].eps = a.eps;
+            gemm_check(g[i], GemmConfig{plan.bm[i], plan.splits[i]}, s);
+        }
+        const int kv = L.window > 0 ? plan.kv[1] : plan.kv[0];
+        if (kv > 1 && (attention_ws_floats(a.m, a.d, kv) > s.ws_floats ||
+                       attention_counters(a.m, a.d) > s.n_counters))
+            fail("the key-range scratch is too small for " + std::to_string(a.m) + " tokens");
     }
-    if (kv > 1 && (attention_ws_floats(a.m, a.d, kv) > s.ws_floats ||
-                   attention_counters(a.m, a.d) > s.n_counters))
-        fail("the key-range scratch is too small for " + std::to_string(a.m) + " tokens");
-    P.at = AttnParams{a.qkv, a.o, a.m, a.d, a.window, kv, s.ws, s.counters};
-    P.epi0 = g[0].epi;
+
+    EncParams P{};
+    P.layers = a.layers, P.first = a.first, P.count = a.count;
+    P.x = a.x, P.qkv = a.qkv, P.o = a.o, P.mid = a.mid;
+    P.stats_attn = a.stats_attn, P.stats_mlp = a.stats_mlp;
+    P.m = a.m, P.d = a.d, P.inter = a.inter, P.rope_rows = a.rope_rows, P.eps = a.eps;
+    for (int g = 0; g < 4; g++) P.bm[g] = plan.bm[g], P.splits[g] = plan.splits[g];
+    P.kv[0] = plan.kv[0], P.kv[1] = plan.kv[1];
+    P.ws = s.ws, P.counters = s.counters;
     P.phases = phases;
+    int barriers = 0;  // between two consecutive selected phases, and between layers
+    for (int ph = 1; ph < 5; ph++)
+        if (((phases >> ph) & 1) && ((phases >> (ph - 1)) & 1)) barriers++;
+    P.barriers = barriers * a.count + (a.count - 1);
+    P.lds_main = lds;
+    P.att_gmax[0] = attention_gmax(a.m, 0);
+    P.att_gmax[1] = attention_gmax(a.m, window);
     P.bar = bar_;
     P.prof = prof;
 
     const int grid_blocks = grid(a, plan);
-    // A barrier between two consecutive selected phases only (the kernel's sync_if).
-    unsigned barriers = 0;
-    for (int ph = 1; ph < 5; ph++)
-        if (((phases >> ph) & 1) && ((phases >> (ph - 1)) & 1)) barriers++;
     void* args[] = {&P};
-    hipError_t e;
-    if (barriers > 0)
-        e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(layer_kernel), dim3(grid_blocks),
-                                       dim3(256), args, 0, stream);
-    else
-        e = hipLaunchKernel(reinterpret_cast<const void*>(layer_kernel), dim3(grid_blocks),
-                            dim3(256), args, 0, stream);
+    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(encoder_kernel),
+                                                    dim3(grid_blocks), dim3(256), args, lds + 16, stream);
     if (e != hipSuccess) fail(std::string(hipGetErrorString(e)) + " (" + plan.str() + ", grid " +
                               std::to_string(grid_blocks) + ")");
 }

@@ -32,6 +32,7 @@ EPI = {
 }
 
 ERR_LEN = 1024
+PROF_WORDS = 32  # u64 stamps per block and layer of the persistent kernel's profile
 
 
 class JuliaHipError(RuntimeError):
@@ -251,15 +252,18 @@ class Engine:
         return mn.value, md.value
 
     def profile_layer(self, n, layer=1, plan=None):
-        """The layer kernel's per-block phase stamps (src/profile.rs): returns (plan, stamps
-        [grid][16] u64 of a 100 MHz clock)."""
-        stamps = np.zeros((4096, 16), np.uint64)
+        """The persistent encoder kernel's per-block phase stamps (src/profile.rs): returns (plan,
+        stamps [grid][layers][PROF_WORDS] u64 of a 100 MHz clock). layer -1: the whole encoder in one
+        launch, as the forward pass runs it; otherwise that one layer."""
+        layers = self.info().layers if layer < 0 else 1
+        rows = 1024 * layers
+        stamps = np.zeros((rows, PROF_WORDS), np.uint64)
         grid = ctypes.c_int()
         pin = None if plan is None else np.ascontiguousarray(plan, np.int32)
         pout = np.zeros(10, np.int32)
         _call(lib().julia_hip_profile_layer, self.ptr, n, layer, _np_ptr(pin), _np_ptr(stamps),
-              4096, ctypes.byref(grid), _np_ptr(pout))
-        return pout, stamps[: grid.value]
+              rows, ctypes.byref(grid), _np_ptr(pout))
+        return pout, stamps[: grid.value * layers].reshape(grid.value, layers, PROF_WORDS)
 
     def tensor(self, name, index=0):
         """(device address, bytes) of a prepared weight tensor."""
