@@ -173,18 +173,30 @@ def main():
     dom = max((k for k in STEP_SHAPES), key=lambda s: kern[s]["total_us"])
     dk = kern[dom]
     n, k, epi, _ = STEP_SHAPES[dom]
+    bm = dk["config"][0]
+    kname = f"gemm_{'lat' if bm < 128 else 'tput'}<{bm}, {jh.EPI[epi]}>"
+    # HBM bytes per dispatch from the committed rocprofv3 counter passes (FETCH_SIZE and
+    # WRITE_SIZE, scaled by the library's copy kernel: profiles/traffic_<step>_293.*), when they
+    # are of this kernel.
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"traffic_{dom}_293.json")
+    if os.path.exists(tfile):
+        with open(tfile) as fh:
+            t = json.load(fh)
+        if t.get("kernel") == kname:
+            traffic = t["traffic_bytes"]
     t_hbm, t_mfma = dk["bytes"] / PEAK_HBM, dk["flops"] / PEAK_F16
     if t_hbm >= t_mfma:
         ach = dk["bytes"] / (dk["us"] * 1e-6) / 1e9
-        out["roofline"] = {"kernel": f"{dom} gemm_{epi} M=293 N={n} K={k}", "bound": "hbm",
+        out["roofline"] = {"kernel": f"{kname}: {dom} gemm_{epi} M=293 N={n} K={k}", "bound": "hbm",
                            "achieved": round(ach, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                           "frac": round(ach / (PEAK_HBM / 1e9), 4), "traffic": None,
+                           "frac": round(ach / (PEAK_HBM / 1e9), 4), "traffic": traffic,
                            "algorithmic_bytes": dk["bytes"], "us": dk["us"]}
     else:
         ach = dk["flops"] / (dk["us"] * 1e-6) / 1e12
-        out["roofline"] = {"kernel": f"{dom} gemm_{epi} M=293 N={n} K={k}", "bound": "mfma",
+        out["roofline"] = {"kernel": f"{kname}: {dom} gemm_{epi} M=293 N={n} K={k}", "bound": "mfma",
                            "achieved": round(ach, 2), "peak": PEAK_F16 / 1e12, "unit": "TFLOP/s",
-                           "frac": round(ach / (PEAK_F16 / 1e12), 4), "traffic": None,
+                           "frac": round(ach / (PEAK_F16 / 1e12), 4), "traffic": traffic,
                            "algorithmic_flops": dk["flops"], "us": dk["us"]}
     log("kernels at 293 tokens:", json.dumps(kern))
 
