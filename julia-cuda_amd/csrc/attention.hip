@@ -13,8 +13,9 @@
 // With `chunks` > 1 the key blocks of each (query block, head) tile are split into ranges, one
 // block each; every range writes its unnormalised output, max and sum to the scratch and the
 // last one of the tile to arrive merges them in range order (kernels/src/attn.rs:92-204).
-// With one range the LDS-resident tile runs (attn_tile.h: the key range staged at once, V^T
-// fragments from the transposing LDS read).
+// With one range the LDS-resident query-slice tile runs (attn_tile.h: 16 queries per block, the
+// key range staged at once and split between the waves, V^T fragments from the transposing LDS
+// read).
 #include <algorithm>
 #include <stdexcept>
 #include <string>
@@ -29,10 +30,11 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
     attention_tile(p, blockIdx.x, blockIdx.y, blockIdx.z, lds, &s_last);
 }
 
-// One block per (query block, head), the key range staged in LDS (dynamic, att_lds_bytes(gmax)).
-__global__ __launch_bounds__(256) void attention_lds_kernel(AttnParams p, int gmax) {
+// One block per (16-query slice, head), the key range staged in LDS (dynamic,
+// att_lds_bytes(gkeys)).
+__global__ __launch_bounds__(256) void attention_lds_kernel(AttnParams p, int gkeys) {
     extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
-    attention_lds_tile(p, blockIdx.x, blockIdx.y, lds_dyn, gmax);
+    attention_slice_tile(p, blockIdx.x, lds_dyn, gkeys);
 }
 
 // Lets the LDS-resident kernel have its dynamic LDS (once per process; the engine calls it at
@@ -40,15 +42,15 @@ __global__ __launch_bounds__(256) void attention_lds_kernel(AttnParams p, int gm
 bool attention_prepare() {
     static const bool ok =
         hipFuncSetAttribute(reinterpret_cast<const void*>(attention_lds_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, att_lds_bytes(8)) == hipSuccess;
+                            hipFuncAttributeMaxDynamicSharedMemorySize, att_lds_bytes(512)) == hipSuccess;
     return ok;
 }
 
-// Key blocks the LDS holds at once for an attention over n rows: all a tile reaches, up to 8.
-int attention_gmax(int n, int window) {
-    const int blocks = (n + 63) / 64;
-    const int reach = window > 0 ? 2 * ((window + 63) / 64) + 1 : blocks;
-    return std::max(1, std::min({8, blocks, reach}));
+// Keys the LDS holds at once for an attention over n rows: all a 16-query slice reaches (from a
+// 32-aligned start, in steps of 32), up to 512.
+int attention_gkeys(int n, int window) {
+    const int reach = window > 0 ? std::min(n, 16 + 2 * window) + 31 : n;
+    return std::max(32, std::min(512, (reach + 31) / 32 * 32));
 }
 
 size_t attention_ws_floats(int n, int d, int chunks) {
@@ -61,7 +63,7 @@ size_t attention_counters(int n, int d) { return (size_t)((n + 63) / 64) * (d / 
 // Key ranges per tile (the reference's default_plan splits global attention, src/forward.rs:
 // 186-187). With the key range staged in LDS in one round trip, a tile's key loop is short and
 // a split's merge (two more round trips through memory) costs more than it saves up to the
-// longest requests: one range. Longer ranges go through LDS in groups of 8 key blocks.
+// longest requests: one range. Longer ranges go through LDS in groups of 512 keys.
 int attention_chunks(int n, int d, int window, int cus) {
     (void)n, (void)d, (void)window, (void)cus;
     return 1;
@@ -81,9 +83,9 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
     AttnParams p{qkv, o, n, d, window, chunks, s.ws, s.counters};
     if (chunks == 1) {
         if (!attention_prepare()) fail("the LDS-resident kernel cannot have its LDS");
-        const int gmax = attention_gmax(n, window);
-        hipLaunchKernelGGL(attention_lds_kernel, dim3((n + 63) / 64, d / 64), dim3(256),
-                           att_lds_bytes(gmax), st, p, gmax);
+        const int gkeys = attention_gkeys(n, window);
+        hipLaunchKernelGGL(attention_lds_kernel, dim3((n + 15) / 16 * (d / 64)), dim3(256),
+                           att_lds_bytes(gkeys), st, p, gkeys);
     } else {
         hipLaunchKernelGGL(attention_kernel, dim3((n + 63) / 64, d / 64, chunks), dim3(256), 0, st, p);
     }

@@ -207,49 +207,62 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
     __syncthreads();  // the tiles are free again
 }
 
-// ---- the LDS-resident tile ----------------------------------------------------------------
-// The same arithmetic as attention_tile with the tile's whole key range staged at once: Q (64
-// queries) and K and V of up to `gmax` key blocks go into LDS with direct global -> LDS loads in
-// one round trip, so the key loop never waits for memory (ranges longer than gmax blocks go in
-// groups). K and V stay row-major ([key][d], 128-byte rows, the 16-byte chunks of row r stored at
-// chunk ^ (r % 8) so a fragment's 16 rows spread over the banks); V^T fragments come from the
-// transposing LDS read. No key ranges: one block per (query block, head).
+// ---- the LDS-resident query slice ---------------------------------------------------------
+// The same arithmetic as attention_tile, shaped for latency: a task is 16 queries of one head
+// (n / 16 x heads tasks, so short sequences still spread over the GPU), and the block's four
+// waves split the slice's key range between them in steps of 32 keys, each keeping its own
+// running max, sum and output, merged through LDS at the end. Q and the key range's K and V go
+// into LDS with direct global -> LDS loads, all in one round trip (ranges longer than `gkeys`
+// keys go in groups). K and V stay row-major ([key][d], 128-byte rows, the 16-byte chunks of row
+// r stored at chunk ^ (r % 8) so a fragment's 16 rows spread over the banks); V^T fragments come
+// from the transposing LDS read. No key ranges across blocks.
 
-// LDS bytes of attention_lds_tile with gmax key blocks per group.
-__host__ __device__ constexpr int att_lds_bytes(int gmax) { return 8192 * (1 + 2 * gmax); }
+// LDS bytes of attention_slice_tile staging up to gkeys keys at once (a multiple of 32); the
+// waves' merge reuses the space.
+__host__ __device__ constexpr int att_lds_bytes(int gkeys) {
+    return 2048 + 256 * gkeys > 4 * 18 * 64 * 4 ? 2048 + 256 * gkeys : 4 * 18 * 64 * 4;
+}
 
 // Byte offset of 16-byte chunk `ch` of row `r` in a swizzled [rows][64 f16] LDS tile.
 __device__ __forceinline__ int att_swz(int r, int ch) { return (r * 8 + (ch ^ (r & 7))) * 16; }
 
-template <bool XG = false>
-__device__ __forceinline__ void attention_lds_tile(const AttnParams& p, int qb, int h, char* lds,
-                                                   int gmax) {
-    const int n = p.n, d = p.d, ld = 3 * d;
-    const int q0 = qb * 64;
+// Task `task` of (n + 15) / 16 slices x heads (XCD-mapped so a head's slices share an XCD's L2).
+// XL: qkv is read device-coherent; XS: o is stored device-coherent.
+template <bool XL = false, bool XS = false>
+__device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int task, char* lds,
+                                                     int gkeys, uint64_t* sub = nullptr) {
+    auto mark = [&](int i) {  // profiling: thread 0's view of the task's stages
+        if (sub && threadIdx.x == 0) sub[i] = wall_clock64();
+    };
+    const int n = p.n, d = p.d, ld = 3 * d, heads = d >> 6;
+    const int slices = (n + 15) >> 4, T = slices * heads;
+    const int L = xcd_task(task, T);
+    const int h = L / slices, q0 = (L % slices) * 16;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g = l >> 4;
+    const int j = r16 >> 2, q = r16 & 3;
     char* qs = lds;
-    char* ks = lds + 8192;
-    char* vs = ks + gmax * 8192;
+    char* ks = lds + 2048;
+    char* vs = ks + gkeys * 128;
 
-    const int nb = (n + 63) >> 6;
-    int kb0 = 0, kb1 = nb;
+    int k0 = 0, k1 = n;
     if (p.window > 0) {
-        kb0 = max(q0 - p.window, 0) >> 6;
-        kb1 = (min(q0 + 63 + p.window, n - 1) >> 6) + 1;
+        k0 = max(q0 - p.window, 0);
+        k1 = min(q0 + 16 + p.window, n);
     }
+    k0 &= ~31;
 
-    // rows [r0, r0 + rows) of qkv's columns col.. col + 63 (clamped to row n - 1) into `dst`:
-    // wave load I of the copy fills LDS chunks 64 I .. 64 I + 63, lane l chunk 64 I + l, which
-    // is row c / 8, logical chunk (c % 8) ^ (row % 8).
+    // rows [r0, r0 + rows) (rows % 8 == 0) of qkv's columns col .. col + 63, clamped to row
+    // n - 1, into `dst`: wave load I fills LDS chunks 64 I .. 64 I + 63, lane l chunk 64 I + l,
+    // which is row c / 8, logical chunk (c % 8) ^ (row % 8).
     auto stage = [&](char* dst, int r0, int rows, int col) {
         for (int I = w; I * 64 < rows * 8; I += 4) {
             const int c = I * 64 + l, row = c >> 3, ch = (c & 7) ^ (row & 7);
             const f16* src = (const f16*)p.qkv + (size_t)min(r0 + row, n - 1) * ld + col + ch * 8;
-            lds_dma16<XG>(src, dst + I * 1024);
+            lds_dma16<XL>(src, dst + I * 1024);
         }
     };
 
-    const int qi = q0 + 16 * w + r16;  // this lane's query
+    const int qi = q0 + r16;  // this lane's query (the same 16 in every wave)
     const float scale = 1.4426950408889634f / 8.0f;  // log2(e) / sqrt(64)
     float mx = -INFINITY, lsum = 0.0f;
     floatx4 oacc[4];
@@ -257,41 +270,69 @@ __device__ __forceinline__ void attention_lds_tile(const AttnParams& p, int qb, 
     for (int t = 0; t < 4; t++) oacc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     half8 qf[2];
 
-    for (int gb = kb0; gb < kb1; gb += gmax) {
-        const int nbk = min(gmax, kb1 - gb);
-        if (gb == kb0) stage(qs, q0, 64, h * 64);
-        stage(ks, gb * 64, nbk * 64, d + h * 64);
-        stage(vs, gb * 64, nbk * 64, 2 * d + h * 64);
+    for (int gk = k0; gk < k1; gk += gkeys) {
+        const int steps = (min(gkeys, k1 - gk) + 31) >> 5;
+        if (gk == k0) stage(qs, q0, 16, h * 64);
+        stage(ks, gk, steps * 32, d + h * 64);
+        stage(vs, gk, steps * 32, 2 * d + h * 64);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();  // the group is in LDS
-        if (gb == kb0) {
-            const int qr = 16 * w + r16;
+        if (gk == k0) {
+            mark(0);
 #pragma unroll
-            for (int k2 = 0; k2 < 2; k2++) qf[k2] = *(const half8*)(qs + att_swz(qr, 4 * k2 + g));
+            for (int k2 = 0; k2 < 2; k2++) qf[k2] = *(const half8*)(qs + att_swz(r16, 4 * k2 + g));
         }
-        for (int b = 0; b < nbk; b++) {
-            const int kbase = (gb + b) * 64;
-            // S^T for keys 16 t + 4 g + e of this block, query qi.
-            floatx4 sc[4];
+        for (int st = w * steps / 4; st < (w + 1) * steps / 4; st++) {
+            const int kb = gk + 32 * st, rb = 32 * st;  // the step's first key and LDS row
+            // Every LDS read of the step first (K fragments of its two 16-key S tiles; V^T
+            // fragments: lane (g, 4 j + q) addresses key rb + 4 g + j (+ 16), d 16 dt + 4 q), so
+            // their latencies overlap.
+            half8 kf[2][2];
+            half4 vlo[4], vhi[4];
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                sc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-                const int kr = b * 64 + 16 * t + r16;
+            for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int k2 = 0; k2 < 2; k2++)
-                    sc[t] = mfma16(*(const half8*)(ks + att_swz(kr, 4 * k2 + g)), qf[k2], sc[t]);
+                    kf[t][k2] = *(const half8*)(ks + att_swz(rb + 16 * t + r16, 4 * k2 + g));
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                const int ch = 2 * dt + (q >> 1), off = (q & 1) * 8;
+                vlo[dt] = lds_read_tr16(vs + att_swz(rb + 4 * g + j, ch) + off);
+                vhi[dt] = lds_read_tr16(vs + att_swz(rb + 16 + 4 * g + j, ch) + off);
             }
+            __builtin_amdgcn_sched_barrier(0);
+            // S^T for keys kb + 16 t + 4 g + e, query qi.
+            floatx4 sc[2];
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                sc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int k2 = 0; k2 < 2; k2++) sc[t] = mfma16(kf[t][k2], qf[k2], sc[t]);
+            }
+            // A step inside the sequence and, for all 16 queries, inside the window needs no mask.
+            const bool full = kb + 32 <= n &&
+                              (p.window == 0 || (q0 + 15 - kb <= p.window && kb + 31 - q0 <= p.window));
             float bm = -INFINITY;
+            if (full) {
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+                for (int t = 0; t < 2; t++)
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const int key = kbase + 16 * t + 4 * g + e;
-                    const int dist = qi > key ? qi - key : key - qi;
-                    const bool ok = key < n && (p.window == 0 || dist <= p.window);
-                    sc[t][e] = ok ? sc[t][e] * scale : -INFINITY;
-                    bm = fmaxf(bm, sc[t][e]);
-                }
+                    for (int e = 0; e < 4; e++) {
+                        sc[t][e] *= scale;
+                        bm = fmaxf(bm, sc[t][e]);
+                    }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 2; t++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int key = kb + 16 * t + 4 * g + e;
+                        const int dist = qi > key ? qi - key : key - qi;
+                        const bool ok = key < n && (p.window == 0 || dist <= p.window);
+                        sc[t][e] = ok ? sc[t][e] * scale : -INFINITY;
+                        bm = fmaxf(bm, sc[t][e]);
+                    }
+            }
             bm = fmaxf(bm, __shfl_xor(bm, 16));
             bm = fmaxf(bm, __shfl_xor(bm, 32));
             const float mnew = fmaxf(mx, bm);
@@ -300,56 +341,78 @@ __device__ __forceinline__ void attention_lds_tile(const AttnParams& p, int qb, 
             mx = mnew;
             float rs = 0.0f;
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+            for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     sc[t][e] = exp2f(sc[t][e] - base);
                     rs += sc[t][e];
                 }
             lsum = lsum * alpha + rs;
+            // O^T += V^T . P^T: lane group g holds (as its P^T values) keys kb + 4 g + (0..3) and
+            // kb + 16 + 4 g + (0..3), the keys of its V^T fragment.
+            half8 pf;
 #pragma unroll
-            for (int t = 0; t < 4; t++) oacc[t] *= alpha;
-
-            // O^T += V^T . P^T over K steps k2 of 32 keys: lane group g holds (as its P^T values)
-            // keys 32 k2 + 4 g + (0..3) and 32 k2 + 16 + 4 g + (0..3). Its V^T fragment for d rows
-            // 16 dt + r16 comes from two transposing reads: lane (g, 4 j + q) addresses key
-            // 32 k2 + 4 g + j (+ 16), d 16 dt + 4 q .. + 3.
-            const int j = r16 >> 2, q = r16 & 3;
+            for (int e = 0; e < 4; e++) {
+                pf[e] = (f16)sc[0][e];
+                pf[4 + e] = (f16)sc[1][e];
+            }
 #pragma unroll
-            for (int k2 = 0; k2 < 2; k2++) {
-                half8 pf;
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    pf[e] = (f16)sc[2 * k2][e];
-                    pf[4 + e] = (f16)sc[2 * k2 + 1][e];
-                }
-                const int vr = b * 64 + 32 * k2 + 4 * g + j;
-#pragma unroll
-                for (int dt = 0; dt < 4; dt++) {
-                    const int ch = 2 * dt + (q >> 1), off = (q & 1) * 8;
-                    const half4 lo = lds_read_tr16(vs + att_swz(vr, ch) + off);
-                    const half4 hi = lds_read_tr16(vs + att_swz(vr + 16, ch) + off);
-                    const half8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    oacc[dt] = mfma16(vf, pf, oacc[dt]);
-                }
+            for (int dt = 0; dt < 4; dt++) {
+                const half4 lo = vlo[dt], hi = vhi[dt];
+                const half8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                oacc[dt] = mfma16(vf, pf, oacc[dt] * alpha);  // rescaled to the new max
             }
         }
         __syncthreads();  // the group's tiles are no longer read
     }
 
+    // The waves' partials (output, max, sum over the query's keys) through LDS; wave 0 merges.
     float tot = lsum + __shfl_xor(lsum, 16);
     tot += __shfl_xor(tot, 32);
-    const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
-    if (qi < n) {
-        f16* op = (f16*)p.o + (size_t)qi * d + h * 64 + 4 * g;
+    float* mg = (float*)lds;  // [wave][18][64]
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) {
-            half4 o;
+    for (int dt = 0; dt < 4; dt++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) o[e] = (f16)(oacc[dt][e] * inv);
-            store8<XG>(op + 16 * dt, o);
+        for (int e = 0; e < 4; e++) mg[(w * 18 + dt * 4 + e) * 64 + l] = oacc[dt][e];
+    mg[(w * 18 + 16) * 64 + l] = mx;
+    mg[(w * 18 + 17) * 64 + l] = tot;
+    __syncthreads();
+    if (w == 0) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) m = fmaxf(m, mg[(ww * 18 + 16) * 64 + l]);
+        const float base = m == -INFINITY ? 0.0f : m;
+        float sum = 0.0f;
+        floatx4 o[4];
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) o[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ww = 0; ww < 4; ww++) {
+            const float f = exp2f(mg[(ww * 18 + 16) * 64 + l] - base);
+            sum += mg[(ww * 18 + 17) * 64 + l] * f;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[dt][e] += mg[(ww * 18 + dt * 4 + e) * 64 + l] * f;
+        }
+        mark(1);
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        if (qi < n) {
+            f16* op = (f16*)p.o + (size_t)qi * d + h * 64 + 4 * g;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                half4 ov;
+#pragma unroll
+                for (int e = 0; e < 4; e++) ov[e] = (f16)(o[dt][e] * inv);
+                store8<XS>(op + 16 * dt, ov);
+            }
+        }
+        if (sub) {
+            release_wait();
+            mark(2);
         }
     }
+    __syncthreads();  // LDS is free again
 }
 
 }  // namespace jh

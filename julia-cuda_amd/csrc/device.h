@@ -257,7 +257,8 @@ __device__ __forceinline__ void epi_load_col(const GemmParams& p, int grp, int c
     }
 }
 
-template <int EPI, bool XG>
+// XS: the statistics are read device-coherent; XR: the residual rows are.
+template <int EPI, bool XS, bool XR = XS>
 __device__ __forceinline__ void epi_load_row(const GemmParams& p, int row, int grp, int c0,
                                              EpiRow& e) {
     const int r = min(row, p.m - 1);
@@ -265,7 +266,7 @@ __device__ __forceinline__ void epi_load_row(const GemmParams& p, int row, int g
         const int slots = p.k >> 6, j = c0 >> 2;
         const float* st = p.stats_in + (size_t)r * slots * 2;
 #pragma unroll
-        for (int i = 0; i < EPI_PRE_SLOTS; i++) e.st[i] = load8f<XG>(st + 2 * min(j + 8 * i, slots - 1));
+        for (int i = 0; i < EPI_PRE_SLOTS; i++) e.st[i] = load8f<XS>(st + 2 * min(j + 8 * i, slots - 1));
     }
     if (EPI & EPI_ROPE) {
         const int pos = min(p.pos ? max(p.pos[r], 0) : r, p.rope_rows - 1);
@@ -274,9 +275,9 @@ __device__ __forceinline__ void epi_load_row(const GemmParams& p, int row, int g
         e.rt[1] = t[1];
     }
     if ((EPI & EPI_RES) && !(EPI & EPI_GEGLU)) {
-        const f16* x = (const f16*)p.c + (size_t)r * p.n + grp * 64 + c0;
-        e.rl = load8h<XG>(x);
-        e.rh = load8h<XG>(x + 32);
+        const f16* x = (const f16*)(p.res ? p.res : p.c) + (size_t)r * p.n + grp * 64 + c0;
+        e.rl = load8h<XR>(x);
+        e.rh = load8h<XR>(x + 32);
     }
 }
 

@@ -63,6 +63,9 @@ struct Engine {
     // Every layer's weights for the persistent encoder kernel, on the device and the host.
     LayerDesc* layers_d = nullptr;
     std::vector<LayerDesc> layers_h;
+    // Its write-once activation buffers (LayerArgs): x after each residual step, each layer's
+    // qkv and o, max_length rows each.
+    jh_half *xa = nullptr, *qa = nullptr, *oa = nullptr;
     // The per-step forward pass as HIP graphs, one per (tokens, markers, question type): 124
     // launches submitted as one. They read the request from fixed buffers (gin: ids, then
     // markers at max_length) and write glogits; stream order keeps queued requests apart.
@@ -87,7 +90,8 @@ struct Engine {
         for (void* p : {(void*)w16, (void*)w32, (void*)x, (void*)qkv, (void*)o, (void*)mid,
                         (void*)hx, (void*)stats_a, (void*)stats_b, (void*)ids_d,
                         (void*)markers_d, (void*)logits_d, (void*)scratch.ws,
-                        (void*)scratch.counters, (void*)layers_d})
+                        (void*)scratch.counters, (void*)layers_d, (void*)xa, (void*)qa,
+                        (void*)oa})
             if (p) hipFree(p);
         if (ids_h) hipHostFree(ids_h);
         if (markers_h) hipHostFree(markers_h);
@@ -129,19 +133,25 @@ struct Engine {
              stats_b);
     }
 
-    // The persistent encoder kernel: layers [first, first + count) as one cooperative launch.
-    LayerArgs layer_args(int first, int count, int n) const {
+    // The persistent encoder kernel: layers [first, first + count) as one cooperative launch,
+    // from the residual stream in x_in.
+    LayerArgs layer_args(int first, int count, int n, const jh_half* x_in) const {
         LayerArgs a{};
-        a.x = x, a.qkv = qkv, a.o = o, a.mid = mid, a.stats_attn = stats_a, a.stats_mlp = stats_b;
+        const size_t ml = (size_t)max_length, d = cfg.d;
+        a.x_in = x_in, a.xa = xa, a.qa = qa, a.oa = oa, a.mid = mid;
+        a.x_stride = ml * d, a.q_stride = ml * 3 * d, a.o_stride = ml * d;
+        a.stats_attn = stats_a, a.stats_mlp = stats_b;
         a.layers = layers_d, a.host_layers = layers_h.data(), a.first = first, a.count = count;
         a.m = n, a.d = cfg.d, a.inter = cfg.inter, a.eps = cfg.norm_eps;
         a.rope_rows = cfg.max_positions;
         return a;
     }
 
-    void launch_encoder_fused(int first, int count, int n) {
-        layer_kernel.launch(layer_args(first, count, n), layer_kernel.default_plan(n, cfg.d, cfg.inter),
-                            scratch, stream);
+    // Returns where the residual stream is after the launch.
+    const jh_half* launch_encoder_fused(int first, int count, int n, const jh_half* x_in) {
+        const LayerArgs a = layer_args(first, count, n, x_in);
+        layer_kernel.launch(a, layer_kernel.default_plan(n, cfg.d, cfg.inter), scratch, stream);
+        return LayerKernel::x_out(a);
     }
 
     // ---- the head (src/forward.rs GpuHead) -------------------------------------------------
@@ -149,7 +159,8 @@ struct Engine {
     // with bias from stats_a; global attention, no RoPE; out_proj + bias + residual, statistics
     // into stats_b; linear1: LN from stats_b, bias, ReLU; linear2 + bias + residual, statistics
     // into stats_a), the scorer's lin1 (LN from stats_a, bias, GELU) and the score.
-    void launch_head(int n, int qtype, const uint32_t* markers, int nm, float* logits) {
+    void launch_head(const jh_half* x, int n, int qtype, const uint32_t* markers, int nm,
+                     float* logits) {
         const int d = cfg.d, F = cfg.head_ff;
         norm_add_launch(x, n, d, f(layout.final_norm), f(layout.type_emb) + (size_t)qtype * d,
                         cfg.norm_eps, hx, stats_a, stream);
@@ -204,11 +215,12 @@ struct Engine {
                 float* logits, bool fused) {
         embed_launch(ids, n, h(layout.tok_embeddings), cfg.vocab, cfg.d, f(layout.emb_norm),
                      cfg.norm_eps, x, stream);
+        const jh_half* xf = x;
         if (fused)
-            launch_encoder_fused(0, cfg.layers, n);
+            xf = launch_encoder_fused(0, cfg.layers, n, x);
         else
             for (int l = 0; l < cfg.layers; l++) launch_layer(l, n);
-        launch_head(n, qtype, markers, nm, logits);
+        launch_head(xf, n, qtype, markers, nm, logits);
     }
 };
 
@@ -293,6 +305,9 @@ Engine* load_engine(const char* dir, size_t max_length) {
         e->layers_h.push_back(ld);
     }
     e->layers_d = dalloc<LayerDesc>(e->layers_h.size(), "layer table");
+    e->xa = dalloc<jh_half>(2 * (size_t)c.layers * n * d, "encoder activations");
+    e->qa = dalloc<jh_half>((size_t)c.layers * n * 3 * d, "encoder activations");
+    e->oa = dalloc<jh_half>((size_t)c.layers * n * d, "encoder activations");
     hip_check(hipMemcpy(e->layers_d, e->layers_h.data(), e->layers_h.size() * sizeof(LayerDesc),
                         hipMemcpyHostToDevice), "layer table");
     e->layer_kernel.init(e->cus, (int)prop.sharedMemPerBlock);
@@ -870,7 +885,7 @@ int julia_hip_profile_layer(const Engine* ce, int n, int layer, const int* plan,
         // One layer (after the ones before it, per step) or, with layer -1, the whole encoder.
         const int first = layer < 0 ? 0 : layer, count = layer < 0 ? e.cfg.layers : 1;
         for (int l = 0; l < first; l++) e.launch_layer(l, n);
-        const LayerArgs a = e.layer_args(first, count, n);
+        const LayerArgs a = e.layer_args(first, count, n, e.x);
         LayerPlan p = e.layer_kernel.default_plan(n, e.cfg.d, e.cfg.inter);
         if (plan) {
             for (int g = 0; g < 4; g++) p.bm[g] = plan[g], p.splits[g] = plan[4 + g];
@@ -916,18 +931,19 @@ int julia_hip_run_trace(const Engine* ce, const uint32_t* ids, size_t n, const u
         const size_t d = e.cfg.d;
         embed_launch(e.ids_d, (int)n, e.h(e.layout.tok_embeddings), e.cfg.vocab, e.cfg.d,
                      e.f(e.layout.emb_norm), e.cfg.norm_eps, e.x, e.stream);
+        const jh_half* xl = e.x;  // the residual stream after each layer
         for (int l = 0; l < e.cfg.layers; l++) {
             if (layer_fused)
-                e.launch_encoder_fused(l, 1, (int)n);
+                xl = e.launch_encoder_fused(l, 1, (int)n, xl);
             else
                 e.launch_layer(l, (int)n);
             if (x_trace) {
-                hip_check(hipMemcpyAsync(x_trace + (size_t)l * n * d, e.x, n * d * 2,
+                hip_check(hipMemcpyAsync(x_trace + (size_t)l * n * d, xl, n * d * 2,
                                          hipMemcpyDeviceToHost, e.stream), "trace");
                 hip_check(hipStreamSynchronize(e.stream), "trace");
             }
         }
-        e.launch_head((int)n, (int)qtype, e.markers_d, (int)n_markers, e.logits_d);
+        e.launch_head(xl, (int)n, (int)qtype, e.markers_d, (int)n_markers, e.logits_d);
         hip_check(hipStreamSynchronize(e.stream), "forward");
         if (layer_fused && e.layer_kernel.barrier_timed_out())
             throw std::runtime_error("layer: a grid barrier timed out (blocks not co-resident)");

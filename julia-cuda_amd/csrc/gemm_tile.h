@@ -221,11 +221,14 @@ constexpr int w_red_floats() { return 4 * BM * 68; }
 
 // Task `task` of c = epilogue(a . w^T) in the persistent kernel. The weight tile is in `lds`
 // already (w_ready: its loads were issued earlier by this block, maybe still in flight) or is
-// fetched here. a is read device-coherent (another block wrote it in this kernel) with 16-byte
-// buffer loads, rows past m reading zeros. The four waves split the tile's K units; their partial
-// tiles are summed through LDS, in the weight tile's space. Every thread calls this; it ends
-// with a block barrier after the last LDS access.
-template <int BM, int EPI>
+// fetched here. a is read with 16-byte buffer loads, rows past m reading zeros: device-coherent
+// when AX (a buffer other blocks write more than once per launch, or several blocks write parts
+// of one line), else through the caches (a buffer written once per launch, each 128-byte line by
+// one block: no L2 can hold a stale copy). The statistics are read device-coherent, the residual
+// (a write-once buffer) through the caches; the outputs are stored device-coherent. The four
+// waves split the tile's K units; their partial tiles are summed through LDS, in the weight
+// tile's space. Every thread calls this; it ends with a block barrier after the last LDS access.
+template <int BM, int EPI, bool AX>
 __device__ __forceinline__ void gemm_w_tile(const GemmParams& p, int task, char* lds, bool w_ready,
                                             uint32_t* s_last, uint64_t* sub = nullptr) {
     auto mark = [&](int i) {  // profiling: thread 0's view of the task's stages
@@ -250,7 +253,7 @@ __device__ __forceinline__ void gemm_w_tile(const GemmParams& p, int task, char*
     EpiRow er[NPASS];
     epi_load_col<EPI>(p, bx, c0, ec);
 #pragma unroll
-    for (int ps = 0; ps < NPASS; ps++) epi_load_row<EPI, true>(p, by * BM + ps * 32 + (tid >> 3), bx, c0, er[ps]);
+    for (int ps = 0; ps < NPASS; ps++) epi_load_row<EPI, true, false>(p, by * BM + ps * 32 + (tid >> 3), bx, c0, er[ps]);
 
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(p.a, (uint32_t)p.m * (uint32_t)p.k * 2u);
     uint32_t aoff[MI];
@@ -270,7 +273,7 @@ __device__ __forceinline__ void gemm_w_tile(const GemmParams& p, int task, char*
         for (int s = 0; s < UMAX; s++) {
             const uint32_t du = (uint32_t)(min(u + s, u1 - 1) - u0) * 64u;
 #pragma unroll
-            for (int i = 0; i < MI; i++) fa[s][i] = bload16<true>(ra, aoff[i] + du);
+            for (int i = 0; i < MI; i++) fa[s][i] = bload16<AX>(ra, aoff[i] + du);
         }
     };
     // The weight fragments of unit s + 1 are read from LDS while unit s's MFMAs run (the reads

@@ -43,6 +43,7 @@ struct GemmParams {
     const jh_half* a;
     const jh_half* w;
     jh_half* c;
+    const jh_half* res;     // residual rows [m][n] (null: c itself, updated in place)
     const float* stats_in;
     const float* colsum;
     const float* bias;
@@ -115,7 +116,7 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
 size_t attention_ws_floats(int n, int d, int chunks);
 size_t attention_counters(int n, int d);
 int attention_chunks(int n, int d, int window, int cus);
-int attention_gmax(int n, int window);
+int attention_gkeys(int n, int window);
 bool attention_prepare();
 
 void embed_launch(const uint32_t* ids, int n, const jh_half* table, int vocab, int d,

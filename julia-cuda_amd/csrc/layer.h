@@ -17,9 +17,10 @@ namespace jh {
 // them zero, and the host clears them after a barrier time-out).
 constexpr int BAR_WORDS = 11 * 32;
 // u64 words per block and layer of the kernel's timestamps: (start, end) of phase p at 2p,
-// 2p + 1 (100 MHz clock), the block's CU id at 10, and for the block's first task of GEMM g
-// (qkv, wo, wi, wo_mlp) at 16 + 4 g + i: its inputs in place (weights in LDS, activations in
-// registers), its MFMAs done, its partial tiles reduced, its epilogue done.
+// 2p + 1 (100 MHz clock), the block's CU id at 10; for the block's first attention task at 12 + i:
+// its key range in LDS, its key loop done, its output stored; and for the block's first task of
+// GEMM g (qkv, wo, wi, wo_mlp) at 16 + 4 g + i: its inputs in place (weights in LDS, activations
+// in registers), its MFMAs done, its partial tiles reduced, its epilogue done.
 constexpr int PROF_WORDS = 32;
 
 // One layer's weights, as the kernel reads them (an array of these lives in device memory).
@@ -31,8 +32,16 @@ struct LayerDesc {
     int pad_;
 };
 
+// The activations of a launch: every output of a phase that other blocks read through their
+// caches goes to a buffer of its own, written once per launch (no L2 can hold a stale copy):
+// layer l reads x_in (its first layer) or xa[2 l - 1], writes xa[2 l] (after wo) and
+// xa[2 l + 1] (after wo_mlp), qkv into qa[l] and o into oa[l] (slots of x_stride, q_stride and
+// o_stride elements; l is the absolute layer index). mid and the statistics, which several
+// blocks write parts of per line, are single buffers read device-coherent.
 struct LayerArgs {
-    jh_half *x, *qkv, *o, *mid;
+    const jh_half* x_in;
+    jh_half *xa, *qa, *oa, *mid;
+    size_t x_stride, q_stride, o_stride;
     float *stats_attn, *stats_mlp;  // wo writes stats_attn (wi reads it), wo_mlp stats_mlp
     const LayerDesc* layers;        // device array, indexed by layer
     const LayerDesc* host_layers;   // the same on the host (for the plan and the checks)
@@ -68,6 +77,10 @@ public:
     // Whether a grid barrier gave up waiting since the last call (then clears the words).
     // Synchronizes with the device.
     bool barrier_timed_out();
+    // Where the launch of `a` leaves the residual stream (x after its last layer).
+    static jh_half* x_out(const LayerArgs& a) {
+        return a.xa + (size_t)(2 * (a.first + a.count - 1) + 1) * a.x_stride;
+    }
     int per_cu() const { return per_cu_; }
     bool available() const { return per_cu_ > 0; }
 

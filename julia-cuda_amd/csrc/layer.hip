@@ -11,6 +11,10 @@
 //
 // The row statistics need no clearing phase: the resstats epilogue writes (not adds) one partial
 // per row and 64-column group.
+//
+// Activations written once per launch (x after each residual step, each layer's qkv and o, each
+// in its own buffer: LayerArgs) are read through the caches; mid and the statistics are read
+// device-coherent. Every output is stored device-coherent (written through to memory).
 #include <algorithm>
 #include <stdexcept>
 #include <string>
@@ -24,7 +28,9 @@ namespace jh {
 struct EncParams {
     const LayerDesc* layers;
     int first, count;
-    jh_half *x, *qkv, *o, *mid;
+    const jh_half* x_in;
+    jh_half *xa, *qa, *oa, *mid;
+    size_t x_stride, q_stride, o_stride;
     float *stats_attn, *stats_mlp;
     int m, d, inter, rope_rows;
     float eps;
@@ -34,7 +40,7 @@ struct EncParams {
     unsigned phases;  // bits 0-4
     int barriers;     // grid barriers in this launch
     int lds_main;     // dynamic LDS bytes before the block's split-K flag
-    int att_gmax[2];  // key blocks the attention tile stages at once: global, window layers
+    int att_gkeys[2];  // keys the attention tile stages at once: global, window layers
     uint32_t* bar;    // the barrier's words (BAR_WORDS, zero between launches)
     uint64_t* prof;   // null, or PROF_WORDS per block and layer: see stamp()
 };
@@ -106,21 +112,36 @@ __device__ __forceinline__ void grid_sync(uint32_t* bar, uint32_t g0, uint32_t n
     __syncthreads();
 }
 
-__device__ __forceinline__ GemmParams make_gemm(const EncParams& P, int g, const LayerDesc& L) {
+// Layer l's activation buffers (LayerArgs): x in, after wo, after wo_mlp; qkv; o.
+__device__ __forceinline__ const jh_half* x_in_of(const EncParams& P, int l) {
+    return l == P.first ? P.x_in : P.xa + (size_t)(2 * l - 1) * P.x_stride;
+}
+__device__ __forceinline__ jh_half* x_attn_of(const EncParams& P, int l) {
+    return P.xa + (size_t)(2 * l) * P.x_stride;
+}
+__device__ __forceinline__ jh_half* x_out_of(const EncParams& P, int l) {
+    return P.xa + (size_t)(2 * l + 1) * P.x_stride;
+}
+
+__device__ __forceinline__ GemmParams make_gemm(const EncParams& P, int g, const LayerDesc& L,
+                                                int l) {
     GemmParams p{};
     p.m = P.m, p.eps = P.eps, p.ws = P.ws, p.counters = P.counters;
     p.splits = P.splits[g];
     if (g == 0) {
-        p.a = P.x, p.w = L.wqkv, p.c = P.qkv, p.n = 3 * P.d, p.k = P.d;
+        p.a = x_in_of(P, l), p.w = L.wqkv, p.c = P.qa + (size_t)l * P.q_stride;
+        p.n = 3 * P.d, p.k = P.d;
         p.rope = L.rope, p.rope_cols = 2 * P.d, p.rope_rows = P.rope_rows;
         if (L.qkv_colsum) p.stats_in = P.stats_mlp, p.colsum = L.qkv_colsum;
     } else if (g == 1) {
-        p.a = P.o, p.w = L.wo, p.c = P.x, p.n = P.d, p.k = P.d, p.stats_out = P.stats_attn;
+        p.a = P.oa + (size_t)l * P.o_stride, p.w = L.wo, p.c = x_attn_of(P, l), p.res = x_in_of(P, l);
+        p.n = P.d, p.k = P.d, p.stats_out = P.stats_attn;
     } else if (g == 2) {
-        p.a = P.x, p.w = L.wi, p.c = P.mid, p.n = 2 * P.inter, p.k = P.d;
+        p.a = x_attn_of(P, l), p.w = L.wi, p.c = P.mid, p.n = 2 * P.inter, p.k = P.d;
         p.stats_in = P.stats_attn, p.colsum = L.wi_colsum;
     } else {
-        p.a = P.mid, p.w = L.wo_mlp, p.c = P.x, p.n = P.d, p.k = P.inter, p.stats_out = P.stats_mlp;
+        p.a = P.mid, p.w = L.wo_mlp, p.c = x_out_of(P, l), p.res = x_attn_of(P, l);
+        p.n = P.d, p.k = P.inter, p.stats_out = P.stats_mlp;
     }
     p.tiles_n = p.n >> 6;
     p.tiles_m = (P.m + P.bm[g] - 1) / P.bm[g];
@@ -131,7 +152,7 @@ __device__ __forceinline__ int gemm_tasks(const GemmParams& g) {
     return g.tiles_n * g.tiles_m * g.splits;
 }
 
-template <int EPI>
+template <int EPI, bool AX>
 __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* lds, bool pre,
                                            uint32_t* s_last, uint64_t* sub) {
     const int T = gemm_tasks(g);
@@ -140,11 +161,11 @@ __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* ld
         const bool ready = pre && first;
         uint64_t* su = first ? sub : nullptr;
         if (bm == 16)
-            gemm_w_tile<16, EPI>(g, t, lds, ready, s_last, su);
+            gemm_w_tile<16, EPI, AX>(g, t, lds, ready, s_last, su);
         else if (bm == 32)
-            gemm_w_tile<32, EPI>(g, t, lds, ready, s_last, su);
+            gemm_w_tile<32, EPI, AX>(g, t, lds, ready, s_last, su);
         else
-            gemm_w_tile<64, EPI>(g, t, lds, ready, s_last, su);
+            gemm_w_tile<64, EPI, AX>(g, t, lds, ready, s_last, su);
     }
 }
 
@@ -168,19 +189,21 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
     };
 
     LayerDesc L = P.layers[P.first];
-    GemmParams gq = make_gemm(P, 0, L);
+    GemmParams gq = make_gemm(P, 0, L, P.first);
     bool pre = false;  // the weight tile of this block's first task in the coming phase is fetched
     for (int li = 0; li < P.count; li++) {
         uint64_t* prof = P.prof ? P.prof + ((size_t)blockIdx.x * P.count + li) * PROF_WORDS : nullptr;
         if (prof && threadIdx.x == 0) prof[10] = __smid();
         auto sub = [prof](int g) { return prof ? prof + 16 + 4 * g : nullptr; };
-        const GemmParams go = make_gemm(P, 1, L), gi = make_gemm(P, 2, L), gm = make_gemm(P, 3, L);
+        const int l = P.first + li;
+        const GemmParams go = make_gemm(P, 1, L, l), gi = make_gemm(P, 2, L, l),
+                         gm = make_gemm(P, 3, L, l);
         if (on(0)) {
             stamp(prof, 0);
             if (gq.colsum)
-                gemm_phase<EPI_K_LNROPE>(gq, P.bm[0], lds, pre, s_last, sub(0));
+                gemm_phase<EPI_K_LNROPE, false>(gq, P.bm[0], lds, pre, s_last, sub(0));
             else
-                gemm_phase<EPI_K_ROPE>(gq, P.bm[0], lds, pre, s_last, sub(0));
+                gemm_phase<EPI_K_ROPE, false>(gq, P.bm[0], lds, pre, s_last, sub(0));
             pre = false;
             stamp_end(prof, 0);
             if (on(1)) sync(nothing);
@@ -188,15 +211,21 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
         if (on(1)) {
             stamp(prof, 2);
             const int chunks = L.window > 0 ? P.kv[1] : P.kv[0];
-            const AttnParams at{P.qkv, P.o, P.m, P.d, L.window, chunks, P.ws, P.counters};
-            const int heads = P.d >> 6, T = ((P.m + 63) >> 6) * heads * chunks;
-            const int gmax = P.att_gmax[L.window > 0 ? 1 : 0];
-            for (int t = blockIdx.x; t < T; t += gridDim.x) {
-                const int tile = t / chunks;
-                if (chunks == 1)
-                    attention_lds_tile<true>(at, tile / heads, tile % heads, lds, gmax);
-                else
+            const AttnParams at{P.qa + (size_t)l * P.q_stride, P.oa + (size_t)l * P.o_stride,
+                                P.m, P.d, L.window, chunks, P.ws, P.counters};
+            const int heads = P.d >> 6;
+            if (chunks == 1) {  // qkv is this layer's own buffer: read through the caches
+                const int T = ((P.m + 15) >> 4) * heads, gkeys = P.att_gkeys[L.window > 0 ? 1 : 0];
+                for (int t = blockIdx.x; t < T; t += gridDim.x) {
+                    uint64_t* su = prof && t == (int)blockIdx.x ? prof + 12 : nullptr;
+                    attention_slice_tile<false, true>(at, t, lds, gkeys, su);
+                }
+            } else {
+                const int T = ((P.m + 63) >> 6) * heads * chunks;
+                for (int t = blockIdx.x; t < T; t += gridDim.x) {
+                    const int tile = t / chunks;
                     attention_tile<true>(at, tile / heads, tile % heads, t % chunks, (f16*)lds, s_last);
+                }
             }
             stamp_end(prof, 1);
             if (on(2)) {
@@ -206,7 +235,7 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
         }
         if (on(2)) {
             stamp(prof, 4);
-            gemm_phase<EPI_K_RESSTATS>(go, P.bm[1], lds, pre, s_last, sub(1));
+            gemm_phase<EPI_K_RESSTATS, false>(go, P.bm[1], lds, pre, s_last, sub(1));
             pre = false;
             stamp_end(prof, 2);
             if (on(3)) {
@@ -216,7 +245,7 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
         }
         if (on(3)) {
             stamp(prof, 6);
-            gemm_phase<EPI_K_LNGEGLU>(gi, P.bm[2], lds, pre, s_last, sub(2));
+            gemm_phase<EPI_K_LNGEGLU, false>(gi, P.bm[2], lds, pre, s_last, sub(2));
             pre = false;
             stamp_end(prof, 3);
             if (on(4)) {
@@ -226,13 +255,13 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
         }
         if (on(4)) {
             stamp(prof, 8);
-            gemm_phase<EPI_K_RESSTATS>(gm, P.bm[3], lds, pre, s_last, sub(3));
+            gemm_phase<EPI_K_RESSTATS, true>(gm, P.bm[3], lds, pre, s_last, sub(3));
             pre = false;
             stamp_end(prof, 4);
         }
         if (li + 1 < P.count) {  // whole layers only (the host checks)
-            L = P.layers[P.first + li + 1];
-            gq = make_gemm(P, 0, L);
+            L = P.layers[l + 1];
+            gq = make_gemm(P, 0, L, l + 1);
             pre = (int)blockIdx.x < gemm_tasks(gq);
             if (pre) sync(fetch_first(gq)); else sync(nothing);
         }
@@ -262,8 +291,8 @@ static int red_bytes(int bm) { return 4 * bm * 68 * 4; }
 int LayerKernel::lds_bytes(const LayerPlan& plan, int d, int inter, int m, int window) {
     int cols[4], ks[4];
     shapes(d, inter, cols, ks);
-    int b = std::max({ATT_LDS_F16 * 2, att_lds_bytes(attention_gmax(m, 0)),
-                      att_lds_bytes(attention_gmax(m, window))});
+    int b = std::max({ATT_LDS_F16 * 2, att_lds_bytes(attention_gkeys(m, 0)),
+                      att_lds_bytes(attention_gkeys(m, window))});
     for (int g = 0; g < 4; g++)
         b = std::max({b, w_tile_bytes(ks[g], plan.splits[g]), red_bytes(plan.bm[g])});
     return (b + 15) / 16 * 16;
@@ -343,7 +372,8 @@ size_t LayerKernel::counters(int max_m, int d, int inter) const {
 int LayerKernel::grid(const LayerArgs& a, const LayerPlan& plan) const {
     int cols[4], ks[4];
     shapes(a.d, a.inter, cols, ks);
-    long most = (long)((a.m + 63) / 64) * (a.d / 64) * std::max(plan.kv[0], plan.kv[1]);
+    long most = (long)((a.m + 15) / 16) * (a.d / 64);  // attention slices
+    most = std::max(most, (long)((a.m + 63) / 64) * (a.d / 64) * std::max(plan.kv[0], plan.kv[1]));
     for (int g = 0; g < 4; g++)
         most = std::max(most, (long)(cols[g] / 64) * ((a.m + plan.bm[g] - 1) / plan.bm[g]) * plan.splits[g]);
     // Enough blocks for the largest phase's tasks in one round if they fit (a multiple of 8, so
@@ -374,17 +404,28 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
     // Every layer's GEMMs pass the per-step launcher's checks (the kernel builds the same ones).
     int cols[4], ks[4];
     shapes(a.d, a.inter, cols, ks);
+    if (!a.x_in || !a.xa || !a.qa || !a.oa || !a.mid || ((uintptr_t)a.x_in % 16) ||
+        a.x_stride < (size_t)a.m * a.d || a.q_stride < (size_t)a.m * 3 * a.d ||
+        a.o_stride < (size_t)a.m * a.d || a.x_stride % 64 || a.q_stride % 64 || a.o_stride % 64)
+        fail("bad activation buffers");
     for (int li = 0; li < a.count; li++) {
-        const LayerDesc& L = a.host_layers[a.first + li];
+        const int l = a.first + li;
+        const LayerDesc& L = a.host_layers[l];
+        jh_half* x_in = l == a.first ? const_cast<jh_half*>(a.x_in) : a.xa + (2 * l - 1) * a.x_stride;
+        jh_half* x_attn = a.xa + 2 * l * a.x_stride;
+        jh_half* x_out = a.xa + (2 * l + 1) * a.x_stride;
+        jh_half* qkv = a.qa + l * a.q_stride;
+        jh_half* o = a.oa + l * a.o_stride;
+        if (x_out == a.x_in || x_attn == a.x_in) fail("x_in is one of the launch's own buffers");
         Gemm g[4] = {};
         const bool ln0 = L.qkv_colsum != nullptr;
-        g[0].epi = ln0 ? EPI_K_LNROPE : EPI_K_ROPE, g[0].a = a.x, g[0].w = L.wqkv, g[0].c = a.qkv;
+        g[0].epi = ln0 ? EPI_K_LNROPE : EPI_K_ROPE, g[0].a = x_in, g[0].w = L.wqkv, g[0].c = qkv;
         g[0].rope = L.rope, g[0].rope_rows = a.rope_rows;
         if (ln0) g[0].stats_in = a.stats_mlp, g[0].colsum = L.qkv_colsum;
-        g[1].epi = EPI_K_RESSTATS, g[1].a = a.o, g[1].w = L.wo, g[1].c = a.x, g[1].stats_out = a.stats_attn;
-        g[2].epi = EPI_K_LNGEGLU, g[2].a = a.x, g[2].w = L.wi, g[2].c = a.mid;
+        g[1].epi = EPI_K_RESSTATS, g[1].a = o, g[1].w = L.wo, g[1].c = x_attn, g[1].stats_out = a.stats_attn;
+        g[2].epi = EPI_K_LNGEGLU, g[2].a = x_attn, g[2].w = L.wi, g[2].c = a.mid;
         g[2].stats_in = a.stats_attn, g[2].colsum = L.wi_colsum;
-        g[3].epi = EPI_K_RESSTATS, g[3].a = a.mid, g[3].w = L.wo_mlp, g[3].c = a.x, g[3].stats_out = a.stats_mlp;
+        g[3].epi = EPI_K_RESSTATS, g[3].a = a.mid, g[3].w = L.wo_mlp, g[3].c = x_out, g[3].stats_out = a.stats_mlp;
         for (int i = 0; i < 4; i++) {
             g[i].m = a.m, g[i].n = cols[i], g[i].k = ks[i], g[i].eps = a.eps;
             gemm_check(g[i], GemmConfig{plan.bm[i], plan.splits[i]}, s);
@@ -397,7 +438,8 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
 
     EncParams P{};
     P.layers = a.layers, P.first = a.first, P.count = a.count;
-    P.x = a.x, P.qkv = a.qkv, P.o = a.o, P.mid = a.mid;
+    P.x_in = a.x_in, P.xa = a.xa, P.qa = a.qa, P.oa = a.oa, P.mid = a.mid;
+    P.x_stride = a.x_stride, P.q_stride = a.q_stride, P.o_stride = a.o_stride;
     P.stats_attn = a.stats_attn, P.stats_mlp = a.stats_mlp;
     P.m = a.m, P.d = a.d, P.inter = a.inter, P.rope_rows = a.rope_rows, P.eps = a.eps;
     for (int g = 0; g < 4; g++) P.bm[g] = plan.bm[g], P.splits[g] = plan.splits[g];
@@ -409,8 +451,8 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
         if (((phases >> ph) & 1) && ((phases >> (ph - 1)) & 1)) barriers++;
     P.barriers = barriers * a.count + (a.count - 1);
     P.lds_main = lds;
-    P.att_gmax[0] = attention_gmax(a.m, 0);
-    P.att_gmax[1] = attention_gmax(a.m, window);
+    P.att_gkeys[0] = attention_gkeys(a.m, 0);
+    P.att_gkeys[1] = attention_gkeys(a.m, window);
     P.bar = bar_;
     P.prof = prof;
 

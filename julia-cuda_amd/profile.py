@@ -45,6 +45,14 @@ def summarize(stamps):
             if len(nst):
                 row["handover_us"] = (nst.min() - en.max()) * TICK_US
                 row["barrier_wait_us"] = float(np.mean(nst - s[ok, 2 * p + 1][: len(nst)])) * TICK_US
+        if name == "attention":
+            sub = s[:, 12:15]
+            okb = ok & (sub > 0).all(axis=1)
+            if okb.any():
+                d = np.diff(np.concatenate([s[okb, 2 * p][:, None], sub[okb]], axis=1), axis=1)
+                for k, name_ in enumerate(("inputs_us", "compute_us", "store_us")):
+                    row[name_] = float(np.mean(d[:, k])) * TICK_US
+                    row["max_" + name_] = float(np.max(d[:, k])) * TICK_US
         g = {"qkv": 0, "wo": 1, "wi": 2, "wo_mlp": 3}.get(name)
         if g is not None:
             sub = s[:, 16 + 4 * g: 20 + 4 * g]
