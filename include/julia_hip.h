@@ -219,6 +219,17 @@ int julia_hip_time_encoder_step(const Engine *e, int step, int m, int bm, int sp
  * stamps holds max_rows rows of 32. */
 int julia_hip_profile_layer(const Engine *e, int n, int layer, const int *plan, uint64_t *stamps,
                             int max_rows, int *grid, int *plan_out, char *err, size_t err_len);
+/* Config 5's batched variant (the reference runs one request at a time): b requests' ids
+ * concatenated (lens[i] each, at most max_length; the sum at most the engine's rows, which the
+ * model spec's batch_rows raises) through embed and the encoder as one set of rows: positions
+ * restart at 0 in every request and attention stays within each request (and its window).
+ * x_out (nullable) receives the residual stream after the last layer, [rows][d] f16 bits;
+ * gpu_ms the GPU time from embed to the encoder's end (HIP events). No head: the batched
+ * variant measures the encoder. */
+int julia_hip_encode_batch(const Engine *e, size_t b, const uint32_t *ids, const size_t *lens,
+                           int layer_fused, uint16_t *x_out, float *gpu_ms, char *err,
+                           size_t err_len);
+
 /* One request with the residual stream copied out after every encoder layer (x_trace, f16 bits
  * [layers][n][d], nullable) and the head's stream after its last layer (head_x, [n][d],
  * nullable): for step-by-step parity checks. */

@@ -70,7 +70,7 @@ int attention_chunks(int n, int d, int window, int cus) {
 }
 
 void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, int chunks,
-                      const Scratch& s, hipStream_t st) {
+                      const Scratch& s, hipStream_t st, const int32_t* seg) {
     auto fail = [](const std::string& m) { throw std::runtime_error("attention: " + m); };
     if (n <= 0) fail("no rows");
     if (d <= 0 || d % 64) fail("d = " + std::to_string(d) + " is not a multiple of 64");
@@ -80,7 +80,9 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
     if (chunks > 1 && (attention_ws_floats(n, d, chunks) > s.ws_floats ||
                        attention_counters(n, d) > s.n_counters || !s.ws || !s.counters))
         fail("the key-range scratch is too small for " + std::to_string(n) + " tokens");
-    AttnParams p{qkv, o, n, d, window, chunks, s.ws, s.counters};
+    if (seg && chunks != 1) fail("concatenated sequences take one key range");
+    if (seg && ((uintptr_t)seg % 8)) fail("seg must be 8-byte aligned");
+    AttnParams p{qkv, o, n, d, window, chunks, s.ws, s.counters, seg};
     if (chunks == 1) {
         if (!attention_prepare()) fail("the LDS-resident kernel cannot have its LDS");
         const int gkeys = attention_gkeys(n, window);

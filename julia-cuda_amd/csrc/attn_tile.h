@@ -244,10 +244,13 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
     char* ks = lds + 2048;
     char* vs = ks + gkeys * 128;
 
-    int k0 = 0, k1 = n;
+    // The keys any of the 16 queries may see: their sequences' rows (all n rows, or from the
+    // first query's sequence start to the last query's sequence end), cut to the window.
+    const int qlast = min(q0 + 15, n - 1);
+    int k0 = p.seg ? p.seg[2 * q0] : 0, k1 = p.seg ? p.seg[2 * qlast + 1] : n;
     if (p.window > 0) {
-        k0 = max(q0 - p.window, 0);
-        k1 = min(q0 + 16 + p.window, n);
+        k0 = max(k0, q0 - p.window);
+        k1 = min(k1, q0 + 16 + p.window);
     }
     k0 &= ~31;
 
@@ -263,6 +266,14 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
     };
 
     const int qi = q0 + r16;  // this lane's query (the same 16 in every wave)
+    // Its own sequence's rows (keys outside are masked), and whether all 16 queries share one.
+    int slo = 0, shi = n;
+    if (p.seg) {
+        const int qc = min(qi, n - 1);
+        slo = p.seg[2 * qc], shi = p.seg[2 * qc + 1];
+    }
+    const bool one_seq = !p.seg || p.seg[2 * q0] == p.seg[2 * qlast];
+    const int ulo = p.seg ? p.seg[2 * q0] : 0, uhi = p.seg ? p.seg[2 * qlast + 1] : n;  // uniform
     const float scale = 1.4426950408889634f / 8.0f;  // log2(e) / sqrt(64)
     float mx = -INFINITY, lsum = 0.0f;
     floatx4 oacc[4];
@@ -309,8 +320,9 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
 #pragma unroll
                 for (int k2 = 0; k2 < 2; k2++) sc[t] = mfma16(kf[t][k2], qf[k2], sc[t]);
             }
-            // A step inside the sequence and, for all 16 queries, inside the window needs no mask.
-            const bool full = kb + 32 <= n &&
+            // A step inside the queries' one sequence and, for all 16, inside the window needs no
+            // mask.
+            const bool full = one_seq && kb >= ulo && kb + 32 <= uhi &&
                               (p.window == 0 || (q0 + 15 - kb <= p.window && kb + 31 - q0 <= p.window));
             float bm = -INFINITY;
             if (full) {
@@ -328,7 +340,7 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
                     for (int e = 0; e < 4; e++) {
                         const int key = kb + 16 * t + 4 * g + e;
                         const int dist = qi > key ? qi - key : key - qi;
-                        const bool ok = key < n && (p.window == 0 || dist <= p.window);
+                        const bool ok = key >= slo && key < shi && (p.window == 0 || dist <= p.window);
                         sc[t][e] = ok ? sc[t][e] * scale : -INFINITY;
                         bm = fmaxf(bm, sc[t][e]);
                     }

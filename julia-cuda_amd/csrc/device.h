@@ -11,6 +11,7 @@ typedef _Float16 f16;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 namespace jh {
 
@@ -238,8 +239,9 @@ constexpr int EPI_PRE_SLOTS = 2;
 struct EpiCol {  // per column: colsum (LN) and bias, lo and hi halves
     float4 cs[2], bs[2];
 };
-struct EpiRow {  // per row: statistics slots, RoPE (cos, sin) pairs, residual lo and hi
+struct EpiRow {  // per row: statistics slots, position, RoPE (cos, sin) pairs, residual lo, hi
     float2 st[EPI_PRE_SLOTS];
+    int pos;
     float4 rt[2];
     half4 rl, rh;
 };
@@ -268,16 +270,23 @@ __device__ __forceinline__ void epi_load_row(const GemmParams& p, int row, int g
 #pragma unroll
         for (int i = 0; i < EPI_PRE_SLOTS; i++) e.st[i] = load8f<XS>(st + 2 * min(j + 8 * i, slots - 1));
     }
-    if (EPI & EPI_ROPE) {
-        const int pos = min(p.pos ? max(p.pos[r], 0) : r, p.rope_rows - 1);
-        const float4* t = (const float4*)(p.rope + ((size_t)pos * 32 + c0) * 2);
-        e.rt[0] = t[0];
-        e.rt[1] = t[1];
-    }
+    if (EPI & EPI_ROPE) e.pos = p.pos ? p.pos[r] : r;
     if ((EPI & EPI_RES) && !(EPI & EPI_GEGLU)) {
         const f16* x = (const f16*)(p.res ? p.res : p.c) + (size_t)r * p.n + grp * 64 + c0;
         e.rl = load8h<XR>(x);
         e.rh = load8h<XR>(x + 32);
+    }
+}
+
+// The RoPE table row of e.pos (set by epi_load_row): a separate step, so that a tile issues every
+// row's position load before any table load (which waits for its position).
+template <int EPI>
+__device__ __forceinline__ void epi_load_rope(const GemmParams& p, int c0, EpiRow& e) {
+    if (EPI & EPI_ROPE) {
+        const int pos = min(max(e.pos, 0), p.rope_rows - 1);
+        const float4* t = (const float4*)(p.rope + ((size_t)pos * 32 + c0) * 2);
+        e.rt[0] = t[0];
+        e.rt[1] = t[1];
     }
 }
 

@@ -51,6 +51,11 @@ struct Engine {
     float* w32 = nullptr;
     size_t n16 = 0, n32 = 0;
     int max_length = 0;
+    int rows = 0;  // activation rows: max_length, or more for concatenated requests (batch_rows)
+    // The batched encoder's inputs: ids, each row's position in its request and its request's
+    // rows (first, one past last).
+    uint32_t* bids_d = nullptr;
+    int32_t *pos_d = nullptr, *seg_d = nullptr;
     // Activations for max_length rows.
     jh_half *x = nullptr, *qkv = nullptr, *o = nullptr, *mid = nullptr, *hx = nullptr;
     float *stats_a = nullptr, *stats_b = nullptr;
@@ -91,7 +96,7 @@ struct Engine {
                         (void*)hx, (void*)stats_a, (void*)stats_b, (void*)ids_d,
                         (void*)markers_d, (void*)logits_d, (void*)scratch.ws,
                         (void*)scratch.counters, (void*)layers_d, (void*)xa, (void*)qa,
-                        (void*)oa})
+                        (void*)oa, (void*)bids_d, (void*)pos_d, (void*)seg_d})
             if (p) hipFree(p);
         if (ids_h) hipHostFree(ids_h);
         if (markers_h) hipHostFree(markers_h);
@@ -102,30 +107,32 @@ struct Engine {
     // ---- the encoder (src/forward.rs GpuEncoder) -------------------------------------------
     void gemm(int epi, const jh_half* a, const jh_half* w, jh_half* c, int m, int n, int k,
               const float* stats_in, const float* colsum, float eps, const float* bias,
-              const float* rope, float* stats_out) {
+              const float* rope, float* stats_out, const int32_t* pos = nullptr) {
         Gemm g{};
         g.epi = epi, g.a = a, g.w = w, g.c = c, g.m = m, g.n = n, g.k = k;
         g.stats_in = stats_in, g.colsum = colsum, g.eps = eps, g.bias = bias;
-        g.rope = rope, g.pos = nullptr, g.rope_rows = cfg.max_positions, g.stats_out = stats_out;
+        g.rope = rope, g.pos = pos, g.rope_rows = cfg.max_positions, g.stats_out = stats_out;
         gemm_launch(g, gemm_choose(m, n, k, cus), scratch, stream);
     }
 
     // Layer l's five steps as five launches (src/forward.rs:105-165, 361-424): qkv (RoPE; the
     // LayerNorm folded in from layer 1, from the statistics wo_mlp left in stats_b), attention,
     // wo (+ residual, statistics into stats_a), wi (LayerNorm from stats_a, GeGLU), wo_mlp
-    // (+ residual, statistics into stats_b).
-    void launch_layer(int l, int n) {
+    // (+ residual, statistics into stats_b). pos and seg (nullable): concatenated requests' row
+    // positions and sequence bounds.
+    void launch_layer(int l, int n, const int32_t* pos = nullptr, const int32_t* seg = nullptr) {
         const EncoderLayer& L = layout.layers[l];
         const int d = cfg.d, I = cfg.inter;
         const float* rope = f(L.global ? layout.rope_global : layout.rope_local);
         if (L.qkv_colsum.present)
             gemm(EPI_K_LNROPE, x, h(L.wqkv), qkv, n, 3 * d, d, stats_b, f(L.qkv_colsum),
-                 cfg.norm_eps, nullptr, rope, nullptr);
+                 cfg.norm_eps, nullptr, rope, nullptr, pos);
         else
             gemm(EPI_K_ROPE, x, h(L.wqkv), qkv, n, 3 * d, d, nullptr, nullptr, 0.0f, nullptr, rope,
-                 nullptr);
+                 nullptr, pos);
         const int window = L.global ? 0 : cfg.window;
-        attention_launch(qkv, o, n, d, window, attention_chunks(n, d, window, cus), scratch, stream);
+        attention_launch(qkv, o, n, d, window, attention_chunks(n, d, window, cus), scratch, stream,
+                         seg);
         gemm(EPI_K_RESSTATS, o, h(L.wo), x, n, d, d, nullptr, nullptr, 0.0f, nullptr, nullptr, stats_a);
         gemm(EPI_K_LNGEGLU, x, h(L.wi), mid, n, 2 * I, d, stats_a, f(L.wi_colsum), cfg.norm_eps,
              nullptr, nullptr, nullptr);
@@ -135,9 +142,11 @@ struct Engine {
 
     // The persistent encoder kernel: layers [first, first + count) as one cooperative launch,
     // from the residual stream in x_in.
-    LayerArgs layer_args(int first, int count, int n, const jh_half* x_in) const {
+    LayerArgs layer_args(int first, int count, int n, const jh_half* x_in,
+                         const int32_t* pos = nullptr, const int32_t* seg = nullptr) const {
         LayerArgs a{};
-        const size_t ml = (size_t)max_length, d = cfg.d;
+        const size_t ml = (size_t)rows, d = cfg.d;
+        a.pos = pos, a.seg = seg;
         a.x_in = x_in, a.xa = xa, a.qa = qa, a.oa = oa, a.mid = mid;
         a.x_stride = ml * d, a.q_stride = ml * 3 * d, a.o_stride = ml * d;
         a.stats_attn = stats_a, a.stats_mlp = stats_b;
@@ -148,8 +157,9 @@ struct Engine {
     }
 
     // Returns where the residual stream is after the launch.
-    const jh_half* launch_encoder_fused(int first, int count, int n, const jh_half* x_in) {
-        const LayerArgs a = layer_args(first, count, n, x_in);
+    const jh_half* launch_encoder_fused(int first, int count, int n, const jh_half* x_in,
+                                        const int32_t* pos = nullptr, const int32_t* seg = nullptr) {
+        const LayerArgs a = layer_args(first, count, n, x_in, pos, seg);
         layer_kernel.launch(a, layer_kernel.default_plan(n, cfg.d, cfg.inter), scratch, stream);
         return LayerKernel::x_out(a);
     }
@@ -250,6 +260,7 @@ Engine* load_engine(const char* dir, size_t max_length) {
         throw std::runtime_error("max_length " + std::to_string(ml) + " is over the model's " +
                                  std::to_string(c.max_positions));
     e->max_length = (int)ml;
+    e->rows = (int)std::max<size_t>(ml, (size_t)c.batch_rows);
     HostWeights hw = prepare_synthetic(c);
     e->layout = hw.layout;
     e->n16 = hw.f16.size(), e->n32 = hw.f32.size();
@@ -259,7 +270,7 @@ Engine* load_engine(const char* dir, size_t max_length) {
     hip_check(hipMemcpy(e->w16, hw.f16.data(), e->n16 * 2, hipMemcpyHostToDevice), "upload");
     hip_check(hipMemcpy(e->w32, hw.f32.data(), e->n32 * 4, hipMemcpyHostToDevice), "upload");
 
-    const size_t n = ml, d = c.d, wide = std::max<size_t>(c.inter, c.head_ff);
+    const size_t n = e->rows, d = c.d, wide = std::max<size_t>(c.inter, c.head_ff);
     e->x = dalloc<jh_half>(n * d, "x");
     e->qkv = dalloc<jh_half>(n * 3 * d, "qkv");
     e->o = dalloc<jh_half>(n * d, "o");
@@ -267,15 +278,18 @@ Engine* load_engine(const char* dir, size_t max_length) {
     e->hx = dalloc<jh_half>(n * d, "hx");
     e->stats_a = dalloc<float>(n * (d / 64) * 2, "stats");
     e->stats_b = dalloc<float>(n * (d / 64) * 2, "stats");
-    e->ids_d = dalloc<uint32_t>(QUEUE * n, "ids");
-    e->markers_d = dalloc<uint32_t>(QUEUE * n, "markers");
-    e->logits_d = dalloc<float>(QUEUE * n, "logits");
-    e->gin = dalloc<uint32_t>(2 * n, "graph input");
-    e->glogits = dalloc<float>(n, "graph logits");
+    e->ids_d = dalloc<uint32_t>(QUEUE * ml, "ids");
+    e->markers_d = dalloc<uint32_t>(QUEUE * ml, "markers");
+    e->logits_d = dalloc<float>(QUEUE * ml, "logits");
+    e->gin = dalloc<uint32_t>(2 * ml, "graph input");
+    e->glogits = dalloc<float>(ml, "graph logits");
+    e->bids_d = dalloc<uint32_t>(n, "batch ids");
+    e->pos_d = dalloc<int32_t>(n, "batch positions");
+    e->seg_d = dalloc<int32_t>(2 * n, "batch sequences");
     if (const char* g = getenv("JULIA_HIP_GRAPHS")) e->use_graphs = strcmp(g, "0") != 0;
-    hip_check(hipHostMalloc((void**)&e->ids_h, QUEUE * n * 4, hipHostMallocDefault), "pinned ids");
-    hip_check(hipHostMalloc((void**)&e->markers_h, QUEUE * n * 4, hipHostMallocDefault), "pinned markers");
-    hip_check(hipHostMalloc((void**)&e->logits_h, QUEUE * n * 4, hipHostMallocDefault), "pinned logits");
+    hip_check(hipHostMalloc((void**)&e->ids_h, QUEUE * ml * 4, hipHostMallocDefault), "pinned ids");
+    hip_check(hipHostMalloc((void**)&e->markers_h, QUEUE * ml * 4, hipHostMallocDefault), "pinned markers");
+    hip_check(hipHostMalloc((void**)&e->logits_h, QUEUE * ml * 4, hipHostMallocDefault), "pinned logits");
     for (int i = 0; i < QUEUE; i++) {
         hip_check(hipEventCreate(&e->ev_start[i]), "hipEventCreate");
         hip_check(hipEventCreate(&e->ev_end[i]), "hipEventCreate");
@@ -285,7 +299,7 @@ Engine* load_engine(const char* dir, size_t max_length) {
     size_t ws = 0, counters = 0;
     const int shapes[][2] = {{3 * (int)d, (int)d}, {(int)d, (int)d},  {2 * c.inter, (int)d},
                              {(int)d, c.inter},     {c.head_ff, (int)d}, {(int)d, c.head_ff}};
-    for (int m = 1; m <= (int)ml; m++) {
+    for (int m = 1; m <= (int)n; m++) {
         for (auto& s : shapes) {
             const GemmConfig cfg = gemm_choose(m, s[0], s[1], e->cus);
             ws = std::max(ws, gemm_ws_floats(m, s[0], cfg));
@@ -312,8 +326,8 @@ Engine* load_engine(const char* dir, size_t max_length) {
                         hipMemcpyHostToDevice), "layer table");
     e->layer_kernel.init(e->cus, (int)prop.sharedMemPerBlock);
     if (!attention_prepare()) throw std::runtime_error("attention: cannot set the kernel's LDS size");
-    ws = std::max(ws, e->layer_kernel.ws_floats((int)ml, (int)d, c.inter));
-    counters = std::max(counters, e->layer_kernel.counters((int)ml, (int)d, c.inter));
+    ws = std::max(ws, e->layer_kernel.ws_floats((int)n, (int)d, c.inter));
+    counters = std::max(counters, e->layer_kernel.counters((int)n, (int)d, c.inter));
     e->scratch.ws = dalloc<float>(ws, "scratch");
     e->scratch.ws_floats = ws;
     counters = (counters + 31) / 32 * 32;  // the barrier's words start on a 128-byte line
@@ -914,6 +928,55 @@ int julia_hip_profile_layer(const Engine* ce, int n, int layer, const int* plan,
             throw;
         }
         hipFree(prof);
+    });
+}
+
+int julia_hip_encode_batch(const Engine* ce, size_t b, const uint32_t* ids, const size_t* lens,
+                           int layer_fused, uint16_t* x_out, float* gpu_ms, char* err,
+                           size_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!ce) throw std::runtime_error("no engine");
+        Engine& e = *const_cast<Engine*>(ce);
+        hip_check(hipSetDevice(e.device), "hipSetDevice");
+        if (b == 0 || !ids || !lens) throw std::runtime_error("no requests");
+        size_t rows = 0;
+        for (size_t i = 0; i < b; i++) {
+            if (lens[i] == 0 || lens[i] > (size_t)e.max_length)
+                throw std::runtime_error("sequence " + std::to_string(i) + ": " +
+                                         std::to_string(lens[i]) + " tokens, not 1 to " +
+                                         std::to_string(e.max_length));
+            rows += lens[i];
+        }
+        if (rows > (size_t)e.rows)
+            throw std::runtime_error(std::to_string(rows) + " rows are over the engine's " +
+                                     std::to_string(e.rows) + " (load with batch_rows)");
+        for (size_t j = 0; j < rows; j++)
+            if (ids[j] >= (uint32_t)e.cfg.vocab)
+                throw std::runtime_error("token id " + std::to_string(ids[j]) + " is past the vocabulary");
+        std::vector<int32_t> pos(rows), seg(2 * rows);
+        for (size_t i = 0, r0 = 0; i < b; r0 += lens[i], i++)
+            for (size_t r = r0; r < r0 + lens[i]; r++) {
+                pos[r] = (int32_t)(r - r0);
+                seg[2 * r] = (int32_t)r0, seg[2 * r + 1] = (int32_t)(r0 + lens[i]);
+            }
+        hip_check(hipMemcpy(e.bids_d, ids, rows * 4, hipMemcpyHostToDevice), "ids");
+        hip_check(hipMemcpy(e.pos_d, pos.data(), rows * 4, hipMemcpyHostToDevice), "positions");
+        hip_check(hipMemcpy(e.seg_d, seg.data(), rows * 8, hipMemcpyHostToDevice), "sequences");
+        const int n = (int)rows;
+        hip_check(hipEventRecord(e.ev_start[0], e.stream), "hipEventRecord");
+        embed_launch(e.bids_d, n, e.h(e.layout.tok_embeddings), e.cfg.vocab, e.cfg.d,
+                     e.f(e.layout.emb_norm), e.cfg.norm_eps, e.x, e.stream);
+        const jh_half* xf = e.x;
+        if (layer_fused)
+            xf = e.launch_encoder_fused(0, e.cfg.layers, n, e.x, e.pos_d, e.seg_d);
+        else
+            for (int l = 0; l < e.cfg.layers; l++) e.launch_layer(l, n, e.pos_d, e.seg_d);
+        hip_check(hipEventRecord(e.ev_end[0], e.stream), "hipEventRecord");
+        hip_check(hipStreamSynchronize(e.stream), "the batched encoder");
+        if (layer_fused && e.layer_kernel.barrier_timed_out())
+            throw std::runtime_error("layer: a grid barrier timed out (blocks not co-resident)");
+        if (gpu_ms) hip_check(hipEventElapsedTime(gpu_ms, e.ev_start[0], e.ev_end[0]), "hipEventElapsedTime");
+        if (x_out) hip_check(hipMemcpy(x_out, xf, rows * e.cfg.d * 2, hipMemcpyDeviceToHost), "x");
     });
 }
 

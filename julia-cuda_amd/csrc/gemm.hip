@@ -9,15 +9,16 @@
 //    reduce their partial tiles through LDS, so a tile's serial K loop is a quarter as long and
 //    there are more tiles to spread over 256 CUs. Grid split-K on top is deterministic: the
 //    last block of a tile to arrive sums every split's partial in split order.
-//  - gemm_tput (BM = 128/256 x 128): the MFMA-bound regime (M >= 2048): a and w tiles staged
-//    through swizzled LDS, double-buffered, four waves each owning a 64 x 64 (or 128 x 64)
-//    output block.
+//  - gemm_big (BM = 128/256 x 128): the MFMA-bound regime (M >= 2048): a and w tiles copied
+//    into three LDS stages by direct global -> LDS loads (gemm_big.h), four waves each owning a
+//    64 x 64 (or 128 x 64) output block.
 //
 // Both hand the finished f32 tile to jh::epilogue (device.h) with the same thread layout.
 #include <algorithm>
 #include <stdexcept>
 #include <string>
 
+#include "gemm_big.h"
 #include "gemm_tile.h"
 
 namespace jh {
@@ -32,146 +33,13 @@ __global__ __launch_bounds__(256) void gemm_lat(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// gemm_tput: BM x 128 tiles (BM = 128 or 256), BK = 64, 4 waves in a 2 x 2 grid, each owning
-// (BM/2) x 64 of the output. a and w tiles go global -> registers -> LDS, two stages; the next
-// stage's global loads are in flight while the current one feeds the MFMAs.
-//
-// a tile rows are 64 f16 (128 B) as eight 16-B chunks; chunk c of row r is stored at chunk
-// c ^ (r & 7), so the 16 rows one fragment load reads spread over all banks. w arrives in
-// fragment order and stays so in LDS: a lane's fragment is 16 contiguous bytes.
-template <int BM>
-struct Tput {
-    static constexpr int BN = 128, BK = 64;
-    static constexpr int A_CH = BM * 8, W_CH = BN * 8;  // 16-B chunks per stage
-    static constexpr int A_PER = A_CH / 256, W_PER = W_CH / 256;
-    static constexpr int WM = BM / 2, MI = WM / 16;     // wave rows, m fragments per wave
-    static constexpr int STAGE = (BM + BN) * BK;        // f16 per stage
-};
-
-__device__ __forceinline__ int swz(int r, int c) { return r * 64 + ((c ^ (r & 7)) << 3); }
-
+// gemm_big: BM x 128 tiles (BM = 128 or 256) for large M; see gemm_big.h. Dynamic LDS:
+// Big<BM>::LDS_BYTES.
 template <int BM, int EPI>
-__global__ __launch_bounds__(256) void gemm_tput(GemmParams p) {
-    using C = Tput<BM>;
-    constexpr int NPASS = BM / 32;  // epilogue passes per 64-column group
-    // Two stages of f16 tiles; reused for the f32 output, one 64-column group (BM x 68) at a time.
-    constexpr int LDS_F16 = 2 * C::STAGE;
-    constexpr int OUT_F32 = BM * 68;
-    constexpr int LDS_BYTES = (LDS_F16 * 2 > OUT_F32 * 4) ? LDS_F16 * 2 : OUT_F32 * 4;
-    __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
+__global__ __launch_bounds__(256) void gemm_big(GemmParams p) {
+    extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
     __shared__ uint32_t s_last;
-    f16* sm = (f16*)smem;
-
-    const int T = p.tiles_n * p.tiles_m * p.splits;
-    const int L = xcd_task(blockIdx.x, T);
-    const int z = L % p.splits, t2 = L / p.splits;
-    const int by = t2 % p.tiles_m, bx = t2 / p.tiles_m;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g = l >> 4;
-    const int wm = w >> 1, wn = w & 1;
-
-    const int KT = p.k / C::BK;  // host checks k % 64 == 0 for this kernel
-    const int kt0 = z * KT / p.splits, kt1 = (z + 1) * KT / p.splits;
-
-    // Global chunk assignment: chunk q = tid + 256 h -> row q / 8, chunk q % 8.
-    const f16* ag[C::A_PER];
-    const f16* wg[C::W_PER];
-#pragma unroll
-    for (int h = 0; h < C::A_PER; h++) {
-        const int q = tid + 256 * h, r = q >> 3;
-        ag[h] = (const f16*)p.a + (size_t)min(by * BM + r, p.m - 1) * p.k + (q & 7) * 8;
-    }
-    // w in fragment order: the stage's four 2048-value blocks (64-row group 2 bx + h / 2, K unit
-    // 2 kt + h % 2) are copied as they are; thread tid takes value tid * 8 of each.
-    const int U = p.k >> 5;
-#pragma unroll
-    for (int h = 0; h < C::W_PER; h++)
-        wg[h] = (const f16*)p.w + ((size_t)(2 * bx + (h >> 1)) * U + (h & 1)) * 2048 + tid * 8;
-    half8 ra[C::A_PER], rw[C::W_PER];
-    auto gload = [&](int kt) {
-#pragma unroll
-        for (int h = 0; h < C::A_PER; h++) ra[h] = *(const half8*)(ag[h] + kt * C::BK);
-#pragma unroll
-        for (int h = 0; h < C::W_PER; h++) rw[h] = *(const half8*)(wg[h] + (size_t)kt * 4096);
-    };
-    auto lstore = [&](int stage) {
-        f16* as = sm + stage * C::STAGE;
-        f16* ws = as + BM * C::BK;
-#pragma unroll
-        for (int h = 0; h < C::A_PER; h++) {
-            const int q = tid + 256 * h;
-            *(half8*)(as + swz(q >> 3, q & 7)) = ra[h];
-        }
-#pragma unroll
-        for (int h = 0; h < C::W_PER; h++) *(half8*)(ws + h * 2048 + tid * 8) = rw[h];
-    };
-
-    floatx4 acc[C::MI][4];
-#pragma unroll
-    for (int i = 0; i < C::MI; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    if (kt0 < kt1) {
-        gload(kt0);
-        lstore(0);
-    }
-    __syncthreads();
-    for (int kt = kt0; kt < kt1; kt++) {
-        const int cur = (kt - kt0) & 1;
-        if (kt + 1 < kt1) gload(kt + 1);
-        const f16* as = sm + cur * C::STAGE;
-        const f16* ws = as + BM * C::BK;
-#pragma unroll
-        for (int s = 0; s < 2; s++) {  // two K-32 steps per stage; lane group g takes chunk 4s+g
-            half8 fa[C::MI], fw[4];
-#pragma unroll
-            for (int i = 0; i < C::MI; i++)
-                fa[i] = *(const half8*)(as + swz(wm * C::WM + 16 * i + r16, 4 * s + g));
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                fw[j] = *(const half8*)(ws + (wn * 2 + s) * 2048 + (j * 64 + l) * 8);
-#pragma unroll
-            for (int i = 0; i < C::MI; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = mfma16(fw[j], fa[i], acc[i][j]);
-        }
-        if (kt + 1 < kt1) lstore(cur ^ 1);
-        __syncthreads();
-    }
-
-    // The output through LDS (f32, rows of 64 + 4 pad), one 64-column group (the waves with
-    // wn == grp) at a time, into the epilogue layout.
-    float* out = (float*)smem;
-    const int c0 = (tid & 7) * 4;
-#pragma unroll
-    for (int grp = 0; grp < 2; grp++) {
-        if (wn == grp) {
-#pragma unroll
-            for (int i = 0; i < C::MI; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    *(floatx4*)&out[(wm * C::WM + 16 * i + r16) * 68 + 16 * j + 4 * g] = acc[i][j];
-        }
-        EpiCol ec;
-        EpiRow er[NPASS];
-        epi_load_col<EPI>(p, bx * 2 + grp, c0, ec);
-#pragma unroll
-        for (int ps = 0; ps < NPASS; ps++)
-            epi_load_row<EPI, false>(p, by * BM + ps * 32 + (tid >> 3), bx * 2 + grp, c0, er[ps]);
-        __syncthreads();
-        float v[NPASS][8];
-#pragma unroll
-        for (int ps = 0; ps < NPASS; ps++) {
-            const float* src = &out[(ps * 32 + (tid >> 3)) * 68 + c0];
-            const float4 lo = *(const float4*)src, hi = *(const float4*)(src + 32);
-            v[ps][0] = lo.x, v[ps][1] = lo.y, v[ps][2] = lo.z, v[ps][3] = lo.w;
-            v[ps][4] = hi.x, v[ps][5] = hi.y, v[ps][6] = hi.z, v[ps][7] = hi.w;
-        }
-        __syncthreads();  // every thread has read the group before the next one is written
-        // Each 64-column group is its own split-K "tile" (two per block).
-        finish<NPASS, EPI>(p, v, (bx * p.tiles_m + by) * 2 + grp, z, by * BM, bx * 2 + grp, BM,
-                           &s_last, ec, er);
-    }
+    gemm_big_tile<BM, EPI, false, false>(p, blockIdx.x, lds_dyn, &s_last);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -245,10 +113,16 @@ void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
 template <int BM, int EPI>
 static void launch_one(const GemmParams& p, hipStream_t st) {
     const int blocks = p.tiles_n * p.tiles_m * p.splits;
-    if (BM >= 128)
-        hipLaunchKernelGGL((gemm_tput<BM >= 128 ? BM : 128, EPI>), dim3(blocks), dim3(256), 0, st, p);
-    else
+    if (BM >= 128) {
+        constexpr int B = BM >= 128 ? BM : 128;
+        static const bool lds_ok =  // once per instantiation, before its first launch
+            hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_big<B, EPI>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, Big<B>::LDS_BYTES) == hipSuccess;
+        if (!lds_ok) throw std::runtime_error("gemm: the throughput kernel cannot have its LDS");
+        hipLaunchKernelGGL((gemm_big<B, EPI>), dim3(blocks), dim3(256), Big<B>::LDS_BYTES, st, p);
+    } else {
         hipLaunchKernelGGL((gemm_lat<BM < 128 ? BM : 64, EPI>), dim3(blocks), dim3(256), 0, st, p);
+    }
 }
 
 template <int EPI>

@@ -113,6 +113,8 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     epi_load_col<EPI>(p, bx, c0, ec);
 #pragma unroll
     for (int ps = 0; ps < NPASS; ps++) epi_load_row<EPI, XG>(p, by * BM + ps * 32 + (tid >> 3), bx, c0, er[ps]);
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, c0, er[ps]);
 
     floatx4 acc[MI][4];
 #pragma unroll
@@ -254,6 +256,8 @@ __device__ __forceinline__ void gemm_w_tile(const GemmParams& p, int task, char*
     epi_load_col<EPI>(p, bx, c0, ec);
 #pragma unroll
     for (int ps = 0; ps < NPASS; ps++) epi_load_row<EPI, true, false>(p, by * BM + ps * 32 + (tid >> 3), bx, c0, er[ps]);
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, c0, er[ps]);
 
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(p.a, (uint32_t)p.m * (uint32_t)p.k * 2u);
     uint32_t aoff[MI];

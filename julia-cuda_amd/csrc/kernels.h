@@ -69,6 +69,10 @@ struct AttnParams {
     int chunks;          // key ranges per (64 queries, head) tile
     float* ws;           // key-range partials
     uint32_t* counters;  // one per (query block, head), zero between launches
+    // Concatenated sequences (the batched forward): for each row, the first row of its sequence
+    // and one past its last ([n][2]); keys outside a query's own sequence are masked. Null: one
+    // sequence of n rows.
+    const int32_t* seg;
 };
 
 namespace jh {
@@ -112,7 +116,7 @@ size_t gemm_ws_floats(int m, int n, GemmConfig cfg);
 size_t gemm_counters(int m, int n, GemmConfig cfg);
 
 void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, int chunks,
-                      const Scratch& s, hipStream_t stream);
+                      const Scratch& s, hipStream_t stream, const int32_t* seg = nullptr);
 size_t attention_ws_floats(int n, int d, int chunks);
 size_t attention_counters(int n, int d);
 int attention_chunks(int n, int d, int window, int cus);

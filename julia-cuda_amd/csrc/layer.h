@@ -43,6 +43,9 @@ struct LayerArgs {
     jh_half *xa, *qa, *oa, *mid;
     size_t x_stride, q_stride, o_stride;
     float *stats_attn, *stats_mlp;  // wo writes stats_attn (wi reads it), wo_mlp stats_mlp
+    // Concatenated requests (nullable): each row's position in its request, and its request's
+    // rows [first, one past last] (AttnParams::seg).
+    const int32_t *pos, *seg;
     const LayerDesc* layers;        // device array, indexed by layer
     const LayerDesc* host_layers;   // the same on the host (for the plan and the checks)
     int first, count;               // the layers this launch runs

@@ -32,6 +32,7 @@ struct EncParams {
     jh_half *xa, *qa, *oa, *mid;
     size_t x_stride, q_stride, o_stride;
     float *stats_attn, *stats_mlp;
+    const int32_t *pos, *seg;
     int m, d, inter, rope_rows;
     float eps;
     int bm[4], splits[4], kv[2];
@@ -131,7 +132,7 @@ __device__ __forceinline__ GemmParams make_gemm(const EncParams& P, int g, const
     if (g == 0) {
         p.a = x_in_of(P, l), p.w = L.wqkv, p.c = P.qa + (size_t)l * P.q_stride;
         p.n = 3 * P.d, p.k = P.d;
-        p.rope = L.rope, p.rope_cols = 2 * P.d, p.rope_rows = P.rope_rows;
+        p.rope = L.rope, p.rope_cols = 2 * P.d, p.rope_rows = P.rope_rows, p.pos = P.pos;
         if (L.qkv_colsum) p.stats_in = P.stats_mlp, p.colsum = L.qkv_colsum;
     } else if (g == 1) {
         p.a = P.oa + (size_t)l * P.o_stride, p.w = L.wo, p.c = x_attn_of(P, l), p.res = x_in_of(P, l);
@@ -212,7 +213,7 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
             stamp(prof, 2);
             const int chunks = L.window > 0 ? P.kv[1] : P.kv[0];
             const AttnParams at{P.qa + (size_t)l * P.q_stride, P.oa + (size_t)l * P.o_stride,
-                                P.m, P.d, L.window, chunks, P.ws, P.counters};
+                                P.m, P.d, L.window, chunks, P.ws, P.counters, P.seg};
             const int heads = P.d >> 6;
             if (chunks == 1) {  // qkv is this layer's own buffer: read through the caches
                 const int T = ((P.m + 15) >> 4) * heads, gkeys = P.att_gkeys[L.window > 0 ? 1 : 0];
@@ -396,6 +397,9 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
             fail("no such plan: " + plan.str());
     if (plan.kv[0] < 1 || plan.kv[0] > 8 || plan.kv[1] < 1 || plan.kv[1] > 8)
         fail("no such plan: " + plan.str());
+    if (a.seg && (plan.kv[0] != 1 || plan.kv[1] != 1))
+        fail("concatenated sequences take one key range: " + plan.str());
+    if ((a.pos == nullptr) != (a.seg == nullptr)) fail("positions go with sequence bounds");
     int window = 0;
     for (int li = 0; li < a.count; li++) window = std::max(window, a.host_layers[a.first + li].window);
     const int lds = lds_bytes(plan, a.d, a.inter, a.m, window);
@@ -420,7 +424,7 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
         Gemm g[4] = {};
         const bool ln0 = L.qkv_colsum != nullptr;
         g[0].epi = ln0 ? EPI_K_LNROPE : EPI_K_ROPE, g[0].a = x_in, g[0].w = L.wqkv, g[0].c = qkv;
-        g[0].rope = L.rope, g[0].rope_rows = a.rope_rows;
+        g[0].rope = L.rope, g[0].rope_rows = a.rope_rows, g[0].pos = a.pos;
         if (ln0) g[0].stats_in = a.stats_mlp, g[0].colsum = L.qkv_colsum;
         g[1].epi = EPI_K_RESSTATS, g[1].a = o, g[1].w = L.wo, g[1].c = x_attn, g[1].stats_out = a.stats_attn;
         g[2].epi = EPI_K_LNGEGLU, g[2].a = x_attn, g[2].w = L.wi, g[2].c = a.mid;
@@ -441,6 +445,7 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
     P.x_in = a.x_in, P.xa = a.xa, P.qa = a.qa, P.oa = a.oa, P.mid = a.mid;
     P.x_stride = a.x_stride, P.q_stride = a.q_stride, P.o_stride = a.o_stride;
     P.stats_attn = a.stats_attn, P.stats_mlp = a.stats_mlp;
+    P.pos = a.pos, P.seg = a.seg;
     P.m = a.m, P.d = a.d, P.inter = a.inter, P.rope_rows = a.rope_rows, P.eps = a.eps;
     for (int g = 0; g < 4; g++) P.bm[g] = plan.bm[g], P.splits[g] = plan.splits[g];
     P.kv[0] = plan.kv[0], P.kv[1] = plan.kv[1];

@@ -188,6 +188,7 @@ ModelConfig parse_model_spec(const std::string& spec) {
         else if (k == "global_every") c.global_every = (int)x;
         else if (k == "max_positions") c.max_positions = (int)x;
         else if (k == "seed") c.seed = (uint64_t)x;
+        else if (k == "batch_rows") c.batch_rows = (int)x;
         else throw std::runtime_error("unknown model spec key '" + k + "'");
     }
     auto bad = [](const std::string& m) { throw std::runtime_error("model spec: " + m); };
@@ -198,6 +199,7 @@ ModelConfig parse_model_spec(const std::string& spec) {
     if (c.vocab <= 0 || c.head_layers < 0 || c.head_layers > 16 || c.window < 0 ||
         c.global_every <= 0 || c.max_positions <= 0 || c.max_positions > (1 << 20))
         bad("vocab, head_layers, window, global_every or max_positions out of range");
+    if (c.batch_rows < 0 || c.batch_rows > (1 << 20)) bad("batch_rows out of range");
     return c;
 }
 

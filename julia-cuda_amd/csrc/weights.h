@@ -16,6 +16,7 @@ namespace jh {
 struct ModelConfig {
     int d = 768, layers = 22, inter = 1152, vocab = 50368, head_layers = 2, head_ff = 1536;
     int n_qtypes = 3, window = 64, global_every = 3, max_positions = 8192;
+    int batch_rows = 0;  // rows of concatenated requests the engine holds (0: max_length)
     float norm_eps = 1e-5f, head_eps = 1e-5f, theta_global = 160000.0f, theta_local = 10000.0f;
     uint64_t seed = 42;
 };

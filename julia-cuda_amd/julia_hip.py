@@ -86,6 +86,7 @@ EXPORTS = [
     "julia_hip_round_f16", "julia_hip_gemm_choose", "julia_hip_gemm_plan_2080ti",
     "julia_hip_gemm_choose_2080ti", "julia_hip_engine_info_get", "julia_hip_engine_tensor",
     "julia_hip_time_encoder_step", "julia_hip_profile_layer", "julia_hip_run_trace",
+    "julia_hip_encode_batch",
 ]
 
 _VP, _SZ, _I, _F, _CP = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_char_p
@@ -144,6 +145,8 @@ def lib():
                                          _SZ]),
         "julia_hip_run_trace": (_I, [_VP, _VP, _SZ, _VP, _SZ, ctypes.c_uint32, _I, _VP, _VP, _VP,
                                      _CP, _SZ]),
+        "julia_hip_encode_batch": (_I, [_VP, _SZ, _VP, _VP, _I, _VP, ctypes.POINTER(_F), _CP,
+                                        _SZ]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -250,6 +253,19 @@ class Engine:
         _call(lib().julia_hip_time_encoder_step, self.ptr, self.STEPS.get(step, step), m, bm,
               splits, warmup, batches, per_batch, ctypes.byref(mn), ctypes.byref(md))
         return mn.value, md.value
+
+    def encode_batch(self, seqs, layer_fused=False, want_x=True):
+        """Config 5's batched encoder: the id sequences concatenated, positions restarting per
+        sequence, attention within each. Returns (x after the encoder [rows][d] f16 bits or None,
+        GPU ms)."""
+        ids = np.ascontiguousarray(np.concatenate([np.asarray(s, np.uint32) for s in seqs]),
+                                   np.uint32)
+        lens = np.array([len(s) for s in seqs], np.uintp)
+        x = np.empty((len(ids), self.info().d), np.uint16) if want_x else None
+        ms = ctypes.c_float()
+        _call(lib().julia_hip_encode_batch, self.ptr, len(seqs), _np_ptr(ids), _np_ptr(lens),
+              int(layer_fused), _np_ptr(x), ctypes.byref(ms))
+        return x, ms.value
 
     def profile_layer(self, n, layer=1, plan=None):
         """The persistent encoder kernel's per-block phase stamps (src/profile.rs): returns (plan,

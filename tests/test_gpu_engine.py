@@ -151,6 +151,39 @@ def test_run_errors(small):
     assert np.isfinite(out[0]).all()
 
 
+def test_batched_encoder_matches_each_request(torch_cuda):
+    """Config 5's batched variant: requests concatenated into one set of rows,
+    positions restarting in every request and attention kept within each, give every request its
+    own encoder output: against the request run alone (per-step kernels) and against the f32
+    oracle. The batch passes 2048 rows, so the per-step path takes the throughput GEMMs."""
+    c = dict(SMALL, batch_rows=4096)
+    e = jh.Engine(spec(c), max_length=1024)
+    m = O.Model(O.cfg(**SMALL))
+    rng = np.random.default_rng(21)
+    lens = [70, 130, 45, 200, 17, 513, 300, 64, 97, 1, 256, 400, 300]
+    seqs = [rng.integers(0, SMALL["vocab"], n).astype(np.uint32) for n in lens]
+    assert sum(lens) > 2048
+    alone = {i: e.run_trace(seqs[i], [], 0)[1][-1] for i in range(0, len(seqs), 3)}
+    oracle = {i: m.forward(seqs[i], 0, [], trace=True)[1][-1] for i in (1, 5)}
+    for fused in (False, True):
+        x, ms = e.encode_batch(seqs, layer_fused=fused)
+        say(f"batched encoder ({'layer kernel' if fused else 'per-step'}): {sum(lens)} rows, "
+            f"{ms:.3f} GPU ms")
+        assert ms > 0 and x.shape == (sum(lens), SMALL["d"])
+        starts = np.concatenate([[0], np.cumsum(lens)])
+        for i, want in alone.items():
+            got = x[starts[i]:starts[i + 1]]
+            compare(f32(got), f32(want), 1e-2, 5e-2, what=f"request {i} ({lens[i]} rows)")
+        for i, want in oracle.items():
+            got = x[starts[i]:starts[i + 1]]
+            compare(f32(got), want, CHAINED_REL, 1e-1, what=f"request {i} vs oracle")
+    with pytest.raises(jh.JuliaHipError, match="rows are over"):
+        e.encode_batch([seqs[5]] * 8)
+    with pytest.raises(jh.JuliaHipError, match="tokens, not 1 to"):
+        e.encode_batch([np.zeros(1025, np.uint32)])
+    e.close()
+
+
 def test_load_errors(torch_cuda):
     with pytest.raises(jh.JuliaHipError, match="max_length"):
         jh.Engine(spec(dict(SMALL, max_positions=512)), max_length=600)

@@ -38,6 +38,8 @@ def test_load_without_a_gpu_or_model_is_an_error():
         jh.Engine("/some/checkpoint/dir")
     with pytest.raises(jh.JuliaHipError, match="d must be"):
         jh.Engine("synthetic:d=100")
+    with pytest.raises(jh.JuliaHipError, match="batch_rows"):
+        jh.Engine("synthetic:batch_rows=-1")
     if jh.device_count() == 0:
         with pytest.raises(jh.JuliaHipError, match="no HIP device"):
             jh.Engine("synthetic:layers=1")
