@@ -112,8 +112,7 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
                 s[t][e] = ok ? s[t][e] * scale : -INFINITY;
                 bm = fmaxf(bm, s[t][e]);
             }
-        bm = fmaxf(bm, __shfl_xor(bm, 16));
-        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        bm = max_xor32(max_xor16(bm));
         const float mnew = fmaxf(mx, bm);
         const float base = mnew == -INFINITY ? 0.0f : mnew;  // no valid key yet: exp2(-inf) = 0
         const float alpha = exp2f(mx - base);
@@ -191,8 +190,7 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
         }
     }
 
-    float tot = lsum + __shfl_xor(lsum, 16);
-    tot += __shfl_xor(tot, 32);
+    const float tot = sum_xor32(sum_xor16(lsum));
     const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
     if (qi < n) {
         f16* op = (f16*)p.o + (size_t)qi * d + h * 64 + 4 * g;
@@ -345,8 +343,7 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
                         bm = fmaxf(bm, sc[t][e]);
                     }
             }
-            bm = fmaxf(bm, __shfl_xor(bm, 16));
-            bm = fmaxf(bm, __shfl_xor(bm, 32));
+            bm = max_xor32(max_xor16(bm));
             const float mnew = fmaxf(mx, bm);
             const float base = mnew == -INFINITY ? 0.0f : mnew;  // no valid key yet: exp2(-inf) = 0
             const float alpha = exp2f(mx - base);
@@ -379,8 +376,7 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
     }
 
     // The waves' partials (output, max, sum over the query's keys) through LDS; wave 0 merges.
-    float tot = lsum + __shfl_xor(lsum, 16);
-    tot += __shfl_xor(tot, 32);
+    const float tot = sum_xor32(sum_xor16(lsum));
     float* mg = (float*)lds;  // [wave][18][64]
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)

@@ -33,19 +33,51 @@ __device__ __forceinline__ half8 mask16(half8 v, uint32_t keep) {
     return v;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+// v from another lane of the same 16-lane row, by a DPP lane pattern (no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+
+// gfx950's lane swaps, as (lane l's value, lane l ^ 16's value) and (l, l ^ 32) pairs in some
+// order that is the same for both lanes of a pair: v_permlane16_swap exchanges the odd 16-lane
+// rows of one operand with the even rows of the other, v_permlane32_swap the upper half of one
+// with the lower half of the other; with both operands v, the two results hold v of the lower and
+// of the upper partner. A symmetric reduction of the pair needs no lane select.
+struct LanePair {
+    float lo, hi;
+};
+__device__ __forceinline__ LanePair lane_pair16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ LanePair lane_pair32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return {__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ float max_xor16(float v) { const LanePair p = lane_pair16(v); return fmaxf(p.lo, p.hi); }
+__device__ __forceinline__ float max_xor32(float v) { const LanePair p = lane_pair32(v); return fmaxf(p.lo, p.hi); }
+__device__ __forceinline__ float sum_xor16(float v) { const LanePair p = lane_pair16(v); return p.lo + p.hi; }
+__device__ __forceinline__ float sum_xor32(float v) { const LanePair p = lane_pair32(v); return p.lo + p.hi; }
+
+// The sum over each group of `W` consecutive lanes (W a power of two <= 64), to every lane, with
+// no LDS round trip. Within 16 lanes by DPP: quad_perm [1,0,3,2] and [2,3,0,1] (the quad's sum in
+// every lane), the half-row mirror (lane i <- 7 - i: the other quad of 8), the row mirror
+// (i <- 15 - i: the other 8 of 16); then the lane swaps. Every lane of a group gets the same bits
+// (each step adds the same two values in either order).
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "group width");
+    if (W >= 2) v += dpp_move<0xB1>(v);
+    if (W >= 4) v += dpp_move<0x4E>(v);
+    if (W >= 8) v += dpp_move<0x141>(v);
+    if (W >= 16) v += dpp_move<0x140>(v);
+    if (W >= 32) v = sum_xor16(v);
+    if (W >= 64) v = sum_xor32(v);
     return v;
 }
 
-// The sum over each group of `W` consecutive lanes (W a power of two <= 64), to every lane.
-template <int W>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int m = W / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-    return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 
 // GELU(x) = x Phi(x), with erf(x / sqrt 2) from Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7),
 // the approximation the reference uses (kernels/src/gemm.rs:139-150): t = 1 / (1 + p |x| / sqrt 2)
@@ -97,6 +129,18 @@ __device__ __forceinline__ void store8(void* p, float2 v) {
         xstore64(p, u);
     } else {
         *(float2*)p = v;
+    }
+}
+
+template <bool XG>
+__device__ __forceinline__ void store16(void* p, half8 v) {
+    if (XG) {
+        uint64_t u[2];
+        __builtin_memcpy(u, &v, 16);
+        xstore64(p, u[0]);
+        xstore64((char*)p + 8, u[1]);
+    } else {
+        *(half8*)p = v;
     }
 }
 

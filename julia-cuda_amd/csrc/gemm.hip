@@ -9,11 +9,13 @@
 //    reduce their partial tiles through LDS, so a tile's serial K loop is a quarter as long and
 //    there are more tiles to spread over 256 CUs. Grid split-K on top is deterministic: the
 //    last block of a tile to arrive sums every split's partial in split order.
-//  - gemm_big (BM = 128/256 x 128): the MFMA-bound regime (M >= 2048): a and w tiles copied
-//    into three LDS stages by direct global -> LDS loads (gemm_big.h), four waves each owning a
-//    64 x 64 (or 128 x 64) output block.
+//  - gemm_big (128 x 128 or 256 x 256 tiles): the MFMA-bound regime (M >= 2048): a and w
+//    tiles copied into four LDS stages by direct global -> LDS loads (gemm_big.h), four waves each
+//    owning a 64 x 64 (or 128 x 128) output block on 32 x 32 x 16 MFMA, the epilogue applied
+//    straight from the accumulators.
 //
-// Both hand the finished f32 tile to jh::epilogue (device.h) with the same thread layout.
+// Both apply the epilogues of device.h (LayerNorm folding, bias, ReLU/GELU, RoPE, GeGLU,
+// residual, output statistics) in the same order.
 #include <algorithm>
 #include <stdexcept>
 #include <string>
@@ -33,13 +35,12 @@ __global__ __launch_bounds__(256) void gemm_lat(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// gemm_big: BM x 128 tiles (BM = 128 or 256) for large M; see gemm_big.h. Dynamic LDS:
-// Big<BM>::LDS_BYTES.
+// gemm_big: BM x BM tiles (BM = 128 or 256) for large M; see gemm_big.h. Dynamic LDS:
+// Big<BM, BM>::LDS_BYTES.
 template <int BM, int EPI>
 __global__ __launch_bounds__(256) void gemm_big(GemmParams p) {
     extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
-    __shared__ uint32_t s_last;
-    gemm_big_tile<BM, EPI, false, false>(p, blockIdx.x, lds_dyn, &s_last);
+    gemm_big_tile<BM, BM, EPI, false, false>(p, blockIdx.x, lds_dyn);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -48,7 +49,7 @@ __global__ __launch_bounds__(256) void gemm_big(GemmParams p) {
 namespace {
 
 std::string cfg_str(GemmConfig c) {
-    return std::to_string(c.bm) + "x" + (c.bm >= 128 ? "128" : "64") + " split " +
+    return std::to_string(c.bm) + "x" + std::to_string(c.bm >= 128 ? c.bm : 64) + " split " +
            std::to_string(c.splits);
 }
 
@@ -56,18 +57,17 @@ bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
 }  // namespace
 
+// Split-K scratch (latency tiles only: the throughput tiles take no split).
 size_t gemm_ws_floats(int m, int n, GemmConfig cfg) {
-    if (cfg.splits <= 1) return 0;
-    const int bn = cfg.bm >= 128 ? 128 : 64;
-    const size_t tiles = (size_t)(n / bn) * ((m + cfg.bm - 1) / cfg.bm);
-    const size_t rows = cfg.bm >= 128 ? cfg.bm : (cfg.bm < 32 ? 32 : cfg.bm);
-    return tiles * cfg.splits * rows * bn;
+    if (cfg.splits <= 1 || cfg.bm >= 128) return 0;
+    const size_t tiles = (size_t)(n / 64) * ((m + cfg.bm - 1) / cfg.bm);
+    const size_t rows = cfg.bm < 32 ? 32 : cfg.bm;
+    return tiles * cfg.splits * rows * 64;
 }
 
 size_t gemm_counters(int m, int n, GemmConfig cfg) {
-    if (cfg.splits <= 1) return 0;
-    const int bn = cfg.bm >= 128 ? 128 : 64;
-    return (size_t)(n / bn) * ((m + cfg.bm - 1) / cfg.bm) * (bn / 64);
+    if (cfg.splits <= 1 || cfg.bm >= 128) return 0;
+    return (size_t)(n / 64) * ((m + cfg.bm - 1) / cfg.bm);
 }
 
 void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
@@ -78,8 +78,12 @@ void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
     const bool tput = cfg.bm >= 128;
     if (!(cfg.bm == 16 || cfg.bm == 32 || cfg.bm == 64 || cfg.bm == 128 || cfg.bm == 256))
         fail("no tile height " + std::to_string(cfg.bm));
-    if (tput && g.n % 128) fail("the " + cfg_str(cfg) + " tiles need n % 128 == 0");
-    const int ksteps = tput ? g.k / 64 : g.k / 32;
+    if (tput && g.n % cfg.bm) fail("the " + cfg_str(cfg) + " tiles need n % " + std::to_string(cfg.bm) + " == 0");
+    if (tput && cfg.splits != 1) fail("the " + cfg_str(cfg) + " tiles take no K split");
+    if (tput && (g.epi & EPI_LN) && g.k > 128 * BIG_LN_SLOTS)
+        fail("the " + cfg_str(cfg) + " tiles take LayerNorm epilogues up to k = " +
+             std::to_string(128 * BIG_LN_SLOTS));
+    const int ksteps = g.k / 32;
     if (cfg.splits < 1 || cfg.splits > 8 || cfg.splits > ksteps)
         fail(std::to_string(cfg.splits) + " splits for " + std::to_string(ksteps) + " K steps");
     if (cfg.splits > 1 && (gemm_ws_floats(g.m, g.n, cfg) > s.ws_floats ||
@@ -117,9 +121,9 @@ static void launch_one(const GemmParams& p, hipStream_t st) {
         constexpr int B = BM >= 128 ? BM : 128;
         static const bool lds_ok =  // once per instantiation, before its first launch
             hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_big<B, EPI>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, Big<B>::LDS_BYTES) == hipSuccess;
+                                hipFuncAttributeMaxDynamicSharedMemorySize, Big<B, B>::LDS_BYTES) == hipSuccess;
         if (!lds_ok) throw std::runtime_error("gemm: the throughput kernel cannot have its LDS");
-        hipLaunchKernelGGL((gemm_big<B, EPI>), dim3(blocks), dim3(256), Big<B>::LDS_BYTES, st, p);
+        hipLaunchKernelGGL((gemm_big<B, EPI>), dim3(blocks), dim3(256), (Big<B, B>::LDS_BYTES), st, p);
     } else {
         hipLaunchKernelGGL((gemm_lat<BM < 128 ? BM : 64, EPI>), dim3(blocks), dim3(256), 0, st, p);
     }
@@ -146,7 +150,7 @@ void gemm_launch(const Gemm& g, GemmConfig cfg, const Scratch& s, hipStream_t st
     p.rope_cols = (g.epi & EPI_ROPE) ? 2 * (g.n / 3) : 0;
     p.rope_rows = g.rope_rows;
     p.splits = cfg.splits;
-    p.tiles_n = g.n / (cfg.bm >= 128 ? 128 : 64);
+    p.tiles_n = g.n / (cfg.bm >= 128 ? cfg.bm : 64);
     p.tiles_m = (g.m + cfg.bm - 1) / cfg.bm;
     switch (g.epi) {
         case EPI_K_ROPE: launch_epi<EPI_K_ROPE>(p, cfg.bm, st); break;

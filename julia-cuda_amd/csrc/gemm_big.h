@@ -1,194 +1,430 @@
-// One output tile of the throughput GEMM (BM = 128 or 256 rows x 128 columns), as a device
-// function: the body of the per-GEMM `gemm_big` kernel for large M, and a task of the persistent
-// encoder kernel on large batches. c = epilogue(a . w^T) as the latency tile computes it.
+// One output tile of the throughput GEMM (BM x BN = 256 x 256 or 128 x 128), as a device function:
+// the body of the per-GEMM `gemm_big` kernel for large M. c = epilogue(a . w^T) with the
+// epilogues of the latency tile (device.h), applied straight from the accumulators.
 //
-// The K loop runs BK = 64 at a time through three LDS stages filled by direct global -> LDS
-// loads (no register staging), so the copies of stages k + 1 and k + 2 are in flight while stage
-// k feeds the MFMAs, with one block barrier per stage.
-//  - a's stage: BM rows x 128 bytes; wave load I takes rows 8 I .. 8 I + 7 whole (8 lanes a row:
-//    full 128-byte lines from memory), lane l into LDS chunk 64 I + l, which is row r = 8 I + l / 8,
-//    chunk l % 8, and holds a's chunk (l % 8) ^ ((r / 2) % 8) of that row: the 16 rows a fragment
-//    read touches (two per bank half) land on 16 different banks.
-//  - w's stage: two 64-row groups x two 32-wide K units of the fragment-ordered matrix, copied
-//    as they are (16 KB, contiguous per group).
-// Four waves in a 2 x 2 grid each own (BM / 2) x 64 outputs with MFMA 32 x 32 x 16 (a single wave
-// per SIMD issues it at ~82% of the f16 peak, 16 x 16 x 32 at ~52%): MR = BM / 64 row fragments x
-// 2 column fragments, w as the A operand (a lane gets 4 groups of 4 consecutive output columns of
-// one row). A 32-row, 16-wide K slice of the fragment order is four 16-byte chunks a lane can
-// address directly, so the packed weights serve this MFMA shape too. The finished tile goes
-// through LDS, one 64-column group at a time, into finish() / the epilogue.
+// Four waves in a 2 x 2 grid each own a (BM / 2) x (BN / 2) block of outputs, computed with MFMA
+// 32 x 32 x 16 (a single wave per SIMD issues it at ~82% of the f16 peak) as MR = BM / 64 row
+// fragments x NC = BN / 64 column fragments, w as the MFMA's A operand: lane l of fragment (i, c)
+// holds output row 32 i + l % 32 and columns 32 c + 8 q + 4 (l / 32) + e, q, e < 4.
+// A 256 x 256 tile reads 64 bytes of operands per 8 Kflop, half what a 256 x 128 tile reads: the
+// copy path into a CU (about 64 bytes per clock) keeps up with the MFMAs.
+//
+// The K loop runs BK = 32 at a time through four LDS stages filled by direct global -> LDS loads
+// (no register staging), three stages ahead, with one block barrier per stage. A stage's copies
+// are issued between the MFMAs of the stage three back: issued in one burst they stall the
+// issuing wave on the address path while its MFMA unit idles.
+//  - a's stage: BM rows x 64 bytes; copy I takes rows 16 I .. 16 I + 15 (4 lanes a row), lane l
+//    into LDS chunk 64 I + l, which is row r = 16 I + l / 4, chunk l % 4, and holds a's chunk
+//    (l % 4) ^ ((r / 4) % 4) of that row: the 16 rows one fragment read serves per LDS cycle
+//    cover all 64 banks.
+//  - w's stage: BN / 64 blocks of the fragment-ordered matrix (64 columns x one 32-wide K unit,
+//    4 KB contiguous each), copied as they are.
+//
+// The epilogue's column-wise part runs on the accumulators: a lane has MR output rows, so the row
+// data (LayerNorm statistics, positions) is a few values a lane, loaded with the first stage, and
+// each row's mean and rstd are computed once; the column data (colsum, bias) is loaded with the
+// first stage into LDS; the rotate-half pair (x, x + 32) of a head and the GeGLU (input, gate) pair sit in one
+// lane. The result goes through LDS into row-contiguous 16-byte pieces for the residual, the
+// output statistics and the stores. The RoPE table rows and the residual are loaded a row
+// fragment ahead, the first right after the last MFMAs are issued.
 #pragma once
 
 #include "gemm_tile.h"
 
 namespace jh {
 
-template <int BM>
+template <int BM, int BN>
 struct Big {
-    static constexpr int BN = 128, BK = 64;
-    static constexpr int WM = BM / 2, MR = WM / 32;        // wave rows, 32-row fragments per wave
+    static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 128), "tile shape");
+    static constexpr int BK = 32, NSTAGE = 4;
+    static constexpr int WM = BM / 2, WN = BN / 2;    // a wave's block
+    static constexpr int MR = WM / 32, NC = WN / 32;  // its 32 x 32 fragments
+    static constexpr int NG = WN / 64;                // its 64-column groups
     static constexpr int A_BYTES = BM * BK * 2, W_BYTES = BN * BK * 2;
-    static constexpr int STAGE = A_BYTES + W_BYTES;         // bytes per stage
-    static constexpr int LOADS = STAGE / 1024 / 4;          // 1 KB wave loads per wave per stage
-    static constexpr int OUT_BYTES = BM * 68 * 4;           // one 64-column group of f32 outputs
-    static constexpr int LDS_BYTES = 3 * STAGE > OUT_BYTES ? 3 * STAGE : OUT_BYTES;
+    static constexpr int STAGE = A_BYTES + W_BYTES;  // bytes per stage
+    static constexpr int LOADS = STAGE / 1024 / 4;   // 1 KB copies per wave per stage
+    static constexpr int COLS = NSTAGE * STAGE;       // per wave: colsum, bias of its columns
+    static constexpr int LDS_BYTES = COLS + 4 * 2 * WN * 4;
 };
 
-// s_waitcnt with vmcnt = n (n < 16) and no wait on the other counters (gfx9 encoding:
-// vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8]).
+// LayerNorm statistics slots one lane reads per row (lanes l and l ^ 32 split a row's K / 64
+// slots): the big tiles take LayerNorm epilogues for K <= 64 * 2 * BIG_LN_SLOTS.
+constexpr int BIG_LN_SLOTS = 8;
+
+// s_waitcnt with vmcnt = n (n < 64) and no wait on the other counters (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0 and vmcnt[5:4] in bits 15:14, expcnt in 6:4, lgkmcnt in 11:8).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 16, "vmcnt field");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+    static_assert(N >= 0 && N < 64, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
-// Task `task` of tiles_n * tiles_m * splits (XCD-mapped; consecutive tasks of an XCD share a's
-// rows and walk w's column groups, so an XCD reads its a rows once and w stays in its L2).
-// AX: a is read device-coherent; XG: the outputs are stored and the statistics read
-// device-coherent. The residual is read through the caches (c itself in a per-GEMM launch, or
-// the persistent kernel's write-once p.res).
-template <int BM, int EPI, bool AX, bool XG>
+// Task `task` of tiles_n * tiles_m (XCD-mapped: an XCD takes a contiguous range of tasks, in the
+// grouped order below). AX: a is read device-coherent; XG: the outputs are stored and the
+// statistics read device-coherent. The residual is read through the caches.
+template <int BM, int BN, int EPI, bool AX, bool XG>
 __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, char* lds,
-                                              uint32_t* s_last) {
-    using C = Big<BM>;
-    constexpr int NPASS = BM / 32;
-    const int T = p.tiles_n * p.tiles_m * p.splits;
-    const int L = xcd_task(task, T);
-    const int z = L % p.splits, t2 = L / p.splits;
-    const int bx = t2 % p.tiles_n, by = t2 / p.tiles_n;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63;
+                                              uint64_t* sub = nullptr) {
+    auto mark = [&](int i) {  // profiling: thread 0's view of the task's stages
+        if (sub && threadIdx.x == 0) sub[i] = wall_clock64();
+    };
+    mark(0);
+    using C = Big<BM, BN>;
+    constexpr int MR = C::MR, NC = C::NC, NG = C::NG;
+    const int T = p.tiles_n * p.tiles_m;
+    const int t2 = xcd_task(task, T);
+    // Groups of G row bands (about 2 MB of a): within a group the column block changes slowest,
+    // so an XCD's concurrent tiles share a few w column blocks and the group's a bands, which
+    // together fit its 4 MB L2 (a walk along whole row bands would cycle all of w through the
+    // L2 once per band).
+    const int G = max(1, (2 << 20) / (BM * p.k * 2));
+    const int gsz = G * p.tiles_n, grp0 = t2 / gsz * G, in = t2 % gsz;
+    const int rows_g = min(G, p.tiles_m - grp0);
+    const int bx = in / rows_g, by = grp0 + in % rows_g;
+    const int tid = threadIdx.x, l = tid & 63, l32 = l & 31, hi = l >> 5;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
     const int wm = w >> 1, wn = w & 1;
-    const int U = p.k >> 5, KT = p.k >> 6;
-    const int kt0 = z * KT / p.splits, kt1 = (z + 1) * KT / p.splits, nkt = kt1 - kt0;
+    const int U = p.k >> 5, nkt = U;               // K units of 32 = stages
+    const int row0 = by * BM + wm * C::WM + l32;   // the lane's row of fragment i: row0 + 32 i
+    const int g0 = (bx * BN + wn * C::WN) >> 6;    // the wave's first 64-column group
 
-    // The epilogue's other inputs for both 64-column groups, in flight with the first stages.
-    const int c0 = (tid & 7) * 4;
-    EpiCol ec[2];
-    EpiRow er[2][NPASS];
+    // ---- epilogue inputs that go with the first stage -----------------------------------------
+    // Column data (colsum, bias of the wave's WN columns): two floats a lane, into the wave's own
+    // LDS words after the stages, read back by the epilogue (no block barrier: one wave writes
+    // and reads them).
+    float* wcols = (float*)(lds + C::COLS) + w * 2 * C::WN;
+    float2 cin[2];
+    constexpr int CPL = C::WN / 64;  // columns a lane brings in per array
+    static_assert(CPL == 1 || CPL == 2, "columns per lane");
+    auto col_in = [&](const float* src, int a) {
+        if (CPL == 2) cin[a] = *(const float2*)(src + g0 * 64 + 2 * l);
+        else cin[a] = make_float2(src[g0 * 64 + l], 0.0f);
+    };
+    if (EPI & EPI_LN) col_in(p.colsum, 0);
+    if (EPI & EPI_BIAS) col_in(p.bias, 1);
+    // Row data: the LayerNorm statistics slots hi, hi + 2, ... of each row (unconditional loads,
+    // clamped, masked when summed) and the RoPE positions.
+    const int slots = p.k >> 6;
+    float2 sl[MR][BIG_LN_SLOTS];
+    int pos_[MR];
 #pragma unroll
-    for (int gg = 0; gg < 2; gg++) {
-        epi_load_col<EPI>(p, bx * 2 + gg, c0, ec[gg]);
+    for (int i = 0; i < MR; i++) {
+        const int r = min(row0 + 32 * i, p.m - 1);
+        pos_[i] = r;
+        if (EPI & EPI_LN) {
+            const float* st = p.stats_in + (size_t)r * slots * 2;
 #pragma unroll
-        for (int ps = 0; ps < NPASS; ps++)
-            epi_load_row<EPI, XG, false>(p, by * BM + ps * 32 + (tid >> 3), bx * 2 + gg, c0, er[gg][ps]);
+            for (int u = 0; u < BIG_LN_SLOTS; u++) sl[i][u] = load8f<XG>(st + 2 * min(2 * u + hi, slots - 1));
+        }
     }
+    if ((EPI & EPI_ROPE) && p.pos) {  // one uniform branch around all the rows' loads
 #pragma unroll
-    for (int gg = 0; gg < 2; gg++)
+        for (int i = 0; i < MR; i++) pos_[i] = p.pos[pos_[i]];
+    }
+    if (EPI & EPI_ROPE) {
+        // The table addresses are computed after the K loop from these four values (left to
+        // itself the compiler computes them here and keeps them live through the loop).
 #pragma unroll
-        for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, c0, er[gg][ps]);
+        for (int i = 0; i < MR; i++) asm volatile("" : "+v"(pos_[i]));
+    }
 
-    // Stage copies: wave w issues loads I = w, w + 4, ... of the stage's A_BYTES / 1024 a loads
-    // then W_BYTES / 1024 w loads.
-    auto issue = [&](int kt, int buf) {
+    // ---- the K loop ---------------------------------------------------------------------------
+    // Stage copies: copy q of the wave's LOADS is load I = w + 4 q of the stage's A_BYTES / 1024
+    // a loads then W_BYTES / 1024 w loads.
+    auto issue_one = [&](int kt, int buf, int q) {
         char* st = lds + buf * C::STAGE;
-#pragma unroll
-        for (int q = 0; q < C::LOADS; q++) {
-            const int I = w + 4 * q;
-            if (I < C::A_BYTES / 1024) {
-                const int r = 8 * I + (l >> 3), ch = (l & 7) ^ ((r >> 1) & 7);
-                const int row = min(by * BM + r, p.m - 1);
-                const f16* src = (const f16*)p.a + (size_t)row * p.k + kt * 64 + ch * 8;
-                lds_dma16<AX>(src, st + I * 1024);
-            } else {
-                const int J = I - C::A_BYTES / 1024;  // 4 KB block J / 4 = (group, unit), part J % 4
-                const int blk = J >> 2, G = bx * 2 + (blk >> 1), u = 2 * kt + (blk & 1);
-                const f16* src = (const f16*)p.w + ((size_t)(G * U + u) * 4 + (J & 3)) * 512 + l * 8;
-                lds_dma16<false>(src, st + C::A_BYTES + J * 1024);
-            }
+        const int I = w + 4 * q;
+        if (I < C::A_BYTES / 1024) {
+            const int r = 16 * I + (l >> 2), ch = (l & 3) ^ ((r >> 2) & 3);
+            const int row = min(by * BM + r, p.m - 1);
+            const f16* src = (const f16*)p.a + (size_t)row * p.k + kt * 32 + ch * 8;
+            lds_dma16<AX>(src, st + I * 1024);
+        } else {
+            const int J = I - C::A_BYTES / 1024;  // 4 KB block J / 4 = column group, part J % 4
+            const size_t blk = (size_t)(bx * (BN / 64) + (J >> 2)) * U + kt;
+            const f16* src = (const f16*)p.w + (blk * 4 + (J & 3)) * 512 + l * 8;
+            lds_dma16<false>(src, st + C::A_BYTES + J * 1024);
         }
     };
+    auto issue = [&](int kt, int buf) {
+#pragma unroll
+        for (int q = 0; q < C::LOADS; q++) issue_one(kt, buf, q);
+    };
+#pragma unroll
+    for (int s = 0; s < C::NSTAGE - 1; s++)
+        if (s < nkt) issue(s, s);
 
-    floatx16 acc[C::MR][2];
+    // Column data of group j, half h, slice q (columns 64 j + 32 h + 8 q + 4 hi ..).
+    auto col4 = [&](int a, int j, int h, int q) {
+        return *(const float4*)(wcols + a * C::WN + 64 * j + 32 * h + 8 * q + 4 * hi);
+    };
+
+    if (nkt > 2)
+        wait_vmcnt<2 * C::LOADS>();
+    else
+        wait_vmcnt<C::LOADS>();
+    auto col_out = [&](int a) {
+        if (CPL == 2) *(float2*)(wcols + a * C::WN + 2 * l) = cin[a];
+        else wcols[a * C::WN + l] = cin[a].x;
+    };
+    if (EPI & EPI_LN) col_out(0);
+    if (EPI & EPI_BIAS) col_out(1);
+    // Each row's mean and rstd (lanes l and l ^ 32 each summed half of its slots), once the first
+    // stage has landed: its wait covers the slots, loaded before it (loads complete in order).
+    float mu_[MR], rs_[MR];
+    if (EPI & EPI_LN) {
 #pragma unroll
-    for (int i = 0; i < C::MR; i++)
+        for (int i = 0; i < MR; i++) {
+            float S = 0.0f, Q = 0.0f;
 #pragma unroll
-        for (int c = 0; c < 2; c++)
+            for (int u = 0; u < BIG_LN_SLOTS; u++) {
+                const bool ok = 2 * u + hi < slots;
+                S += ok ? sl[i][u].x : 0.0f;
+                Q += ok ? sl[i][u].y : 0.0f;
+            }
+            S = sum_xor32(S);
+            Q = sum_xor32(Q);
+            const float mean = S / (float)p.k;
+            const float var = fmaxf(Q / (float)p.k - mean * mean, 0.0f);
+            mu_[i] = mean;
+            rs_[i] = 1.0f / sqrtf(var + p.eps);
+            // (kept here: sunk past the K loop to its use, the computation would keep the
+            // loaded slots live through the loop)
+            asm volatile("" : "+v"(mu_[i]), "+v"(rs_[i]));
+        }
+    }
+
+    floatx16 acc[MR][NC];
+#pragma unroll
+    for (int i = 0; i < MR; i++)
+#pragma unroll
+        for (int c = 0; c < NC; c++)
 #pragma unroll
             for (int e = 0; e < 16; e++) acc[i][c][e] = 0.0f;
 
-    if (nkt > 0) issue(kt0, 0);
-    if (nkt > 1) issue(kt0 + 1, 1);
-    const int l32 = l & 31, hi = l >> 5;
+    constexpr int NM = MR * NC, PER = C::LOADS / 2, GAP = NM / PER;
+    static_assert(C::LOADS % 2 == 0 && GAP >= 1, "copies per K-16 step");
     for (int s = 0; s < nkt; s++) {
-        // This wave's copies of stage s are done (the next stage's may stay in flight), then a
-        // bare barrier: every wave's are, and every wave is done reading stage s - 1, whose
-        // buffer the copy issued next overwrites. (__syncthreads' release fence would wait for
-        // all of this wave's copies, the next stage's too.)
-        if (s + 1 < nkt)
+        // This wave's copies of stage s are done (the two later stages' may stay in flight), then
+        // a bare barrier: every wave's are, and every wave is done reading stage s - 1, whose
+        // buffer the copies issued next overwrite. (__syncthreads' release fence would wait for
+        // all of this wave's copies.)
+        if (s + 2 < nkt)
+            wait_vmcnt<2 * C::LOADS>();
+        else if (s + 1 < nkt)
             wait_vmcnt<C::LOADS>();
         else
             wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
-        if (s + 2 < nkt) issue(kt0 + s + 2, (s + 2) % 3);
-        const char* st = lds + (s % 3) * C::STAGE;
+        if (s == 0) mark(1);
+        const bool more = s + 3 < nkt;
+        const int kt3 = s + 3, buf3 = (s + 3) % C::NSTAGE;
+        const char* st = lds + (s % C::NSTAGE) * C::STAGE;
         const char* ws = st + C::A_BYTES;
-        // Four K-16 steps t. Lane l takes K 16 t + 8 (l / 32) .. + 7: a's chunk 2 t + l / 32 of row
-        // 32 i + l % 32; w's row 32 c + l % 32 of the wave's 64-column group, which in the
-        // fragment order is unit t / 2, fragment 2 c + (l % 32) / 16, lane group 2 (t % 2) + l / 32.
-        // Step t + 1's fragments are read while step t's MFMAs run (two register sets).
-        half8 fa[2][C::MR], fw[2][2];
-        auto rd = [&](int t) {
-            const int b = t & 1;
+        // Two K-16 steps t. Lane l takes K 16 t + 8 (l / 32) .. + 7: a's chunk 2 t + l / 32 of
+        // row 32 i + l % 32; w's row 32 c + l % 32 of the wave's columns, which in the fragment
+        // order is block (the wave's first column) / 64 + c / 2, fragment 2 (c % 2) + (l % 32) / 16,
+        // lane group 2 t + l / 32.
+        half8 fa[2][MR], fw[2][NC];
 #pragma unroll
-            for (int i = 0; i < C::MR; i++) {
+        for (int t = 0; t < 2; t++) {
+#pragma unroll
+            for (int i = 0; i < MR; i++) {
                 const int r = wm * C::WM + 32 * i + l32;
-                fa[b][i] = *(const half8*)(st + (r * 8 + ((2 * t + hi) ^ ((r >> 1) & 7))) * 16);
+                fa[t][i] = *(const half8*)(st + r * 64 + (((2 * t + hi) ^ ((r >> 2) & 3)) << 4));
             }
 #pragma unroll
-            for (int c = 0; c < 2; c++) {
-                const int j = 2 * c + (l32 >> 4), g2 = 2 * (t & 1) + hi;
-                fw[b][c] = *(const half8*)(ws + ((wn * 2 + (t >> 1)) * 4 + j) * 1024 + (g2 * 16 + (l & 15)) * 16);
+            for (int c = 0; c < NC; c++) {
+                const int g = wn * (C::WN / 64) + (c >> 1), j = 2 * (c & 1) + (l32 >> 4);
+                fw[t][c] = *(const half8*)(ws + (g * 4 + j) * 1024 + ((2 * t + hi) * 16 + (l & 15)) * 16);
             }
-        };
-        auto mm = [&](int t) {
-            const int b = t & 1;
-#pragma unroll
-            for (int i = 0; i < C::MR; i++)
-#pragma unroll
-                for (int c = 0; c < 2; c++)
-                    acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[b][c], fa[b][i], acc[i][c], 0, 0, 0);
-        };
-        rd(0);
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            if (t + 1 < 4) rd(t + 1);
-            __builtin_amdgcn_sched_barrier(0);  // the next step's reads ahead of this step's MFMAs
-            mm(t);
-            __builtin_amdgcn_sched_barrier(0);
         }
+        __builtin_amdgcn_sched_barrier(0);  // both steps' reads ahead of the MFMAs
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+#pragma unroll
+            for (int x = 0; x < NM; x++) {
+                const int i = x / NC, c = x % NC;
+                acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[t][c], fa[t][i], acc[i][c], 0, 0, 0);
+                if (x % GAP == GAP - 1 && x / GAP < PER) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    if (more) issue_one(kt3, buf3, t * PER + x / GAP);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();  // every wave is done with the stages: the outputs reuse the space
+    mark(2);
 
-    // The output through LDS (f32, rows of 64 + 4 pad), one 64-column group (the waves with
-    // wn == grp) at a time, into the epilogue layout.
-    float* out = (float*)lds;
+    // ---- the epilogue -------------------------------------------------------------------------
+    // Per row fragment i: the column-wise part (LayerNorm, bias, ReLU/GELU, RoPE, GeGLU) on the
+    // accumulators, where a lane holds the RoPE and GeGLU pairs; the f32 result through the
+    // wave's own LDS rows (32 rows of WO columns, padded to WO + 4 floats: 16 rows of one write
+    // cover all 64 banks) into rows of 8 consecutive columns a lane; then the residual, the f16
+    // rounding, the output statistics (8 lanes a 64-column group) and 16-byte stores, 16 (or 8)
+    // lanes a row.
+    constexpr bool GEGLU = (EPI & EPI_GEGLU) != 0;
+    constexpr bool RES = (EPI & EPI_RES) && !GEGLU;
+    constexpr int WO = GEGLU ? C::WN / 2 : C::WN;  // output columns of the wave
+    constexpr int LPR = WO / 8, RPP = 64 / LPR;     // lanes a row, rows a pass
+    constexpr int NPASS = 32 / RPP, PAD = WO + 4;
+    const int ncol = GEGLU ? (p.n >> 1) : p.n;
+    const int col0 = (GEGLU ? g0 * 32 : g0 * 64);   // the wave's first output column
+    float* sg = (float*)lds + w * 32 * PAD;
+    __syncthreads();  // every wave is done reading the stages
+
+    struct RowIn {
+        float4 rt[4][2];        // RoPE (cos, sin) of dimensions 8 q + 4 hi .. + 3
+        half8 rr[NPASS];        // residual, transposed layout
+    };
+    auto load_row = [&](int i, RowIn& in) {
+        if (EPI & EPI_ROPE) {
+            const int pos = min(max(pos_[i], 0), p.rope_rows - 1);
 #pragma unroll
-    for (int grp = 0; grp < 2; grp++) {
-        if (wn == grp) {  // acc[i][c][4 q + e]: row 32 i + l % 32, column 32 c + 8 q + 4 (l / 32) + e
+            for (int q = 0; q < 4; q++) {
+                const float4* t = (const float4*)(p.rope + ((size_t)pos * 32 + 8 * q + 4 * hi) * 2);
+                in.rt[q][0] = t[0];
+                in.rt[q][1] = t[1];
+            }
+        }
+        if (RES) {
+            const f16* x = (const f16*)(p.res ? p.res : p.c);
 #pragma unroll
-            for (int i = 0; i < C::MR; i++)
+            for (int ps = 0; ps < NPASS; ps++) {
+                const int r = min(by * BM + wm * C::WM + 32 * i + ps * RPP + l / LPR, p.m - 1);
+                in.rr[ps] = *(const half8*)(x + (size_t)r * ncol + col0 + 8 * (l % LPR));
+            }
+        }
+    };
+    RowIn rin[2];
+    load_row(0, rin[0]);
+
 #pragma unroll
-                for (int c = 0; c < 2; c++)
+    for (int i = 0; i < MR; i++) {
+        // (scheduling fences: one row fragment's values, addresses and stores at a time)
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 1 < MR) load_row(i + 1, rin[(i + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        const RowIn& ri = rin[i & 1];
+#pragma unroll
+        for (int j = 0; j < NG; j++) {
+            const int g = g0 + j;
+            // v[h][4 q + e]: column 64 g + 32 h + 8 q + 4 hi + e
+            float v[2][16];
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int x = 0; x < 16; x++) v[h][x] = acc[i][2 * j + h][x];
+            if (EPI & EPI_LN) {
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float4 c4 = col4(0, j, h, q);
+                        const float cc[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            v[h][4 * q + e] = rs_[i] * (v[h][4 * q + e] - mu_[i] * cc[e]);
+                    }
+            }
+            if (EPI & EPI_BIAS) {
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float4 b4 = col4(1, j, h, q);
+                        const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+                        for (int e = 0; e < 4; e++) v[h][4 * q + e] += bb[e];
+                    }
+            }
+            if (EPI & EPI_RELU) {
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int x = 0; x < 16; x++) v[h][x] = fmaxf(v[h][x], 0.0f);
+            }
+            if (EPI & EPI_GELU) {
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int x = 0; x < 16; x++) v[h][x] = gelu(v[h][x]);
+            }
+            if (EPI & EPI_ROPE) {
+                // q and k heads: columns x and x + 32 of a head are the rotate-half pair of
+                // dimension x; the table holds (cos, sin) per dimension.
+                if (g * 64 < p.rope_cols) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float4 t0 = ri.rt[q][0], t1 = ri.rt[q][1];
+                        const float co[4] = {t0.x, t0.z, t1.x, t1.z}, sn[4] = {t0.y, t0.w, t1.y, t1.w};
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const float x1 = v[0][4 * q + e], x2 = v[1][4 * q + e];
+                            v[0][4 * q + e] = x1 * co[e] - x2 * sn[e];
+                            v[1][4 * q + e] = x2 * co[e] + x1 * sn[e];
+                        }
+                    }
+                }
+            }
+            float* dst = sg + l32 * PAD + 4 * hi;
+            if (GEGLU) {
+                // Packed rows 64 g + x are the input of output column 32 g + x, + 32 its gate.
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    float4 o;
+                    o.x = gelu(v[0][4 * q]) * v[1][4 * q];
+                    o.y = gelu(v[0][4 * q + 1]) * v[1][4 * q + 1];
+                    o.z = gelu(v[0][4 * q + 2]) * v[1][4 * q + 2];
+                    o.w = gelu(v[0][4 * q + 3]) * v[1][4 * q + 3];
+                    *(float4*)(dst + 32 * j + 8 * q) = o;
+                }
+            } else {
+#pragma unroll
+                for (int h = 0; h < 2; h++)
 #pragma unroll
                     for (int q = 0; q < 4; q++)
-                        *(floatx4*)&out[(wm * C::WM + 32 * i + l32) * 68 + 32 * c + 8 * q + 4 * hi] =
-                            floatx4{acc[i][c][4 * q], acc[i][c][4 * q + 1], acc[i][c][4 * q + 2],
-                                    acc[i][c][4 * q + 3]};
+                        *(float4*)(dst + 64 * j + 32 * h + 8 * q) =
+                            make_float4(v[h][4 * q], v[h][4 * q + 1], v[h][4 * q + 2], v[h][4 * q + 3]);
+            }
         }
-        __syncthreads();
-        float v[NPASS][8];
+        // The wave's rows back, 8 columns a lane (LDS operations of one wave complete in order).
+        // Lanes 8-15 of each 16 read their two halves in the other order: no two lanes of a
+        // 16-lane group share a bank.
+        const int cl = 8 * (l % LPR), sw = (LPR == 16 && (l & 8)) ? 4 : 0;
 #pragma unroll
         for (int ps = 0; ps < NPASS; ps++) {
-            const float* src = &out[(ps * 32 + (tid >> 3)) * 68 + c0];
-            const float4 lo = *(const float4*)src, hi = *(const float4*)(src + 32);
-            v[ps][0] = lo.x, v[ps][1] = lo.y, v[ps][2] = lo.z, v[ps][3] = lo.w;
-            v[ps][4] = hi.x, v[ps][5] = hi.y, v[ps][6] = hi.z, v[ps][7] = hi.w;
+            const int rl = ps * RPP + l / LPR;
+            const float* src = sg + rl * PAD + cl;
+            const float4 a0 = *(const float4*)(src + sw), a1 = *(const float4*)(src + 4 - sw);
+            const float4 lo = sw ? a1 : a0, hi4 = sw ? a0 : a1;
+            float y[8] = {lo.x, lo.y, lo.z, lo.w, hi4.x, hi4.y, hi4.z, hi4.w};
+            if (RES) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) y[e] += (float)ri.rr[ps][e];
+            }
+            half8 o;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = (f16)y[e];
+            const int row = by * BM + wm * C::WM + 32 * i + rl;
+            const bool valid = row < p.m;
+            if (valid) store16<XG>((f16*)p.c + (size_t)row * ncol + col0 + cl, o);
+            if (EPI & EPI_STATS) {
+                float s = 0.0f, sq = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float b = (float)o[e];
+                    s += b, sq += b * b;
+                }
+                s = group_sum<8>(s);
+                sq = group_sum<8>(sq);
+                if (valid && (l & 7) == 0)
+                    store8<XG>(p.stats_out + ((size_t)row * (p.n >> 6) + (col0 + cl) / 64) * 2, make_float2(s, sq));
+            }
         }
-        __syncthreads();  // every thread has read the group before the next one is written
-        // Each 64-column group is its own split-K "tile" (two per block).
-        finish<NPASS, EPI, XG>(p, v, (bx * p.tiles_m + by) * 2 + grp, z, by * BM, bx * 2 + grp, BM,
-                               s_last, ec[grp], er[grp]);
     }
+    mark(3);
 }
 
 }  // namespace jh

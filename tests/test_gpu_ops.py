@@ -132,6 +132,10 @@ def check_gemm(P, out16, stats, label):
 def test_config1_gemm_lnrope(torch_cuda, scratch, bm, splits):
     say(f"config 1 gemm_lnrope M=293 K=768 N=2304 bm={bm} splits={splits}")
     P = gemm_problem("lnrope", 293, 2304, 768, seed=11)
+    if bm >= 128 and splits > 1:
+        with pytest.raises(jh.JuliaHipError, match="take no K split"):
+            run_gemm(torch_cuda, P, bm, splits, scratch)
+        return
     out, _ = run_gemm(torch_cuda, P, bm, splits, scratch)
     check_gemm(P, out, None, f"lnrope bm={bm} z={splits}")
 
@@ -153,6 +157,10 @@ CONFIG2 = [("resstats", 768, 768), ("lngeglu", 2304, 768), ("resstats", 768, 115
 def test_config2_layer_gemms(torch_cuda, scratch, kind, n, k, bm, splits):
     say(f"config 2 {kind} M=512 N={n} K={k} bm={bm} splits={splits}")
     P = gemm_problem(kind, 512, n, k, seed=21 + n + k)
+    if bm >= 128 and splits > 1:
+        with pytest.raises(jh.JuliaHipError, match="take no K split"):
+            run_gemm(torch_cuda, P, bm, splits, scratch)
+        return
     out, st = run_gemm(torch_cuda, P, bm, splits, scratch)
     check_gemm(P, out, st, f"{kind} n={n} k={k} bm={bm} z={splits}")
 
@@ -169,6 +177,22 @@ def test_head_gemms(torch_cuda, scratch, kind, n, k):
 
 
 # ---- MFMA-bound sizes ---------------------------------------------------------------------
+# Every epilogue on the throughput tiles (128 x 128 and 256 x 256), M not a multiple of either.
+BIG_EPIS = [("lnrope", 2304, 768), ("rope", 2304, 768), ("lngeglu", 2304, 768),
+            ("resstats", 768, 768), ("resstats", 768, 1152), ("lnbias", 2304, 768),
+            ("biasresstats", 768, 1536), ("lnbiasrelu", 1536, 768), ("lnbiasgelu", 768, 768)]
+
+
+@pytest.mark.parametrize("kind,n,k", BIG_EPIS, ids=[f"{a}-{b}-{c}" for a, b, c in BIG_EPIS])
+@pytest.mark.parametrize("bm", [128, 256])
+def test_big_tiles_every_epilogue(torch_cuda, scratch, kind, n, k, bm):
+    say(f"big tiles {kind} M=2100 N={n} K={k} bm={bm}")
+    P = gemm_problem(kind, 2100, n, k, seed=51 + n + k)
+    out, st = run_gemm(torch_cuda, P, bm, 1, scratch)
+    check_gemm(P, out, st, f"{kind} M=2100 n={n} k={k} bm={bm}")
+
+
+
 @pytest.mark.parametrize("bm", [128, 256])
 def test_large_m_lngeglu(torch_cuda, scratch, bm):
     say(f"lngeglu M=4096 N=2304 K=768 bm={bm}")
