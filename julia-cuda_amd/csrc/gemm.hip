@@ -10,9 +10,9 @@
 //    there are more tiles to spread over 256 CUs. Grid split-K on top is deterministic: the
 //    last block of a tile to arrive sums every split's partial in split order.
 //  - gemm_big (128 x 128 or 256 x 256 tiles): the MFMA-bound regime (M >= 2048): a and w
-//    tiles copied into four LDS stages by direct global -> LDS loads (gemm_big.h), four waves each
-//    owning a 64 x 64 (or 128 x 128) output block on 32 x 32 x 16 MFMA, the epilogue applied
-//    straight from the accumulators.
+//    tiles copied into four LDS stages by direct global -> LDS loads (gemm_big.h), four or eight
+//    waves each owning a 64 x 64 (or 128 x 64) output block on 32 x 32 x 16 MFMA, the epilogue's
+//    column-wise part applied on the accumulators.
 //
 // Both apply the epilogues of device.h (LayerNorm folding, bias, ReLU/GELU, RoPE, GeGLU,
 // residual, output statistics) in the same order.
@@ -38,7 +38,7 @@ __global__ __launch_bounds__(256) void gemm_lat(GemmParams p) {
 // gemm_big: BM x BM tiles (BM = 128 or 256) for large M; see gemm_big.h. Dynamic LDS:
 // Big<BM, BM>::LDS_BYTES.
 template <int BM, int EPI>
-__global__ __launch_bounds__(256) void gemm_big(GemmParams p) {
+__global__ __launch_bounds__((Big<BM, BM>::THREADS)) void gemm_big(GemmParams p) {
     extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
     gemm_big_tile<BM, BM, EPI, false, false>(p, blockIdx.x, lds_dyn);
 }
@@ -123,7 +123,7 @@ static void launch_one(const GemmParams& p, hipStream_t st) {
             hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_big<B, EPI>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, Big<B, B>::LDS_BYTES) == hipSuccess;
         if (!lds_ok) throw std::runtime_error("gemm: the throughput kernel cannot have its LDS");
-        hipLaunchKernelGGL((gemm_big<B, EPI>), dim3(blocks), dim3(256), (Big<B, B>::LDS_BYTES), st, p);
+        hipLaunchKernelGGL((gemm_big<B, EPI>), dim3(blocks), dim3(Big<B, B>::THREADS), (Big<B, B>::LDS_BYTES), st, p);
     } else {
         hipLaunchKernelGGL((gemm_lat<BM < 128 ? BM : 64, EPI>), dim3(blocks), dim3(256), 0, st, p);
     }

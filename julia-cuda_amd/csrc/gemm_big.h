@@ -2,12 +2,13 @@
 // the body of the per-GEMM `gemm_big` kernel for large M. c = epilogue(a . w^T) with the
 // epilogues of the latency tile (device.h), applied straight from the accumulators.
 //
-// Four waves in a 2 x 2 grid each own a (BM / 2) x (BN / 2) block of outputs, computed with MFMA
-// 32 x 32 x 16 (a single wave per SIMD issues it at ~82% of the f16 peak) as MR = BM / 64 row
-// fragments x NC = BN / 64 column fragments, w as the MFMA's A operand: lane l of fragment (i, c)
-// holds output row 32 i + l % 32 and columns 32 c + 8 q + 4 (l / 32) + e, q, e < 4.
-// A 256 x 256 tile reads 64 bytes of operands per 8 Kflop, half what a 256 x 128 tile reads: the
-// copy path into a CU (about 64 bytes per clock) keeps up with the MFMAs.
+// Waves in a 2 x (BN / 64) grid (eight for 256 x 256: two a SIMD, so that one wave's MFMAs run
+// while the other waits on its copies or LDS reads) each own a (BM / 2) x 64 block of outputs,
+// computed with MFMA 32 x 32 x 16 as MR = BM / 64 row fragments x 2 column fragments, w as the
+// MFMA's A operand: lane l of fragment (i, c) holds output row 32 i + l % 32 and columns
+// 32 c + 8 q + 4 (l / 32) + e, q, e < 4. A 256 x 256 tile reads 64 bytes of operands per
+// 8 Kflop, half what a 256 x 128 tile reads: the copy path into a CU (about 64 bytes per clock)
+// keeps up with the MFMAs.
 //
 // The K loop runs BK = 32 at a time through four LDS stages filled by direct global -> LDS loads
 // (no register staging), three stages ahead, with one block barrier per stage. A stage's copies
@@ -22,11 +23,11 @@
 //
 // The epilogue's column-wise part runs on the accumulators: a lane has MR output rows, so the row
 // data (LayerNorm statistics, positions) is a few values a lane, loaded with the first stage, and
-// each row's mean and rstd are computed once; the column data (colsum, bias) is loaded with the
-// first stage into LDS; the rotate-half pair (x, x + 32) of a head and the GeGLU (input, gate) pair sit in one
+// each row's mean and rstd are computed once a tile (two threads a row) into LDS; the column
+// data (colsum, bias) is loaded with the first stage into LDS; the rotate-half pair (x, x + 32) of a head and the GeGLU (input, gate) pair sit in one
 // lane. The result goes through LDS into row-contiguous 16-byte pieces for the residual, the
-// output statistics and the stores. The RoPE table rows and the residual are loaded a row
-// fragment ahead, the first right after the last MFMAs are issued.
+// output statistics and the stores. The RoPE table rows and the residual are loaded two row
+// fragments ahead, the first two right after the last MFMAs are issued.
 #pragma once
 
 #include "gemm_tile.h"
@@ -37,18 +38,23 @@ template <int BM, int BN>
 struct Big {
     static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 128), "tile shape");
     static constexpr int BK = 32, NSTAGE = 4;
-    static constexpr int WM = BM / 2, WN = BN / 2;    // a wave's block
+    static constexpr int WAVES_M = 2, WAVES_N = BN / 64;  // 2 x 4 waves (256) or 2 x 2 (128)
+    static constexpr int NWAVES = WAVES_M * WAVES_N, THREADS = 64 * NWAVES;
+    static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;  // a wave's block
     static constexpr int MR = WM / 32, NC = WN / 32;  // its 32 x 32 fragments
     static constexpr int NG = WN / 64;                // its 64-column groups
     static constexpr int A_BYTES = BM * BK * 2, W_BYTES = BN * BK * 2;
-    static constexpr int STAGE = A_BYTES + W_BYTES;  // bytes per stage
-    static constexpr int LOADS = STAGE / 1024 / 4;   // 1 KB copies per wave per stage
+    static constexpr int STAGE = A_BYTES + W_BYTES;   // bytes per stage
+    static constexpr int LOADS = STAGE / 1024 / NWAVES;  // 1 KB copies per wave per stage
     static constexpr int COLS = NSTAGE * STAGE;       // per wave: colsum, bias of its columns
-    static constexpr int LDS_BYTES = COLS + 4 * 2 * WN * 4;
+    static constexpr int ROWS = COLS + NWAVES * 2 * WN * 4;  // per row: LayerNorm mean, rstd
+    static constexpr int LDS_BYTES = ROWS + BM * 8;
+    static_assert(NG == 1 && LOADS >= 1, "wave blocks of 64 columns");
+    static_assert(THREADS == 2 * BM, "two threads a row for the row statistics");
 };
 
-// LayerNorm statistics slots one lane reads per row (lanes l and l ^ 32 split a row's K / 64
-// slots): the big tiles take LayerNorm epilogues for K <= 64 * 2 * BIG_LN_SLOTS.
+// LayerNorm statistics slots one thread reads (two threads split a row's K / 64 slots): the big
+// tiles take LayerNorm epilogues for K <= 64 * 2 * BIG_LN_SLOTS.
 constexpr int BIG_LN_SLOTS = 8;
 
 // s_waitcnt with vmcnt = n (n < 64) and no wait on the other counters (gfx9 encoding:
@@ -83,7 +89,7 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     const int bx = in / rows_g, by = grp0 + in % rows_g;
     const int tid = threadIdx.x, l = tid & 63, l32 = l & 31, hi = l >> 5;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
-    const int wm = w >> 1, wn = w & 1;
+    const int wm = w / C::WAVES_N, wn = w % C::WAVES_N;
     const int U = p.k >> 5, nkt = U;               // K units of 32 = stages
     const int row0 = by * BM + wm * C::WM + l32;   // the lane's row of fragment i: row0 + 32 i
     const int g0 = (bx * BN + wn * C::WN) >> 6;    // the wave's first 64-column group
@@ -102,21 +108,20 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     };
     if (EPI & EPI_LN) col_in(p.colsum, 0);
     if (EPI & EPI_BIAS) col_in(p.bias, 1);
-    // Row data: the LayerNorm statistics slots hi, hi + 2, ... of each row (unconditional loads,
-    // clamped, masked when summed) and the RoPE positions.
+    // Row data: the LayerNorm statistics, two threads a row of the tile, thread t taking slots
+    // t % 2, t % 2 + 2, ... of row t / 2 (unconditional loads, clamped, masked when summed); the
+    // lane's RoPE positions.
     const int slots = p.k >> 6;
-    float2 sl[MR][BIG_LN_SLOTS];
+    float2 sl[BIG_LN_SLOTS];
+    if (EPI & EPI_LN) {
+        const int r = min(by * BM + (tid >> 1), p.m - 1);
+        const float* st = p.stats_in + (size_t)r * slots * 2;
+#pragma unroll
+        for (int u = 0; u < BIG_LN_SLOTS; u++) sl[u] = load8f<XG>(st + 2 * min(2 * u + (tid & 1), slots - 1));
+    }
     int pos_[MR];
 #pragma unroll
-    for (int i = 0; i < MR; i++) {
-        const int r = min(row0 + 32 * i, p.m - 1);
-        pos_[i] = r;
-        if (EPI & EPI_LN) {
-            const float* st = p.stats_in + (size_t)r * slots * 2;
-#pragma unroll
-            for (int u = 0; u < BIG_LN_SLOTS; u++) sl[i][u] = load8f<XG>(st + 2 * min(2 * u + hi, slots - 1));
-        }
-    }
+    for (int i = 0; i < MR; i++) pos_[i] = min(row0 + 32 * i, p.m - 1);
     if ((EPI & EPI_ROPE) && p.pos) {  // one uniform branch around all the rows' loads
 #pragma unroll
         for (int i = 0; i < MR; i++) pos_[i] = p.pos[pos_[i]];
@@ -129,11 +134,11 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     }
 
     // ---- the K loop ---------------------------------------------------------------------------
-    // Stage copies: copy q of the wave's LOADS is load I = w + 4 q of the stage's A_BYTES / 1024
+    // Stage copies: copy q of the wave's LOADS is load I = w + NWAVES q of the stage's A_BYTES / 1024
     // a loads then W_BYTES / 1024 w loads.
     auto issue_one = [&](int kt, int buf, int q) {
         char* st = lds + buf * C::STAGE;
-        const int I = w + 4 * q;
+        const int I = w + C::NWAVES * q;
         if (I < C::A_BYTES / 1024) {
             const int r = 16 * I + (l >> 2), ch = (l & 3) ^ ((r >> 2) & 3);
             const int row = min(by * BM + r, p.m - 1);
@@ -163,35 +168,31 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
         wait_vmcnt<2 * C::LOADS>();
     else
         wait_vmcnt<C::LOADS>();
+    mark(1);  // (not in the loop: the clock read is a scalar-memory operation, and with one of
+              // those outstanding the compiler waits for every LDS read at once)
     auto col_out = [&](int a) {
         if (CPL == 2) *(float2*)(wcols + a * C::WN + 2 * l) = cin[a];
         else wcols[a * C::WN + l] = cin[a].x;
     };
     if (EPI & EPI_LN) col_out(0);
     if (EPI & EPI_BIAS) col_out(1);
-    // Each row's mean and rstd (lanes l and l ^ 32 each summed half of its slots), once the first
-    // stage has landed: its wait covers the slots, loaded before it (loads complete in order).
-    float mu_[MR], rs_[MR];
+    // Each row's mean and rstd into LDS (read by the epilogue), once the first stage has landed:
+    // its wait covers the slots, loaded before it (loads complete in order). The barrier before
+    // the first fragment reads orders these writes before every wave's reads.
+    float2* rows_ms = (float2*)(lds + C::ROWS);
     if (EPI & EPI_LN) {
+        float S = 0.0f, Q = 0.0f;
 #pragma unroll
-        for (int i = 0; i < MR; i++) {
-            float S = 0.0f, Q = 0.0f;
-#pragma unroll
-            for (int u = 0; u < BIG_LN_SLOTS; u++) {
-                const bool ok = 2 * u + hi < slots;
-                S += ok ? sl[i][u].x : 0.0f;
-                Q += ok ? sl[i][u].y : 0.0f;
-            }
-            S = sum_xor32(S);
-            Q = sum_xor32(Q);
-            const float mean = S / (float)p.k;
-            const float var = fmaxf(Q / (float)p.k - mean * mean, 0.0f);
-            mu_[i] = mean;
-            rs_[i] = 1.0f / sqrtf(var + p.eps);
-            // (kept here: sunk past the K loop to its use, the computation would keep the
-            // loaded slots live through the loop)
-            asm volatile("" : "+v"(mu_[i]), "+v"(rs_[i]));
+        for (int u = 0; u < BIG_LN_SLOTS; u++) {
+            const bool ok = 2 * u + (tid & 1) < slots;
+            S += ok ? sl[u].x : 0.0f;
+            Q += ok ? sl[u].y : 0.0f;
         }
+        S = group_sum<2>(S);
+        Q = group_sum<2>(Q);
+        const float mean = S / (float)p.k;
+        const float var = fmaxf(Q / (float)p.k - mean * mean, 0.0f);
+        if ((tid & 1) == 0) rows_ms[tid >> 1] = make_float2(mean, 1.0f / sqrtf(var + p.eps));
     }
 
     floatx16 acc[MR][NC];
@@ -202,55 +203,68 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
 #pragma unroll
             for (int e = 0; e < 16; e++) acc[i][c][e] = 0.0f;
 
-    constexpr int NM = MR * NC, PER = C::LOADS / 2, GAP = NM / PER;
-    static_assert(C::LOADS % 2 == 0 && GAP >= 1, "copies per K-16 step");
-    for (int s = 0; s < nkt; s++) {
-        // This wave's copies of stage s are done (the two later stages' may stay in flight), then
-        // a bare barrier: every wave's are, and every wave is done reading stage s - 1, whose
-        // buffer the copies issued next overwrite. (__syncthreads' release fence would wait for
-        // all of this wave's copies.)
-        if (s + 2 < nkt)
-            wait_vmcnt<2 * C::LOADS>();
-        else if (s + 1 < nkt)
-            wait_vmcnt<C::LOADS>();
-        else
-            wait_vmcnt<0>();
-        __builtin_amdgcn_s_barrier();
-        if (s == 0) mark(1);
-        const bool more = s + 3 < nkt;
-        const int kt3 = s + 3, buf3 = (s + 3) % C::NSTAGE;
-        const char* st = lds + (s % C::NSTAGE) * C::STAGE;
-        const char* ws = st + C::A_BYTES;
-        // Two K-16 steps t. Lane l takes K 16 t + 8 (l / 32) .. + 7: a's chunk 2 t + l / 32 of
-        // row 32 i + l % 32; w's row 32 c + l % 32 of the wave's columns, which in the fragment
-        // order is block (the wave's first column) / 64 + c / 2, fragment 2 (c % 2) + (l % 32) / 16,
-        // lane group 2 t + l / 32.
-        half8 fa[2][MR], fw[2][NC];
-#pragma unroll
-        for (int t = 0; t < 2; t++) {
-#pragma unroll
-            for (int i = 0; i < MR; i++) {
-                const int r = wm * C::WM + 32 * i + l32;
-                fa[t][i] = *(const half8*)(st + r * 64 + (((2 * t + hi) ^ ((r >> 2) & 3)) << 4));
-            }
-#pragma unroll
-            for (int c = 0; c < NC; c++) {
-                const int g = wn * (C::WN / 64) + (c >> 1), j = 2 * (c & 1) + (l32 >> 4);
-                fw[t][c] = *(const half8*)(ws + (g * 4 + j) * 1024 + ((2 * t + hi) * 16 + (l & 15)) * 16);
-            }
+    // Fragments of one K-16 step: lane l takes K 16 t + 8 (l / 32) .. + 7 of the stage: a's chunk
+    // 2 t + l / 32 of row 32 i + l % 32; w's row 32 c + l % 32 of the wave's columns, which in the
+    // fragment order is block (the wave's first column) / 64 + c / 2, fragment 2 (c % 2) +
+    // (l % 32) / 16, lane group 2 t + l / 32. Read r of a step, in the order the MFMAs use them:
+    // w fragment 0, a fragment 0, the other w fragments, the other a fragments.
+    half8 fa[2][MR], fw[2][NC];
+    constexpr int NR = MR + NC;  // reads per step
+    auto rd = [&](int stage, int t, int r) {
+        const char* st = lds + (stage % C::NSTAGE) * C::STAGE;
+        if (r == 1 || r > NC) {
+            const int i = r == 1 ? 0 : r - NC;
+            const int row = wm * C::WM + 32 * i + l32;
+            fa[t][i] = *(const half8*)(st + row * 64 + (((2 * t + hi) ^ ((row >> 2) & 3)) << 4));
+        } else {
+            const int c = r == 0 ? 0 : r - 1;
+            const int g = wn * (C::WN / 64) + (c >> 1), j = 2 * (c & 1) + (l32 >> 4);
+            fw[t][c] = *(const half8*)(st + C::A_BYTES + (g * 4 + j) * 1024 + ((2 * t + hi) * 16 + (l & 15)) * 16);
         }
-        __builtin_amdgcn_sched_barrier(0);  // both steps' reads ahead of the MFMAs
+    };
+
+    // Stage 0 is in (this wave's copies: the wait above; every wave's: the barrier).
+    __builtin_amdgcn_s_barrier();
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
+    for (int r = 0; r < NR; r++) rd(0, 0, r);
+
+    // Iteration s: (A) step 0's MFMAs with step 1's reads between them; (B) this wave's copies of
+    // stage s + 1 done (stage s + 2's may stay in flight), then a bare barrier: every wave's are,
+    // and every wave is done with stage s - 1 (its last reads fed MFMAs before the barrier);
+    // (C) step 1's MFMAs with the next stage's step-0 reads and stage s + 3's copies (into stage
+    // s - 1's buffer) between them. A step's fragments are read one MFMA phase before they are
+    // used. (__syncthreads' release fence would wait for all of this wave's copies.)
+    constexpr int NM = MR * NC, PER = C::LOADS, GAP = NM / PER;
+    static_assert(GAP >= 1, "copies per K-16 step");
+    for (int s = 0; s < nkt; s++) {
 #pragma unroll
-            for (int x = 0; x < NM; x++) {
-                const int i = x / NC, c = x % NC;
-                acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[t][c], fa[t][i], acc[i][c], 0, 0, 0);
-                if (x % GAP == GAP - 1 && x / GAP < PER) {
-                    __builtin_amdgcn_sched_barrier(0);
-                    if (more) issue_one(kt3, buf3, t * PER + x / GAP);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
+        for (int x = 0; x < NM; x++) {
+            const int i = x / NC, c = x % NC;
+            __builtin_amdgcn_sched_barrier(0);
+            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[0][c], fa[0][i], acc[i][c], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (x < NR) rd(s, 1, x);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const bool next = s + 1 < nkt;
+        if (next) {
+            if (s + 2 < nkt)
+                wait_vmcnt<C::LOADS>();
+            else
+                wait_vmcnt<0>();
+            __builtin_amdgcn_s_barrier();
+        }
+        const bool more = s + 3 < nkt;
+#pragma unroll
+        for (int x = 0; x < NM; x++) {
+            const int i = x / NC, c = x % NC;
+            __builtin_amdgcn_sched_barrier(0);
+            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[1][c], fa[1][i], acc[i][c], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (next && x < NR) rd(s + 1, 0, x);
+            if (x % GAP == GAP - 1 && x / GAP < PER) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (more) issue_one(s + 3, (s + 3) % C::NSTAGE, x / GAP);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -297,16 +311,17 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
             }
         }
     };
-    RowIn rin[2];
+    RowIn rin[3];  // two row fragments ahead
     load_row(0, rin[0]);
+    if (MR > 1) load_row(1, rin[1]);
 
 #pragma unroll
     for (int i = 0; i < MR; i++) {
         // (scheduling fences: one row fragment's values, addresses and stores at a time)
         __builtin_amdgcn_sched_barrier(0);
-        if (i + 1 < MR) load_row(i + 1, rin[(i + 1) & 1]);
+        if (i + 2 < MR) load_row(i + 2, rin[(i + 2) % 3]);
         __builtin_amdgcn_sched_barrier(0);
-        const RowIn& ri = rin[i & 1];
+        const RowIn& ri = rin[i % 3];
 #pragma unroll
         for (int j = 0; j < NG; j++) {
             const int g = g0 + j;
@@ -317,6 +332,7 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
 #pragma unroll
                 for (int x = 0; x < 16; x++) v[h][x] = acc[i][2 * j + h][x];
             if (EPI & EPI_LN) {
+                const float2 ms = rows_ms[wm * C::WM + 32 * i + l32];  // (mean, rstd)
 #pragma unroll
                 for (int h = 0; h < 2; h++)
 #pragma unroll
@@ -325,7 +341,7 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
                         const float cc[4] = {c4.x, c4.y, c4.z, c4.w};
 #pragma unroll
                         for (int e = 0; e < 4; e++)
-                            v[h][4 * q + e] = rs_[i] * (v[h][4 * q + e] - mu_[i] * cc[e]);
+                            v[h][4 * q + e] = ms.y * (v[h][4 * q + e] - ms.x * cc[e]);
                     }
             }
             if (EPI & EPI_BIAS) {
