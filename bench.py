@@ -1,4 +1,4 @@
-"""Benchmark: the full Julia-1-shaped forward pass (22-layer ModernBERT
+"""Benchmark: the full Julia-1-shaped forward pass (the benchmark's config 4: 22-layer ModernBERT
 encoder, hidden 768, 12 heads, GeGLU 1152, plus the head and scorer; seeded synthetic weights)
 on one 293-token request per step, through the drop-in C ABI (julia_cuda_run), on one MI355X.
 

@@ -314,7 +314,13 @@ __device__ __forceinline__ void epi_load_row(const GemmParams& p, int row, int g
 #pragma unroll
         for (int i = 0; i < EPI_PRE_SLOTS; i++) e.st[i] = load8f<XS>(st + 2 * min(j + 8 * i, slots - 1));
     }
-    if (EPI & EPI_ROPE) e.pos = p.pos ? p.pos[r] : r;
+    if (EPI & EPI_ROPE) {
+        // An unconditional load (from the table itself when there are no positions): a load
+        // under a branch leaves the compiler unsure where it is in the load order, and the
+        // table loads that wait for it would then wait for every load issued before them.
+        const int v = *(const int*)(p.pos ? (const void*)(p.pos + r) : (const void*)p.rope);
+        e.pos = p.pos ? v : r;
+    }
     if ((EPI & EPI_RES) && !(EPI & EPI_GEGLU)) {
         const f16* x = (const f16*)(p.res ? p.res : p.c) + (size_t)r * p.n + grp * 64 + c0;
         e.rl = load8h<XR>(x);

@@ -26,9 +26,11 @@
 namespace jh {
 
 // ---------------------------------------------------------------------------------------------
-// gemm_lat: grid = tiles_n * tiles_m * splits blocks (1-D, XCD-mapped), 256 threads.
+// gemm_lat: grid = tiles_n * tiles_m * splits blocks (1-D, XCD-mapped), 256 threads, at most 256
+// registers a lane so that two blocks share a CU (a CU with two tiles overlaps one's loads with
+// the other's MFMAs and epilogue).
 template <int BM, int EPI>
-__global__ __launch_bounds__(256) void gemm_lat(GemmParams p) {
+__global__ __launch_bounds__(256, 2) void gemm_lat(GemmParams p) {
     __shared__ __attribute__((aligned(16))) float red[lat_lds_floats<BM>()];
     __shared__ uint32_t s_last;
     gemm_lat_tile<BM, EPI>(p, blockIdx.x, red, &s_last);
@@ -76,7 +78,7 @@ void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
     if (g.m <= 0) fail("no rows");
     if (g.n <= 0 || g.n % 64) fail("n = " + std::to_string(g.n) + " is not a multiple of 64");
     const bool tput = cfg.bm >= 128;
-    if (!(cfg.bm == 16 || cfg.bm == 32 || cfg.bm == 64 || cfg.bm == 128 || cfg.bm == 256))
+    if (!(cfg.bm == 16 || cfg.bm == 32 || cfg.bm == 48 || cfg.bm == 64 || cfg.bm == 128 || cfg.bm == 256))
         fail("no tile height " + std::to_string(cfg.bm));
     if (tput && g.n % cfg.bm) fail("the " + cfg_str(cfg) + " tiles need n % " + std::to_string(cfg.bm) + " == 0");
     if (tput && cfg.splits != 1) fail("the " + cfg_str(cfg) + " tiles take no K split");
@@ -112,6 +114,8 @@ void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
     if ((g.epi & EPI_GEGLU) && (g.epi & (EPI_RES | EPI_STATS | EPI_ROPE)))
         fail("GeGLU does not combine with a residual, statistics or RoPE");
     if (stats && (g.stats_out == g.stats_in)) fail("stats_out may not alias stats_in");
+    if (!tput && ksteps / cfg.splits < 4)  // each of the four waves takes a K step of every split
+        fail(std::to_string(cfg.splits) + " splits leave a wave no K step of " + std::to_string(ksteps));
 }
 
 template <int BM, int EPI>
@@ -134,6 +138,7 @@ static void launch_epi(const GemmParams& p, int bm, hipStream_t st) {
     switch (bm) {
         case 16: launch_one<16, EPI>(p, st); break;
         case 32: launch_one<32, EPI>(p, st); break;
+        case 48: launch_one<48, EPI>(p, st); break;
         case 64: launch_one<64, EPI>(p, st); break;
         case 128: launch_one<128, EPI>(p, st); break;
         default: launch_one<256, EPI>(p, st); break;
@@ -169,32 +174,25 @@ void gemm_launch(const Gemm& g, GemmConfig cfg, const Scratch& s, hipStream_t st
         throw std::runtime_error(std::string("gemm (") + cfg_str(cfg) + "): " + hipGetErrorString(e));
 }
 
-// The tiling for one request's GEMMs on a 256-CU GPU. Small M is latency-bound: what matters is
-// the longest chain of dependent K steps on the busiest CU. The model: a latency-kernel task
-// costs a fixed part plus a part per K step of its wave (K / 32 / 4 / splits steps), growing a
-// little with the tile height; tasks fill the CUs in rounds; split-K adds a reduction. Large M
-// goes to the throughput kernel's 128- or 256-row tiles.
+// The tiling for one request's GEMMs on a 256-CU GPU. Small M is bound by how fast a CU takes in
+// its tiles' operands: the model is a fixed ~4 us (launch, first round trip, reduction,
+// epilogue) plus the busiest CU's operand bytes, ceil(tiles / CUs) x (BM + 64) x K x 2, at about
+// 55 GB/s into one CU (measured on MI355X: 48-row tiles for qkv and wi at 293 tokens, 16-row for
+// wo and wo_mlp, 32-row from ~400 tokens up). Ties go to the shorter tile. Large M goes to the
+// throughput kernel's 128 x 128 or 256 x 256 tiles.
 GemmConfig gemm_choose(int m, int n, int k, int cus) {
     if (cus <= 0) cus = 256;
     if (m >= 2048 && n % 128 == 0 && k % 64 == 0) {
-        const long t256 = (long)(n / 128) * ((m + 255) / 256);
+        const long t256 = (n % 256 == 0) ? (long)(n / 256) * ((m + 255) / 256) : 0;
         return GemmConfig{t256 >= cus ? 256 : 128, 1};
     }
-    GemmConfig best{64, 1};
+    GemmConfig best{32, 1};
     double best_cost = 1e30;
-    const int units = k / 32;
-    for (int bm : {16, 32, 64}) {
-        for (int s = 1; s <= 4; s++) {
-            if (units / (4 * s) < 2) continue;
-            const long tasks = (long)(n / 64) * ((m + bm - 1) / bm) * s;
-            const int per_cu = bm == 64 ? 2 : 4;  // resident tiles per CU (LDS, waves)
-            const long rounds = (tasks + (long)cus * per_cu - 1) / ((long)cus * per_cu);
-            const double busy = (double)std::min<long>(tasks, (long)cus * per_cu) / cus;
-            const double steps = (double)units / (4.0 * s);
-            const double task = 2.0 + steps * (0.12 + 0.03 * (bm / 16)) * (0.75 + 0.25 * busy);
-            double cost = (double)rounds * task + (s > 1 ? 1.0 + 0.1 * s : 0.0);
-            if (cost < best_cost - 1e-9) best_cost = cost, best = GemmConfig{bm, s};
-        }
+    for (int bm : {16, 32, 48, 64}) {
+        const long tiles = (long)(n / 64) * ((m + bm - 1) / bm);
+        const long per_cu = (tiles + cus - 1) / cus;
+        const double cost = 4.0 + (double)per_cu * (bm + 64) * k * 2 / 55e3;
+        if (cost < best_cost - 0.05) best_cost = cost, best = GemmConfig{bm, 1};
     }
     return best;
 }

@@ -440,6 +440,9 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
             }
         }
     }
+    // Every wave is done with the LDS before the block's next task (the persistent kernel runs
+    // several in a row) copies into it.
+    __syncthreads();
     mark(3);
 }
 

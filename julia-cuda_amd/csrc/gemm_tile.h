@@ -1,7 +1,9 @@
-// One output tile of the latency GEMM (BM = 16/32/64 rows x 64 columns), as a device function:
+// One output tile of the latency GEMM (BM = 16/32/48/64 rows x 64 columns), as a device function:
 // the body of the per-GEMM `gemm_lat` kernels and a task of the persistent layer kernel, which
 // pass their own LDS. See gemm.hip for the design.
 #pragma once
+
+#include <type_traits>
 
 #include "device.h"
 
@@ -80,14 +82,19 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
 // `red` right after.
 template <int BM, int EPI, bool XG = false>
 __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, float* red,
-                                              uint32_t* s_last) {
+                                              uint32_t* s_last, uint64_t* sub = nullptr) {
+    auto mark = [&](int i) {  // profiling: thread 0's view of the task's stages
+        if (sub && threadIdx.x == 0) sub[i] = wall_clock64();
+    };
+    mark(0);
     constexpr int MI = BM / 16;
     constexpr int NPASS = (BM + 31) / 32;
     const int T = p.tiles_n * p.tiles_m * p.splits;
     const int L = xcd_task(task, T);
     const int z = L % p.splits, t2 = L / p.splits;
     const int by = t2 % p.tiles_m, bx = t2 / p.tiles_m;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g = l >> 4;
+    const int tid = threadIdx.x, l = tid & 63, r16 = l & 15, g = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
 
     // This block's K steps (32 wide), then this wave's quarter of them.
     const int U = p.k >> 5;
@@ -95,17 +102,11 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     const int u0 = ub + w * nu / 4, u1 = ub + (w + 1) * nu / 4;
 
     const f16* ap[MI];
-    const f16* wp[4];
 #pragma unroll
     for (int i = 0; i < MI; i++) {
         const int row = min(by * BM + 16 * i + r16, p.m - 1);  // rows past m: read, never stored
         ap[i] = (const f16*)p.a + (size_t)row * p.k + 8 * g;
     }
-    // w in fragment order: unit uu's fragment j is 512 values at ((bx U + uu) 4 + j) 512, and
-    // lane l's 8 of them at l * 8 (W rows bx 64 + 16 j + l % 16, K 32 uu + 8 (l / 16) + e).
-#pragma unroll
-    for (int j = 0; j < 4; j++) wp[j] = (const f16*)p.w + ((size_t)bx * U * 4 + j) * 512 + l * 8;
-
     // The epilogue's other inputs, in flight with the first operand loads.
     const int c0 = (tid & 7) * 4;
     EpiCol ec;
@@ -113,8 +114,6 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     epi_load_col<EPI>(p, bx, c0, ec);
 #pragma unroll
     for (int ps = 0; ps < NPASS; ps++) epi_load_row<EPI, XG>(p, by * BM + ps * 32 + (tid >> 3), bx, c0, er[ps]);
-#pragma unroll
-    for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, c0, er[ps]);
 
     floatx4 acc[MI][4];
 #pragma unroll
@@ -122,39 +121,79 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // The wave's K steps in chunks of up to UMAX, each chunk's fragments all loaded before its
-    // MFMAs: a small tile's K loop is latency-bound, so one round trip per chunk instead of one
-    // per step. The a operand (an activation) comes through the coherent path when XG.
+    // The wave's K steps in chunks of UC, two chunks in flight: chunk c + 1's fragments load
+    // while chunk c's MFMAs run, so a wave pays one round trip to memory however many chunks its
+    // K range takes. The a operand (an activation) comes through the coherent path when XG.
     //
-    // The loads are unconditional (a step past the wave's range re-reads its last step, and its
-    // a fragment is masked to zero without a branch): a guarded load becomes a branch, and the
-    // compiler drains every outstanding load at each branch, which would serialise the steps.
-    constexpr int UMAX = MI == 1 ? 9 : (MI == 2 ? 6 : 4);
-    for (int u = u0; u < u1; u += UMAX) {
-        half8 fa[UMAX][MI], fw[UMAX][4];
+    // The loads are unconditional within a chunk (a step past the wave's range re-reads its last
+    // step, and its a fragment is masked to zero without a branch): a guarded load becomes a
+    // branch, and the compiler drains every outstanding load at each divergent branch, which would
+    // serialise the steps. The chunk guards depend on the wave index only (scalar branches).
+    // UC K steps a chunk (2 x UC x (MI + 4) x 4 VGPRs of fragments): four, three or two; five for
+    // 16-row tiles whose waves have more than eight K steps (K = 1152), which then take one round
+    // trip instead of two.
+    auto kloop = [&](auto uc_) {
+        constexpr int UC = decltype(uc_)::value;
+        half8 fa0[UC][MI], fw0[UC][4], fa1[UC][MI], fw1[UC][4];
+        // w in fragment order: unit uu's fragment j is 512 values at ((bx U + uu) 4 + j) 512,
+        // and lane l's 8 of them at l * 8 (W rows bx 64 + 16 j + l % 16, K 32 uu + 8 (l / 16) +
+        // e); read through a buffer descriptor over exactly the wave's K steps: a slot past them
+        // reads zeros without touching memory (a clamped re-read would still cost its bytes).
+        const auto wr = buffer_rsrc((const f16*)p.w + ((size_t)bx * U + u0) * 2048,
+                                    (uint32_t)(u1 - u0) * 4096);
+        auto load = [&](half8 (&fa)[UC][MI], half8 (&fw)[UC][4], int u) {
 #pragma unroll
-        for (int s = 0; s < UMAX; s++) {
-            const int uu = min(u + s, u1 - 1);
+            for (int s = 0; s < UC; s++) {
+                const int uu = min(u + s, u1 - 1);
 #pragma unroll
-            for (int j = 0; j < 4; j++) fw[s][j] = *(const half8*)(wp[j] + (size_t)uu * 2048);
+                for (int j = 0; j < 4; j++)
+                    fw[s][j] = bload16<false>(wr, (uint32_t)(u + s - u0) * 4096 + j * 1024 + l * 16);
 #pragma unroll
-            for (int i = 0; i < MI; i++) fa[s][i] = load16h<XG>(ap[i] + uu * 32);
-        }
-        // Keep the scheduler from interleaving the MFMAs into the loads (it would reuse the
-        // fragment registers and wait for each step's loads before issuing the next).
+                for (int i = 0; i < MI; i++) fa[s][i] = load16h<XG>(ap[i] + uu * 32);
+            }
+        };
+        auto compute = [&](const half8 (&fa)[UC][MI], const half8 (&fw)[UC][4], int u) {
+#pragma unroll
+            for (int s = 0; s < UC; s++) {
+                const uint32_t keep = u + s < u1 ? 0xffffffffu : 0u;
+#pragma unroll
+                for (int i = 0; i < MI; i++) {
+                    const half8 a = mask16(fa[s][i], keep);
+#pragma unroll
+                    for (int j = 0; j < 4; j++) acc[i][j] = mfma16(fw[s][j], a, acc[i][j]);
+                }
+            }
+        };
+        // (Scheduling fences keep the compiler from interleaving the MFMAs into the loads, where
+        // it would reuse the fragment registers and wait for each step's loads before the next.)
+        // The first two chunks unconditionally (every wave has a K step: the host checks; a slot
+        // past the wave's range re-reads its last a step and reads zeros of w), so that the
+        // compiler knows where the position loads stand in the load order when the table loads
+        // wait for them.
+        load(fa0, fw0, u0);
+        load(fa1, fw1, u0 + UC);
+        // The RoPE table rows after the operand loads: they wait for the positions, and issued
+        // first that wait would hold back the operand loads by a round trip.
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < UMAX; s++) {
-            const uint32_t keep = u + s < u1 ? 0xffffffffu : 0u;
-#pragma unroll
-            for (int i = 0; i < MI; i++) {
-                const half8 a = mask16(fa[s][i], keep);
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = mfma16(fw[s][j], a, acc[i][j]);
-            }
+        for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, c0, er[ps]);
+        for (int u = u0; u < u1; u += 2 * UC) {
+            __builtin_amdgcn_sched_barrier(0);
+            compute(fa0, fw0, u);
+            __builtin_amdgcn_sched_barrier(0);
+            if (u + 2 * UC < u1) load(fa0, fw0, u + 2 * UC);
+            __builtin_amdgcn_sched_barrier(0);
+            if (u + UC < u1) compute(fa1, fw1, u + UC);
+            __builtin_amdgcn_sched_barrier(0);
+            if (u + 3 * UC < u1) load(fa1, fw1, u + 3 * UC);
         }
-    }
+    };
+    if (MI == 1 && u1 - u0 > 8)
+        kloop(std::integral_constant<int, 5>{});
+    else
+        kloop(std::integral_constant<int, MI == 1 ? 4 : (MI == 2 ? 3 : 2)>{});
 
+    mark(1);
     // acc[i][j] lane: row 16 i + r16, columns 16 j + 4 g + e of the tile. Wave w's partial at
     // red[w][row][col] (rows of 68 floats).
 #pragma unroll
@@ -181,7 +220,9 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
         }
     }
     __syncthreads();  // red is free again
+    mark(2);
     finish<NPASS, EPI, XG>(p, v, bx * p.tiles_m + by, z, by * BM, bx, BM, s_last, ec, er);
+    mark(3);
 }
 
 // ---- the persistent kernel's tile: weights staged in LDS --------------------------------------

@@ -20,6 +20,7 @@
 #include <string>
 
 #include "attn_tile.h"
+#include "gemm_big.h"
 #include "gemm_tile.h"
 #include "layer.h"
 
@@ -144,7 +145,7 @@ __device__ __forceinline__ GemmParams make_gemm(const EncParams& P, int g, const
         p.a = P.mid, p.w = L.wo_mlp, p.c = x_out_of(P, l), p.res = x_attn_of(P, l);
         p.n = P.d, p.k = P.inter, p.stats_out = P.stats_mlp;
     }
-    p.tiles_n = p.n >> 6;
+    p.tiles_n = p.n / (P.bm[g] >= 128 ? 128 : 64);
     p.tiles_m = (P.m + P.bm[g] - 1) / P.bm[g];
     return p;
 }
@@ -153,6 +154,8 @@ __device__ __forceinline__ int gemm_tasks(const GemmParams& g) {
     return g.tiles_n * g.tiles_m * g.splits;
 }
 
+// bm 16/32/64: the latency tile with its weights in LDS; 128: the throughput tile (128 x 128,
+// large batches), which stages both operands itself.
 template <int EPI, bool AX>
 __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* lds, bool pre,
                                            uint32_t* s_last, uint64_t* sub) {
@@ -161,7 +164,9 @@ __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* ld
         const bool first = t == (int)blockIdx.x;
         const bool ready = pre && first;
         uint64_t* su = first ? sub : nullptr;
-        if (bm == 16)
+        if (bm == 128)
+            gemm_big_tile<128, 128, EPI, AX, true>(g, t, lds, su);
+        else if (bm == 16)
             gemm_w_tile<16, EPI, AX>(g, t, lds, ready, s_last, su);
         else if (bm == 32)
             gemm_w_tile<32, EPI, AX>(g, t, lds, ready, s_last, su);
@@ -188,6 +193,8 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
     auto fetch_first = [wl](const GemmParams& g) {
         return [&g, wl] { w_tile_fetch(g, w_tile_of(g, blockIdx.x), wl, 1); };
     };
+    // A block fetches its first weight tile during the barrier (latency tiles only).
+    auto prefetch = [&](const GemmParams& g, int bm) { return bm < 128 && (int)blockIdx.x < gemm_tasks(g); };
 
     LayerDesc L = P.layers[P.first];
     GemmParams gq = make_gemm(P, 0, L, P.first);
@@ -230,7 +237,7 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
             }
             stamp_end(prof, 1);
             if (on(2)) {
-                pre = (int)blockIdx.x < gemm_tasks(go);
+                pre = prefetch(go, P.bm[1]);
                 if (pre) sync(fetch_first(go)); else sync(nothing);
             }
         }
@@ -240,7 +247,7 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
             pre = false;
             stamp_end(prof, 2);
             if (on(3)) {
-                pre = (int)blockIdx.x < gemm_tasks(gi);
+                pre = prefetch(gi, P.bm[2]);
                 if (pre) sync(fetch_first(gi)); else sync(nothing);
             }
         }
@@ -250,7 +257,7 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
             pre = false;
             stamp_end(prof, 3);
             if (on(4)) {
-                pre = (int)blockIdx.x < gemm_tasks(gm);
+                pre = prefetch(gm, P.bm[3]);
                 if (pre) sync(fetch_first(gm)); else sync(nothing);
             }
         }
@@ -263,7 +270,7 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
         if (li + 1 < P.count) {  // whole layers only (the host checks)
             L = P.layers[l + 1];
             gq = make_gemm(P, 0, L, l + 1);
-            pre = (int)blockIdx.x < gemm_tasks(gq);
+            pre = prefetch(gq, P.bm[0]);
             if (pre) sync(fetch_first(gq)); else sync(nothing);
         }
     }
@@ -295,7 +302,8 @@ int LayerKernel::lds_bytes(const LayerPlan& plan, int d, int inter, int m, int w
     int b = std::max({ATT_LDS_F16 * 2, att_lds_bytes(attention_gkeys(m, 0)),
                       att_lds_bytes(attention_gkeys(m, window))});
     for (int g = 0; g < 4; g++)
-        b = std::max({b, w_tile_bytes(ks[g], plan.splits[g]), red_bytes(plan.bm[g])});
+        b = plan.bm[g] >= 128 ? std::max(b, Big<128, 128>::LDS_BYTES)
+                              : std::max({b, w_tile_bytes(ks[g], plan.splits[g]), red_bytes(plan.bm[g])});
     return (b + 15) / 16 * 16;
 }
 
@@ -327,6 +335,12 @@ LayerPlan LayerKernel::default_plan(int m, int d, int inter) const {
     shapes(d, inter, cols, ks);
     const double bw = 67e3;  // bytes per us into one CU
     for (int g = 0; g < 4; g++) {
+        // Large batches: the throughput tile (the per-step chooser's threshold).
+        if (m >= 2048 && cols[g] % 128 == 0 && ks[g] % 32 == 0 && ks[g] <= 128 * BIG_LN_SLOTS &&
+            Big<128, 128>::LDS_BYTES <= lds_max_) {
+            p.bm[g] = 128, p.splits[g] = 1;
+            continue;
+        }
         double best = 1e30;
         p.bm[g] = 16, p.splits[g] = ks[g] / 32 >= 8 ? 2 : 1;
         for (int bm : {16, 32, 64}) {
@@ -376,7 +390,8 @@ int LayerKernel::grid(const LayerArgs& a, const LayerPlan& plan) const {
     long most = (long)((a.m + 15) / 16) * (a.d / 64);  // attention slices
     most = std::max(most, (long)((a.m + 63) / 64) * (a.d / 64) * std::max(plan.kv[0], plan.kv[1]));
     for (int g = 0; g < 4; g++)
-        most = std::max(most, (long)(cols[g] / 64) * ((a.m + plan.bm[g] - 1) / plan.bm[g]) * plan.splits[g]);
+        most = std::max(most, (long)(cols[g] / (plan.bm[g] >= 128 ? 128 : 64)) *
+                                  ((a.m + plan.bm[g] - 1) / plan.bm[g]) * plan.splits[g]);
     // Enough blocks for the largest phase's tasks in one round if they fit (a multiple of 8, so
     // that the task-to-XCD map is even), else every resident block.
     const long grid = std::min<long>((long)per_cu_ * cus_, (most + 7) / 8 * 8);
@@ -392,8 +407,8 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
     if (phases == 0 || phases > 0x1f) fail("no phases selected");
     if (phases != 0x1f && a.count != 1) fail("a subset of the phases runs one layer only");
     for (int g = 0; g < 4; g++)
-        if (!(plan.bm[g] == 16 || plan.bm[g] == 32 || plan.bm[g] == 64) || plan.splits[g] < 1 ||
-            plan.splits[g] > 4)
+        if (!(plan.bm[g] == 16 || plan.bm[g] == 32 || plan.bm[g] == 64 || plan.bm[g] == 128) ||
+            plan.splits[g] < 1 || plan.splits[g] > 4 || (plan.bm[g] == 128 && plan.splits[g] != 1))
             fail("no such plan: " + plan.str());
     if (plan.kv[0] < 1 || plan.kv[0] > 8 || plan.kv[1] < 1 || plan.kv[1] > 8)
         fail("no such plan: " + plan.str());

@@ -152,7 +152,7 @@ def test_run_errors(small):
 
 
 def test_batched_encoder_matches_each_request(torch_cuda):
-    """Config 5's batched variant (SURVEY 0.4): requests concatenated into one set of rows,
+    """Config 5's batched variant: requests concatenated into one set of rows,
     positions restarting in every request and attention kept within each, give every request its
     own encoder output: against the request run alone (per-step kernels) and against the f32
     oracle. The batch passes 2048 rows, so the per-step path takes the throughput GEMMs."""

@@ -2,7 +2,7 @@
 _norm_add / _score), against the CPU oracle on the same seeded inputs: the f32 reference over
 unfolded weights (LayerNorms in f64) and the f16 emulation of each kernel's arithmetic.
 
-The configurations are BASELINE.json's: config 1 (the fused qkv GEMM `gemm_lnrope`, M=293,
+The configurations are the benchmark's: config 1 (the fused qkv GEMM `gemm_lnrope`, M=293,
 K=768, N=2304, RoPE theta 160000), config 2 (wo / wi / wo_mlp at M=512, every tile height and
 split-K), config 3 (attention, 12 heads x 64, n in {72, 293, 1024}, global and +-64 window),
 plus the head's four epilogues, the bandwidth kernels, and MFMA-bound shapes (M >= 4096)."""
@@ -316,6 +316,10 @@ def test_gemm_rejects_bad_shapes(torch_cuda, scratch):
                         stats_out=c.data_ptr())
     with pytest.raises(jh.JuliaHipError, match="multiple of 64"):
         jh.gemm(args, 32, 1, scratch)
+    args = jh.gemm_args("resstats", a.data_ptr(), w.data_ptr(), c.data_ptr(), 64, 64, 64,
+                        stats_out=c.data_ptr())
+    with pytest.raises(jh.JuliaHipError, match="leave a wave no K step"):
+        jh.gemm(args, 32, 1, scratch)  # k = 64: two K steps for four waves
     args = jh.gemm_args("lnrope", a.data_ptr(), w.data_ptr(), c.data_ptr(), 64, 64, 64)
     with pytest.raises(jh.JuliaHipError, match="LayerNorm inputs"):
         jh.gemm(args, 32, 1, scratch)

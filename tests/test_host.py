@@ -204,8 +204,20 @@ def test_reference_choose_rule():
 @pytest.mark.parametrize("n,k", [(2304, 768), (768, 768), (768, 1152), (1536, 768)])
 def test_chooser_picks_valid_configs(m, n, k):
     bm, sp = jh.gemm_choose(m, n, k, 256)
-    assert bm in (16, 32, 64, 128, 256)
+    assert bm in (16, 32, 48, 64, 128, 256)
     if bm >= 128:
-        assert n % 128 == 0 and sp == 1
+        assert n % bm == 0 and sp == 1
     else:
         assert 1 <= sp <= 4 and (k // 32) // (4 * sp) >= 2
+
+
+def test_chooser_matches_the_measured_winners():
+    """The latency tiles' picks at the request lengths measured on MI355X (per-step GEMM times,
+    the fastest tile height within ~0.2 us): qkv/wi 48 rows at 293 tokens and 32 at 1024, wo and
+    wo_mlp 16 rows at 293."""
+    assert jh.gemm_choose(293, 2304, 768, 256)[0] == 48
+    assert jh.gemm_choose(293, 768, 768, 256)[0] == 16
+    assert jh.gemm_choose(293, 768, 1152, 256)[0] == 16
+    assert jh.gemm_choose(448, 768, 768, 256)[0] == 32
+    assert jh.gemm_choose(18752, 2304, 768, 256) == (256, 1)
+    assert jh.gemm_choose(4096, 768, 768, 256) == (128, 1)
