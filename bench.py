@@ -11,7 +11,9 @@ persistent layer kernel; it also carries
   - `cpu_baseline`: the f32 CPU oracle (oracle/liboracle.so) on the box's host cores, on a
     bounded sample of the same workload,
   - config 4's latency distribution (mean, p50, p99 over seeded request lengths 72-1024),
-  - config 5's persistent layer kernel at 448 tokens.
+  - config 5: the persistent layer kernel at 448 tokens, and the batched variant (64 requests of
+    config 4's lengths concatenated, ~18.8k rows) through both paths, with per-phase GPU time,
+    TFLOP/s and fraction of f16 MFMA peak.
 """
 
 import argparse
@@ -79,6 +81,37 @@ STEP_SHAPES = {  # step: (n, k, epilogue, count per forward)
 def attention_flops(n, window):
     pairs = n * n if window == 0 else sum(min(n, i + window + 1) - max(0, i - window) for i in range(n))
     return 4 * 64 * H * pairs
+
+
+def config5_batched(lens, seed=55):
+    """Config 5's batched variant: the requests concatenated (positions restarting, attention
+    within each), the encoder through the per-step kernels and the persistent kernel; per-phase
+    GPU ms of the per-step path with TFLOP/s and fraction of f16 MFMA peak."""
+    rng = np.random.default_rng(seed)
+    seqs = [rng.integers(0, VOCAB, int(n)).astype(np.uint32) for n in lens]
+    rows = int(sum(lens))
+    eng = jh.Engine(f"synthetic:batch_rows={rows}", max_length=1024)
+    res = {"requests": len(lens), "rows": rows}
+    for fused in (False, True):
+        eng.encode_batch(seqs, layer_fused=fused, want_x=False)
+        ms = [eng.encode_batch(seqs, layer_fused=fused, want_x=False)[1] for _ in range(3)]
+        res["layer_kernel_ms" if fused else "per_step_ms"] = round(float(np.median(ms)), 3)
+    ph = eng.encode_batch_phases(seqs)
+    eng.close()
+    n_glob = sum(1 for l in range(L) if l % 3 == 0)  # every third layer global
+    flops = {s: 2 * rows * n * k * L for s, (n, k, _, _) in STEP_SHAPES.items()}
+    flops["attention"] = sum(n_glob * attention_flops(int(n), 0) + (L - n_glob) * attention_flops(int(n), 64)
+                             for n in lens)
+    phases = {}
+    for s, ms in ph.items():
+        tf = flops[s] / (ms * 1e-3) / 1e12
+        phases[s] = {"ms": round(ms, 3), "TFLOPs": round(tf, 1), "frac_peak": round(tf * 1e12 / PEAK_F16, 4)}
+    res["phases_per_step"] = phases
+    gemm_fl = sum(flops[s] for s in STEP_SHAPES)
+    gemm_ms = sum(ph[s] for s in STEP_SHAPES)
+    res["gemm_TFLOPs"] = round(gemm_fl / (gemm_ms * 1e-3) / 1e12, 1)
+    res["gemm_frac_peak"] = round(gemm_fl / (gemm_ms * 1e-3) / PEAK_F16, 4)
+    return res
 
 
 def main():
@@ -170,11 +203,12 @@ def main():
         if v.get("flops"):
             v["TFLOPs"] = round(v["flops"] / (v["us"] * 1e-6) / 1e12, 2)
     out["kernels_293"] = kern
-    dom = max((k for k in STEP_SHAPES), key=lambda s: kern[s]["total_us"])
+    # The roofline kernel: config 1's fused qkv GEMM (with wi the largest share of the forward).
+    dom = "qkv"
     dk = kern[dom]
     n, k, epi, _ = STEP_SHAPES[dom]
     bm = dk["config"][0]
-    kname = f"gemm_{'lat' if bm < 128 else 'tput'}<{bm}, {jh.EPI[epi]}>"
+    kname = f"gemm_{'lat' if bm < 128 else 'big'}<{bm}, {jh.EPI[epi]}>"
     # HBM bytes per dispatch from the committed rocprofv3 counter passes (FETCH_SIZE and
     # WRITE_SIZE, scaled by the library's copy kernel: profiles/traffic_<step>_293.*), when they
     # are of this kernel.
@@ -226,6 +260,8 @@ def main():
     out["config5_448"] = {"per_step_ms": round(float(np.mean(ms_s)), 4),
                           "layer_kernel_ms": round(float(np.mean(ms_f)), 4)}
     eng_big.close()
+    out["config5_batched"] = config5_batched(lengths(np.random.default_rng(4), 64))  # config 4's requests
+    log("config 5 batched:", json.dumps(out["config5_batched"]))
 
     # ---- config 4's latency distribution ----
     lens = lengths(np.random.default_rng(4), 64)

@@ -230,6 +230,12 @@ int julia_hip_encode_batch(const Engine *e, size_t b, const uint32_t *ids, const
                            int layer_fused, uint16_t *x_out, float *gpu_ms, char *err,
                            size_t err_len);
 
+/* The same batch through the per-step kernels with a HIP event between every two steps: the GPU
+ * ms of each step summed over the layers, phase_ms[5] = qkv, attention, wo, wi, wo_mlp (config
+ * 5's per-phase timings; the reference's --layer-fused profile is src/profile.rs). */
+int julia_hip_encode_batch_phases(const Engine *e, size_t b, const uint32_t *ids,
+                                  const size_t *lens, float *phase_ms, char *err, size_t err_len);
+
 /* One request with the residual stream copied out after every encoder layer (x_trace, f16 bits
  * [layers][n][d], nullable) and the head's stream after its last layer (head_x, [n][d],
  * nullable): for step-by-step parity checks. */

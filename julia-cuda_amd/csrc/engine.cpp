@@ -120,24 +120,65 @@ struct Engine {
     // wo (+ residual, statistics into stats_a), wi (LayerNorm from stats_a, GeGLU), wo_mlp
     // (+ residual, statistics into stats_b). pos and seg (nullable): concatenated requests' row
     // positions and sequence bounds.
-    void launch_layer(int l, int n, const int32_t* pos = nullptr, const int32_t* seg = nullptr) {
+    // ev (profiling): six events, recorded before each of the five steps and after the last.
+    void launch_layer(int l, int n, const int32_t* pos = nullptr, const int32_t* seg = nullptr,
+                      hipEvent_t* ev = nullptr) {
         const EncoderLayer& L = layout.layers[l];
         const int d = cfg.d, I = cfg.inter;
         const float* rope = f(L.global ? layout.rope_global : layout.rope_local);
+        auto mark = [&](int i) {
+            if (ev) hip_check(hipEventRecord(ev[i], stream), "hipEventRecord");
+        };
+        mark(0);
         if (L.qkv_colsum.present)
             gemm(EPI_K_LNROPE, x, h(L.wqkv), qkv, n, 3 * d, d, stats_b, f(L.qkv_colsum),
                  cfg.norm_eps, nullptr, rope, nullptr, pos);
         else
             gemm(EPI_K_ROPE, x, h(L.wqkv), qkv, n, 3 * d, d, nullptr, nullptr, 0.0f, nullptr, rope,
                  nullptr, pos);
+        mark(1);
         const int window = L.global ? 0 : cfg.window;
         attention_launch(qkv, o, n, d, window, attention_chunks(n, d, window, cus), scratch, stream,
                          seg);
+        mark(2);
         gemm(EPI_K_RESSTATS, o, h(L.wo), x, n, d, d, nullptr, nullptr, 0.0f, nullptr, nullptr, stats_a);
+        mark(3);
         gemm(EPI_K_LNGEGLU, x, h(L.wi), mid, n, 2 * I, d, stats_a, f(L.wi_colsum), cfg.norm_eps,
              nullptr, nullptr, nullptr);
+        mark(4);
         gemm(EPI_K_RESSTATS, mid, h(L.wo_mlp), x, n, d, I, nullptr, nullptr, 0.0f, nullptr, nullptr,
              stats_b);
+        mark(5);
+    }
+
+    // Config 5's batched input: the sequences' ids, positions restarting per sequence, and each
+    // row's sequence bounds, on the device. Returns the rows.
+    int prepare_batch(size_t b, const uint32_t* ids, const size_t* lens) {
+        if (b == 0 || !ids || !lens) throw std::runtime_error("no requests");
+        size_t n = 0;
+        for (size_t i = 0; i < b; i++) {
+            if (lens[i] == 0 || lens[i] > (size_t)max_length)
+                throw std::runtime_error("sequence " + std::to_string(i) + ": " +
+                                         std::to_string(lens[i]) + " tokens, not 1 to " +
+                                         std::to_string(max_length));
+            n += lens[i];
+        }
+        if (n > (size_t)rows)
+            throw std::runtime_error(std::to_string(n) + " rows are over the engine's " +
+                                     std::to_string(rows) + " (load with batch_rows)");
+        for (size_t j = 0; j < n; j++)
+            if (ids[j] >= (uint32_t)cfg.vocab)
+                throw std::runtime_error("token id " + std::to_string(ids[j]) + " is past the vocabulary");
+        std::vector<int32_t> pos(n), seg(2 * n);
+        for (size_t i = 0, r0 = 0; i < b; r0 += lens[i], i++)
+            for (size_t r = r0; r < r0 + lens[i]; r++) {
+                pos[r] = (int32_t)(r - r0);
+                seg[2 * r] = (int32_t)r0, seg[2 * r + 1] = (int32_t)(r0 + lens[i]);
+            }
+        hip_check(hipMemcpy(bids_d, ids, n * 4, hipMemcpyHostToDevice), "ids");
+        hip_check(hipMemcpy(pos_d, pos.data(), n * 4, hipMemcpyHostToDevice), "positions");
+        hip_check(hipMemcpy(seg_d, seg.data(), n * 8, hipMemcpyHostToDevice), "sequences");
+        return (int)n;
     }
 
     // The persistent encoder kernel: layers [first, first + count) as one cooperative launch,
@@ -938,31 +979,8 @@ int julia_hip_encode_batch(const Engine* ce, size_t b, const uint32_t* ids, cons
         if (!ce) throw std::runtime_error("no engine");
         Engine& e = *const_cast<Engine*>(ce);
         hip_check(hipSetDevice(e.device), "hipSetDevice");
-        if (b == 0 || !ids || !lens) throw std::runtime_error("no requests");
-        size_t rows = 0;
-        for (size_t i = 0; i < b; i++) {
-            if (lens[i] == 0 || lens[i] > (size_t)e.max_length)
-                throw std::runtime_error("sequence " + std::to_string(i) + ": " +
-                                         std::to_string(lens[i]) + " tokens, not 1 to " +
-                                         std::to_string(e.max_length));
-            rows += lens[i];
-        }
-        if (rows > (size_t)e.rows)
-            throw std::runtime_error(std::to_string(rows) + " rows are over the engine's " +
-                                     std::to_string(e.rows) + " (load with batch_rows)");
-        for (size_t j = 0; j < rows; j++)
-            if (ids[j] >= (uint32_t)e.cfg.vocab)
-                throw std::runtime_error("token id " + std::to_string(ids[j]) + " is past the vocabulary");
-        std::vector<int32_t> pos(rows), seg(2 * rows);
-        for (size_t i = 0, r0 = 0; i < b; r0 += lens[i], i++)
-            for (size_t r = r0; r < r0 + lens[i]; r++) {
-                pos[r] = (int32_t)(r - r0);
-                seg[2 * r] = (int32_t)r0, seg[2 * r + 1] = (int32_t)(r0 + lens[i]);
-            }
-        hip_check(hipMemcpy(e.bids_d, ids, rows * 4, hipMemcpyHostToDevice), "ids");
-        hip_check(hipMemcpy(e.pos_d, pos.data(), rows * 4, hipMemcpyHostToDevice), "positions");
-        hip_check(hipMemcpy(e.seg_d, seg.data(), rows * 8, hipMemcpyHostToDevice), "sequences");
-        const int n = (int)rows;
+        const int n = e.prepare_batch(b, ids, lens);
+        const size_t rows = (size_t)n;
         hip_check(hipEventRecord(e.ev_start[0], e.stream), "hipEventRecord");
         embed_launch(e.bids_d, n, e.h(e.layout.tok_embeddings), e.cfg.vocab, e.cfg.d,
                      e.f(e.layout.emb_norm), e.cfg.norm_eps, e.x, e.stream);
@@ -977,6 +995,29 @@ int julia_hip_encode_batch(const Engine* ce, size_t b, const uint32_t* ids, cons
             throw std::runtime_error("layer: a grid barrier timed out (blocks not co-resident)");
         if (gpu_ms) hip_check(hipEventElapsedTime(gpu_ms, e.ev_start[0], e.ev_end[0]), "hipEventElapsedTime");
         if (x_out) hip_check(hipMemcpy(x_out, xf, rows * e.cfg.d * 2, hipMemcpyDeviceToHost), "x");
+    });
+}
+
+int julia_hip_encode_batch_phases(const Engine* ce, size_t b, const uint32_t* ids,
+                                  const size_t* lens, float* phase_ms, char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!ce) throw std::runtime_error("no engine");
+        if (!phase_ms) throw std::runtime_error("no output");
+        Engine& e = *const_cast<Engine*>(ce);
+        hip_check(hipSetDevice(e.device), "hipSetDevice");
+        const int n = e.prepare_batch(b, ids, lens);
+        embed_launch(e.bids_d, n, e.h(e.layout.tok_embeddings), e.cfg.vocab, e.cfg.d,
+                     e.f(e.layout.emb_norm), e.cfg.norm_eps, e.x, e.stream);
+        for (int i = 0; i < 5; i++) phase_ms[i] = 0.0f;
+        for (int l = 0; l < e.cfg.layers; l++) {
+            e.launch_layer(l, n, e.pos_d, e.seg_d, e.ev_start);
+            hip_check(hipStreamSynchronize(e.stream), "the batched encoder");
+            for (int i = 0; i < 5; i++) {
+                float ms = 0.0f;
+                hip_check(hipEventElapsedTime(&ms, e.ev_start[i], e.ev_start[i + 1]), "hipEventElapsedTime");
+                phase_ms[i] += ms;
+            }
+        }
     });
 }
 

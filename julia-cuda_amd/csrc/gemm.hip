@@ -183,8 +183,10 @@ void gemm_launch(const Gemm& g, GemmConfig cfg, const Scratch& s, hipStream_t st
 GemmConfig gemm_choose(int m, int n, int k, int cus) {
     if (cus <= 0) cus = 256;
     if (m >= 2048 && n % 128 == 0 && k % 64 == 0) {
+        // 256 x 256 tiles once they fill half the CUs (one tile a CU; measured: 48 of them lose
+        // to 384 tiles of 128 x 128, 144 and up win), else 128 x 128 (two a CU).
         const long t256 = (n % 256 == 0) ? (long)(n / 256) * ((m + 255) / 256) : 0;
-        return GemmConfig{t256 >= cus ? 256 : 128, 1};
+        return GemmConfig{2 * t256 >= cus ? 256 : 128, 1};
     }
     GemmConfig best{32, 1};
     double best_cost = 1e30;

@@ -87,6 +87,7 @@ EXPORTS = [
     "julia_hip_gemm_choose_2080ti", "julia_hip_engine_info_get", "julia_hip_engine_tensor",
     "julia_hip_time_encoder_step", "julia_hip_profile_layer", "julia_hip_run_trace",
     "julia_hip_encode_batch",
+    "julia_hip_encode_batch_phases",
 ]
 
 _VP, _SZ, _I, _F, _CP = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_char_p
@@ -147,6 +148,7 @@ def lib():
                                      _CP, _SZ]),
         "julia_hip_encode_batch": (_I, [_VP, _SZ, _VP, _VP, _I, _VP, ctypes.POINTER(_F), _CP,
                                         _SZ]),
+        "julia_hip_encode_batch_phases": (_I, [_VP, _SZ, _VP, _VP, ctypes.POINTER(_F), _CP, _SZ]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -266,6 +268,17 @@ class Engine:
         _call(lib().julia_hip_encode_batch, self.ptr, len(seqs), _np_ptr(ids), _np_ptr(lens),
               int(layer_fused), _np_ptr(x), ctypes.byref(ms))
         return x, ms.value
+
+    def encode_batch_phases(self, seqs):
+        """The batched encoder through the per-step kernels with events between the steps:
+        {step: GPU ms summed over the layers}."""
+        ids = np.ascontiguousarray(np.concatenate([np.asarray(s, np.uint32) for s in seqs]),
+                                   np.uint32)
+        lens = np.array([len(s) for s in seqs], np.uintp)
+        out = (ctypes.c_float * 5)()
+        _call(lib().julia_hip_encode_batch_phases, self.ptr, len(seqs), _np_ptr(ids),
+              _np_ptr(lens), out)
+        return dict(zip(("qkv", "attention", "wo", "wi", "wo_mlp"), [float(v) for v in out]))
 
     def profile_layer(self, n, layer=1, plan=None):
         """The persistent encoder kernel's per-block phase stamps (src/profile.rs): returns (plan,

@@ -3,8 +3,11 @@
 plain device-to-device copy of a known size to calibrate byte counters against.
 
     python julia-cuda_amd/kernel_bench.py --step wi --tokens 293 --iters 200 --copy-mb 64
+    python julia-cuda_amd/kernel_bench.py --batch 64 --iters 3 --copy-mb 0
 
-Prints the step's median time per call (HIP events) and the copy's bytes.
+Prints the step's median time per call (HIP events) and the copy's bytes. With --batch N: config
+5's batched encoder instead (N requests of config 4's seeded lengths concatenated, per-step
+kernels then the persistent kernel, --iters times each).
 """
 
 import argparse
@@ -24,7 +27,20 @@ def main():
     ap.add_argument("--splits", type=int, default=1)
     ap.add_argument("--copy-mb", type=int, default=64)
     ap.add_argument("--spec", default="synthetic")
+    ap.add_argument("--batch", type=int, default=0)
     args = ap.parse_args()
+    if args.batch:
+        import numpy as np
+        rng = np.random.default_rng(4)
+        lens = np.clip(np.round(rng.lognormal(np.log(260.0), 0.5, args.batch)), 72, 1024).astype(int)
+        seqs = [rng.integers(0, 50368, int(n)).astype(np.uint32) for n in lens]
+        e = jh.Engine(f"synthetic:batch_rows={int(lens.sum())}", max_length=1024)
+        for fused in (False, True):
+            ms = [e.encode_batch(seqs, layer_fused=fused, want_x=False)[1] for _ in range(args.iters)]
+            print(f"batch of {args.batch} ({int(lens.sum())} rows), {'persistent' if fused else 'per-step'}: "
+                  f"{sorted(ms)[len(ms) // 2]:.3f} ms", flush=True)
+        e.close()
+        return
     e = jh.Engine(args.spec, max_length=max(1024, args.tokens))
     mn, md = e.time_step(args.step, args.tokens, args.bm, args.splits, warmup=10, batches=1,
                          per_batch=args.iters)

@@ -221,3 +221,4 @@ def test_chooser_matches_the_measured_winners():
     assert jh.gemm_choose(448, 768, 768, 256)[0] == 32
     assert jh.gemm_choose(18752, 2304, 768, 256) == (256, 1)
     assert jh.gemm_choose(4096, 768, 768, 256) == (128, 1)
+    assert jh.gemm_choose(18752, 768, 768, 256) == (256, 1)
