@@ -13,9 +13,11 @@
 // With `chunks` > 1 the key blocks of each (query block, head) tile are split into ranges, one
 // block each; every range writes its unnormalised output, max and sum to the scratch and the
 // last one of the tile to arrive merges them in range order (kernels/src/attn.rs:92-204).
-// With one range the LDS-resident query-slice tile runs (attn_tile.h: 16 queries per block, the
-// key range staged at once and split between the waves, V^T fragments from the transposing LDS
-// read).
+// With one range and up to ATT_SLICE_ROWS rows the LDS-resident query-slice tile runs
+// (attn_tile.h: 16 queries per block, the key range staged at once and split between the waves,
+// V^T fragments from the transposing LDS read): the latency shape for one request. Longer inputs
+// (config 5's concatenated requests) take the 64-query tile, which loads each key once per 64
+// queries instead of once per 16.
 #include <algorithm>
 #include <stdexcept>
 #include <string>
@@ -83,7 +85,7 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
     if (seg && chunks != 1) fail("concatenated sequences take one key range");
     if (seg && ((uintptr_t)seg % 8)) fail("seg must be 8-byte aligned");
     AttnParams p{qkv, o, n, d, window, chunks, s.ws, s.counters, seg};
-    if (chunks == 1) {
+    if (chunks == 1 && n <= ATT_SLICE_ROWS) {
         if (!attention_prepare()) fail("the LDS-resident kernel cannot have its LDS");
         const int gkeys = attention_gkeys(n, window);
         hipLaunchKernelGGL(attention_lds_kernel, dim3((n + 15) / 16 * (d / 64)), dim3(256),

@@ -9,6 +9,9 @@ namespace jh {
 
 constexpr int ATT_PART = 18;  // f32 per thread in a key-range partial: 16 outputs, max, sum
 
+// Rows up to which one key range goes to the 16-query slice tile; above, the 64-query tile.
+constexpr int ATT_SLICE_ROWS = 2048;
+
 // LDS f16 attention_tile needs: the K tile [64 keys][72] and the V^T tile [64 d][68].
 constexpr int ATT_LDS_F16 = 64 * 72 + 64 * 68;
 
@@ -25,18 +28,30 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
     const int q0 = qb * 64;
     const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g = l >> 4;
 
-    // Key blocks this tile needs, then this chunk's range of them (possibly empty).
+    // Key blocks this tile needs, then this chunk's range of them (possibly empty). With
+    // concatenated sequences (p.seg) a query sees the keys of its own sequence only: the tile's
+    // keys lie between its first row's sequence start and its last row's sequence end.
     const int nb = (n + 63) >> 6;
     int kb0 = 0, kb1 = nb;
+    if (p.seg) {
+        kb0 = p.seg[2 * q0] >> 6;
+        kb1 = ((p.seg[2 * min(q0 + 63, n - 1) + 1] - 1) >> 6) + 1;
+    }
     if (p.window > 0) {
-        kb0 = max(q0 - p.window, 0) >> 6;
-        kb1 = (min(q0 + 63 + p.window, n - 1) >> 6) + 1;
+        kb0 = max(kb0, max(q0 - p.window, 0) >> 6);
+        kb1 = min(kb1, (min(q0 + 63 + p.window, n - 1) >> 6) + 1);
     }
     const int nkb = kb1 - kb0;
     const int c0 = kb0 + chunk * nkb / p.chunks, c1 = kb0 + (chunk + 1) * nkb / p.chunks;
 
-    // This wave's 16 queries as B operands (two K steps over d = 64).
+    // This wave's 16 queries as B operands (two K steps over d = 64), and each query's key
+    // bounds (its sequence's rows).
     const int qi = q0 + 16 * w + r16;
+    int slo = 0, shi = n;
+    if (p.seg) {
+        slo = p.seg[2 * min(qi, n - 1)];
+        shi = p.seg[2 * min(qi, n - 1) + 1];
+    }
     half8 qf[2];
     {
         const f16* qp = (const f16*)p.qkv + (size_t)min(qi, n - 1) * ld + h * 64 + 8 * g;
@@ -108,7 +123,7 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
             for (int e = 0; e < 4; e++) {
                 const int key = kbase + 16 * t + 4 * g + e;
                 const int dist = qi > key ? qi - key : key - qi;
-                const bool ok = key < n && (p.window == 0 || dist <= p.window);
+                const bool ok = key >= slo && key < shi && (p.window == 0 || dist <= p.window);
                 s[t][e] = ok ? s[t][e] * scale : -INFINITY;
                 bm = fmaxf(bm, s[t][e]);
             }

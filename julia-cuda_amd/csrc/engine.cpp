@@ -930,12 +930,13 @@ int julia_hip_profile_layer(const Engine* ce, int n, int layer, const int* plan,
         if (!ce) throw std::runtime_error("no engine");
         Engine& e = *const_cast<Engine*>(ce);
         hip_check(hipSetDevice(e.device), "hipSetDevice");
-        if (n <= 0 || n > e.max_length) throw std::runtime_error("profile: n out of range");
+        if (n <= 0 || n > e.rows) throw std::runtime_error("profile: n out of range");
         if (layer < -1 || layer >= e.cfg.layers) throw std::runtime_error("profile: no such layer");
         std::vector<uint32_t> ids(n);
         for (int i = 0; i < n; i++) ids[i] = (uint32_t)(i * 7919 % e.cfg.vocab);
-        hip_check(hipMemcpy(e.ids_d, ids.data(), n * 4, hipMemcpyHostToDevice), "ids");
-        embed_launch(e.ids_d, n, e.h(e.layout.tok_embeddings), e.cfg.vocab, e.cfg.d,
+        uint32_t* ids_d = n > e.max_length ? e.bids_d : e.ids_d;  // (one sequence of n rows)
+        hip_check(hipMemcpy(ids_d, ids.data(), n * 4, hipMemcpyHostToDevice), "ids");
+        embed_launch(ids_d, n, e.h(e.layout.tok_embeddings), e.cfg.vocab, e.cfg.d,
                      e.f(e.layout.emb_norm), e.cfg.norm_eps, e.x, e.stream);
         // One layer (after the ones before it, per step) or, with layer -1, the whole encoder.
         const int first = layer < 0 ? 0 : layer, count = layer < 0 ? e.cfg.layers : 1;

@@ -156,7 +156,7 @@ __device__ __forceinline__ int gemm_tasks(const GemmParams& g) {
 
 // bm 16/32/64: the latency tile with its weights in LDS; 128: the throughput tile (128 x 128,
 // large batches), which stages both operands itself.
-template <int EPI, bool AX>
+template <int EPI, bool AX, bool BIG>
 __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* lds, bool pre,
                                            uint32_t* s_last, uint64_t* sub) {
     const int T = gemm_tasks(g);
@@ -164,7 +164,7 @@ __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* ld
         const bool first = t == (int)blockIdx.x;
         const bool ready = pre && first;
         uint64_t* su = first ? sub : nullptr;
-        if (bm == 128)
+        if (BIG || bm == 128)
             gemm_big_tile<128, 128, EPI, AX, true>(g, t, lds, su);
         else if (bm == 16)
             gemm_w_tile<16, EPI, AX>(g, t, lds, ready, s_last, su);
@@ -175,7 +175,11 @@ __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* ld
     }
 }
 
-__global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
+// BIG: the large-batch instance (LayerKernel::is_big plans): only the throughput tiles and the
+// 64-query attention tile are compiled in, in at most 256 registers a lane, so that two blocks
+// share a CU (the 128 x 128 tile wants eight waves a CU). The other instance takes every plan.
+template <bool BIG>
+__global__ __launch_bounds__(256, BIG ? 2 : 1) void encoder_kernel(EncParams P) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     uint32_t* s_last = (uint32_t*)(lds + P.lds_main);
     uint32_t g0 = 0, nb = 0;
@@ -194,7 +198,9 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
         return [&g, wl] { w_tile_fetch(g, w_tile_of(g, blockIdx.x), wl, 1); };
     };
     // A block fetches its first weight tile during the barrier (latency tiles only).
-    auto prefetch = [&](const GemmParams& g, int bm) { return bm < 128 && (int)blockIdx.x < gemm_tasks(g); };
+    auto prefetch = [&](const GemmParams& g, int bm) {
+        return !BIG && bm < 128 && (int)blockIdx.x < gemm_tasks(g);
+    };
 
     LayerDesc L = P.layers[P.first];
     GemmParams gq = make_gemm(P, 0, L, P.first);
@@ -209,9 +215,9 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
         if (on(0)) {
             stamp(prof, 0);
             if (gq.colsum)
-                gemm_phase<EPI_K_LNROPE, false>(gq, P.bm[0], lds, pre, s_last, sub(0));
+                gemm_phase<EPI_K_LNROPE, false, BIG>(gq, P.bm[0], lds, pre, s_last, sub(0));
             else
-                gemm_phase<EPI_K_ROPE, false>(gq, P.bm[0], lds, pre, s_last, sub(0));
+                gemm_phase<EPI_K_ROPE, false, BIG>(gq, P.bm[0], lds, pre, s_last, sub(0));
             pre = false;
             stamp_end(prof, 0);
             if (on(1)) sync(nothing);
@@ -222,7 +228,7 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
             const AttnParams at{P.qa + (size_t)l * P.q_stride, P.oa + (size_t)l * P.o_stride,
                                 P.m, P.d, L.window, chunks, P.ws, P.counters, P.seg};
             const int heads = P.d >> 6;
-            if (chunks == 1) {  // qkv is this layer's own buffer: read through the caches
+            if (!BIG && chunks == 1 && P.m <= ATT_SLICE_ROWS) {  // qkv: own buffer, cached
                 const int T = ((P.m + 15) >> 4) * heads, gkeys = P.att_gkeys[L.window > 0 ? 1 : 0];
                 for (int t = blockIdx.x; t < T; t += gridDim.x) {
                     uint64_t* su = prof && t == (int)blockIdx.x ? prof + 12 : nullptr;
@@ -243,7 +249,7 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
         }
         if (on(2)) {
             stamp(prof, 4);
-            gemm_phase<EPI_K_RESSTATS, false>(go, P.bm[1], lds, pre, s_last, sub(1));
+            gemm_phase<EPI_K_RESSTATS, false, BIG>(go, P.bm[1], lds, pre, s_last, sub(1));
             pre = false;
             stamp_end(prof, 2);
             if (on(3)) {
@@ -253,7 +259,7 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
         }
         if (on(3)) {
             stamp(prof, 6);
-            gemm_phase<EPI_K_LNGEGLU, false>(gi, P.bm[2], lds, pre, s_last, sub(2));
+            gemm_phase<EPI_K_LNGEGLU, false, BIG>(gi, P.bm[2], lds, pre, s_last, sub(2));
             pre = false;
             stamp_end(prof, 3);
             if (on(4)) {
@@ -263,7 +269,7 @@ __global__ __launch_bounds__(256) void encoder_kernel(EncParams P) {
         }
         if (on(4)) {
             stamp(prof, 8);
-            gemm_phase<EPI_K_RESSTATS, true>(gm, P.bm[3], lds, pre, s_last, sub(3));
+            gemm_phase<EPI_K_RESSTATS, true, BIG>(gm, P.bm[3], lds, pre, s_last, sub(3));
             pre = false;
             stamp_end(prof, 4);
         }
@@ -307,20 +313,27 @@ int LayerKernel::lds_bytes(const LayerPlan& plan, int d, int inter, int m, int w
     return (b + 15) / 16 * 16;
 }
 
+// The large-batch instance's LDS: the 128 x 128 tile or the 64-query attention tile.
+static int big_lds_bytes() {
+    return (std::max<int>(Big<128, 128>::LDS_BYTES, ATT_LDS_F16 * 2) + 15) / 16 * 16;
+}
+
 void LayerKernel::init(int cus, int lds_max) {
     cus_ = cus > 0 ? cus : 256;
     lds_max_ = lds_max - 16;  // the split-K flag after the main area
-    per_cu_ = 0;
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(encoder_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, lds_max) != hipSuccess) {
-        (void)hipGetLastError();
-        return;
-    }
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(encoder_kernel),
-                                                     256, lds_max) != hipSuccess)
-        n = 0;
-    per_cu_ = n;  // with the largest LDS a plan may use: one block per CU
+    per_cu_ = per_cu_big_ = 0;
+    auto occupancy = [](const void* k, int lds) {
+        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) {
+            (void)hipGetLastError();
+            return 0;
+        }
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, 256, lds) != hipSuccess) n = 0;
+        return n;
+    };
+    // with the largest LDS a plan may use: one block per CU
+    per_cu_ = occupancy(reinterpret_cast<const void*>(encoder_kernel<false>), lds_max);
+    per_cu_big_ = occupancy(reinterpret_cast<const void*>(encoder_kernel<true>), big_lds_bytes() + 16);
 }
 
 // Per GEMM the tile height and split-K with the least modelled time on a grid of one block per
@@ -335,9 +348,10 @@ LayerPlan LayerKernel::default_plan(int m, int d, int inter) const {
     shapes(d, inter, cols, ks);
     const double bw = 67e3;  // bytes per us into one CU
     for (int g = 0; g < 4; g++) {
-        // Large batches: the throughput tile (the per-step chooser's threshold).
-        if (m >= 2048 && cols[g] % 128 == 0 && ks[g] % 32 == 0 && ks[g] <= 128 * BIG_LN_SLOTS &&
-            Big<128, 128>::LDS_BYTES <= lds_max_) {
+        // Large batches: the throughput tile (LayerNorm epilogues, qkv and wi, need K <= 1024).
+        const bool ln = g == 0 || g == 2;
+        if (m > ATT_SLICE_ROWS && cols[g] % 128 == 0 && ks[g] % 32 == 0 &&
+            (!ln || ks[g] <= 128 * BIG_LN_SLOTS) && Big<128, 128>::LDS_BYTES <= lds_max_) {
             p.bm[g] = 128, p.splits[g] = 1;
             continue;
         }
@@ -394,7 +408,8 @@ int LayerKernel::grid(const LayerArgs& a, const LayerPlan& plan) const {
                                   ((a.m + plan.bm[g] - 1) / plan.bm[g]) * plan.splits[g]);
     // Enough blocks for the largest phase's tasks in one round if they fit (a multiple of 8, so
     // that the task-to-XCD map is even), else every resident block.
-    const long grid = std::min<long>((long)per_cu_ * cus_, (most + 7) / 8 * 8);
+    const int per_cu = is_big(plan, a.m) ? per_cu_big_ : per_cu_;
+    const long grid = std::min<long>((long)per_cu * cus_, (most + 7) / 8 * 8);
     return (int)std::max<long>(grid, 1);
 }
 
@@ -417,7 +432,9 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
     if ((a.pos == nullptr) != (a.seg == nullptr)) fail("positions go with sequence bounds");
     int window = 0;
     for (int li = 0; li < a.count; li++) window = std::max(window, a.host_layers[a.first + li].window);
-    const int lds = lds_bytes(plan, a.d, a.inter, a.m, window);
+    const bool big = is_big(plan, a.m);
+    if (big && per_cu_big_ <= 0) fail("the encoder kernel's large-batch instance does not fit on a CU");
+    const int lds = big ? big_lds_bytes() : lds_bytes(plan, a.d, a.inter, a.m, window);
     if (lds > lds_max_) fail("the plan's weight tiles do not fit the LDS: " + plan.str());
 
     // Every layer's GEMMs pass the per-step launcher's checks (the kernel builds the same ones).
@@ -478,10 +495,18 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
 
     const int grid_blocks = grid(a, plan);
     void* args[] = {&P};
-    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(encoder_kernel),
-                                                    dim3(grid_blocks), dim3(256), args, lds + 16, stream);
+    const void* kernel = big ? reinterpret_cast<const void*>(encoder_kernel<true>)
+                             : reinterpret_cast<const void*>(encoder_kernel<false>);
+    const hipError_t e = hipLaunchCooperativeKernel(kernel, dim3(grid_blocks), dim3(256), args,
+                                                    lds + 16, stream);
     if (e != hipSuccess) fail(std::string(hipGetErrorString(e)) + " (" + plan.str() + ", grid " +
                               std::to_string(grid_blocks) + ")");
+}
+
+bool LayerKernel::is_big(const LayerPlan& plan, int m) {
+    for (int g = 0; g < 4; g++)
+        if (plan.bm[g] != 128) return false;
+    return m > ATT_SLICE_ROWS && plan.kv[0] == 1 && plan.kv[1] == 1;
 }
 
 bool LayerKernel::barrier_timed_out() {
