@@ -37,7 +37,7 @@ namespace jh {
 template <int BM, int BN>
 struct Big {
     static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 128), "tile shape");
-    static constexpr int BK = 32, NSTAGE = 4;
+    static constexpr int TM = BM, TN = BN, BK = 32, NSTAGE = 4;
     static constexpr int WAVES_M = 2, WAVES_N = BN / 64;  // 2 x 4 waves (256) or 2 x 2 (128)
     static constexpr int NWAVES = WAVES_M * WAVES_N, THREADS = 64 * NWAVES;
     static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;  // a wave's block
@@ -48,7 +48,11 @@ struct Big {
     static constexpr int LOADS = STAGE / 1024 / NWAVES;  // 1 KB copies per wave per stage
     static constexpr int COLS = NSTAGE * STAGE;       // per wave: colsum, bias of its columns
     static constexpr int ROWS = COLS + NWAVES * 2 * WN * 4;  // per row: LayerNorm mean, rstd
-    static constexpr int LDS_BYTES = ROWS + BM * 8;
+    static constexpr int POSR = ROWS + BM * 8;                // per row: RoPE position
+    static constexpr int LDS_BYTES = POSR + BM * 4;
+    // RoPE epilogues, after the K loop: the tile's table rows (BM x 256 bytes) in the stages'
+    // space, then the f16 staging of the output rows.
+    static constexpr int TABLE_BYTES = BM * 256;
     static_assert(NG == 1 && LOADS >= 1, "wave blocks of 64 columns");
     static_assert(THREADS == 2 * BM, "two threads a row for the row statistics");
 };
@@ -119,18 +123,13 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
 #pragma unroll
         for (int u = 0; u < BIG_LN_SLOTS; u++) sl[u] = load8f<XG>(st + 2 * min(2 * u + (tid & 1), slots - 1));
     }
-    int pos_[MR];
-#pragma unroll
-    for (int i = 0; i < MR; i++) pos_[i] = min(row0 + 32 * i, p.m - 1);
-    if ((EPI & EPI_ROPE) && p.pos) {  // one uniform branch around all the rows' loads
-#pragma unroll
-        for (int i = 0; i < MR; i++) pos_[i] = p.pos[pos_[i]];
-    }
+    // The RoPE position of row tid / 2 (an unconditional load: from the table itself when there
+    // are no positions), into LDS with the row statistics.
+    int rpos = 0;
     if (EPI & EPI_ROPE) {
-        // The table addresses are computed after the K loop from these four values (left to
-        // itself the compiler computes them here and keeps them live through the loop).
-#pragma unroll
-        for (int i = 0; i < MR; i++) asm volatile("" : "+v"(pos_[i]));
+        const int r = min(by * BM + (tid >> 1), p.m - 1);
+        const int v = *(const int*)(p.pos ? (const void*)(p.pos + r) : (const void*)p.rope);
+        rpos = min(max(p.pos ? v : r, 0), p.rope_rows - 1);
     }
 
     // ---- the K loop ---------------------------------------------------------------------------
@@ -194,6 +193,8 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
         const float var = fmaxf(Q / (float)p.k - mean * mean, 0.0f);
         if ((tid & 1) == 0) rows_ms[tid >> 1] = make_float2(mean, 1.0f / sqrtf(var + p.eps));
     }
+    int* rows_pos = (int*)(lds + C::POSR);
+    if ((EPI & EPI_ROPE) && (tid & 1) == 0) rows_pos[tid >> 1] = rpos;
 
     floatx16 acc[MR][NC];
 #pragma unroll
@@ -280,28 +281,42 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     // lanes a row.
     constexpr bool GEGLU = (EPI & EPI_GEGLU) != 0;
     constexpr bool RES = (EPI & EPI_RES) && !GEGLU;
+    constexpr bool ROPE = (EPI & EPI_ROPE) != 0;
+    // The staging holds f32 where the residual and statistics follow (rounding after the
+    // residual add), f16 otherwise (the same rounding, half the LDS traffic).
+    constexpr bool H16 = !RES && !(EPI & EPI_STATS);
     constexpr int WO = GEGLU ? C::WN / 2 : C::WN;  // output columns of the wave
     constexpr int LPR = WO / 8, RPP = 64 / LPR;     // lanes a row, rows a pass
-    constexpr int NPASS = 32 / RPP, PAD = WO + 4;
+    constexpr int NPASS = 32 / RPP, PAD = WO + 4, PADH = WO + 8;
+    static_assert(!ROPE || (H16 && C::TABLE_BYTES + C::NWAVES * 32 * PADH * 2 <= C::COLS),
+                  "RoPE table and f16 staging in the stages' space");
     const int ncol = GEGLU ? (p.n >> 1) : p.n;
     const int col0 = (GEGLU ? g0 * 32 : g0 * 64);   // the wave's first output column
-    float* sg = (float*)lds + w * 32 * PAD;
+    char* stage_base = lds + (ROPE ? C::TABLE_BYTES : 0);
+    float* sg = (float*)stage_base + w * 32 * PAD;
+    f16* sgh = (f16*)stage_base + w * 32 * PADH;
     __syncthreads();  // every wave is done reading the stages
 
+    // RoPE: the tile's table rows into LDS as whole lines (copy I takes rows 4 I .. 4 I + 3, 16
+    // lanes a row; the 16-byte chunk c of row r is stored at chunk c ^ (r % 16), so that the 16
+    // rows one read serves cover all 64 banks). A lane's own gathers would touch 32 lines a load
+    // instruction, over again in every wave that shares the rows.
+    const char* table = lds;
+    if (ROPE) {
+        constexpr int COPIES = C::TM / 4 / C::NWAVES;
+#pragma unroll
+        for (int q = 0; q < COPIES; q++) {
+            const int I = w + C::NWAVES * q, rr = 4 * I + (l >> 4), c = (l & 15) ^ (rr & 15);
+            lds_dma16<false>(p.rope + ((size_t)rows_pos[rr] * 32 + c * 2) * 2, lds + I * 1024);
+        }
+        wait_vmcnt<0>();
+        __syncthreads();
+    }
+
     struct RowIn {
-        float4 rt[4][2];        // RoPE (cos, sin) of dimensions 8 q + 4 hi .. + 3
         half8 rr[NPASS];        // residual, transposed layout
     };
     auto load_row = [&](int i, RowIn& in) {
-        if (EPI & EPI_ROPE) {
-            const int pos = min(max(pos_[i], 0), p.rope_rows - 1);
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float4* t = (const float4*)(p.rope + ((size_t)pos * 32 + 8 * q + 4 * hi) * 2);
-                in.rt[q][0] = t[0];
-                in.rt[q][1] = t[1];
-            }
-        }
         if (RES) {
             const f16* x = (const f16*)(p.res ? p.res : p.c);
 #pragma unroll
@@ -371,9 +386,14 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
                 // q and k heads: columns x and x + 32 of a head are the rotate-half pair of
                 // dimension x; the table holds (cos, sin) per dimension.
                 if (g * 64 < p.rope_cols) {
+                    const int tr = wm * C::WM + 32 * i + l32;  // the row in the tile
+                    const char* trow = table + tr * 256;
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
-                        const float4 t0 = ri.rt[q][0], t1 = ri.rt[q][1];
+                        // dimensions 8 q + 4 hi .. + 3: chunks 4 q + 2 hi and + 1
+                        const int ca = 4 * q + 2 * hi;
+                        const float4 t0 = *(const float4*)(trow + ((ca ^ (tr & 15)) << 4));
+                        const float4 t1 = *(const float4*)(trow + (((ca + 1) ^ (tr & 15)) << 4));
                         const float co[4] = {t0.x, t0.z, t1.x, t1.z}, sn[4] = {t0.y, t0.w, t1.y, t1.w};
 #pragma unroll
                         for (int e = 0; e < 4; e++) {
@@ -385,7 +405,18 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
                 }
             }
             float* dst = sg + l32 * PAD + 4 * hi;
-            if (GEGLU) {
+            f16* dsth = sgh + l32 * PADH + 4 * hi;
+            if (H16 && !GEGLU) {
+#pragma unroll
+                for (int h = 0; h < 2; h++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        half4 o;
+#pragma unroll
+                        for (int e = 0; e < 4; e++) o[e] = (f16)v[h][4 * q + e];
+                        *(half4*)(dsth + 64 * j + 32 * h + 8 * q) = o;
+                    }
+            } else if (GEGLU) {
                 // Packed rows 64 g + x are the input of output column 32 g + x, + 32 its gate.
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
@@ -412,17 +443,21 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
 #pragma unroll
         for (int ps = 0; ps < NPASS; ps++) {
             const int rl = ps * RPP + l / LPR;
-            const float* src = sg + rl * PAD + cl;
-            const float4 a0 = *(const float4*)(src + sw), a1 = *(const float4*)(src + 4 - sw);
-            const float4 lo = sw ? a1 : a0, hi4 = sw ? a0 : a1;
-            float y[8] = {lo.x, lo.y, lo.z, lo.w, hi4.x, hi4.y, hi4.z, hi4.w};
-            if (RES) {
-#pragma unroll
-                for (int e = 0; e < 8; e++) y[e] += (float)ri.rr[ps][e];
-            }
             half8 o;
+            if (H16 && !GEGLU) {
+                o = *(const half8*)(sgh + rl * PADH + cl);
+            } else {
+                const float* src = sg + rl * PAD + cl;
+                const float4 a0 = *(const float4*)(src + sw), a1 = *(const float4*)(src + 4 - sw);
+                const float4 lo = sw ? a1 : a0, hi4 = sw ? a0 : a1;
+                float y[8] = {lo.x, lo.y, lo.z, lo.w, hi4.x, hi4.y, hi4.z, hi4.w};
+                if (RES) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) o[e] = (f16)y[e];
+                    for (int e = 0; e < 8; e++) y[e] += (float)ri.rr[ps][e];
+                }
+#pragma unroll
+                for (int e = 0; e < 8; e++) o[e] = (f16)y[e];
+            }
             const int row = by * BM + wm * C::WM + 32 * i + rl;
             const bool valid = row < p.m;
             if (valid) store16<XG>((f16*)p.c + (size_t)row * ncol + col0 + cl, o);
