@@ -130,14 +130,14 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
         bm = max_xor32(max_xor16(bm));
         const float mnew = fmaxf(mx, bm);
         const float base = mnew == -INFINITY ? 0.0f : mnew;  // no valid key yet: exp2(-inf) = 0
-        const float alpha = exp2f(mx - base);
+        const float alpha = fast_exp2(mx - base);
         mx = mnew;
         float rs = 0.0f;
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                s[t][e] = exp2f(s[t][e] - base);
+                s[t][e] = fast_exp2(s[t][e] - base);
                 rs += s[t][e];
             }
         lsum = lsum * alpha + rs;
@@ -196,7 +196,7 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
         for (int dt = 0; dt < 4; dt++) oacc[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
         for (int z = 0; z < p.chunks; z++) {
             const float* src = slots + (size_t)z * ATT_PART * 256 + tid;
-            const float f = exp2f(xload32(src + 16 * 256) - base);
+            const float f = fast_exp2(xload32(src + 16 * 256) - base);
             lsum += xload32(src + 17 * 256) * f;
 #pragma unroll
             for (int dt = 0; dt < 4; dt++)
@@ -230,18 +230,18 @@ __device__ __forceinline__ void attention_tile(const AttnParams& p, int qb, int 
 // r stored at chunk ^ (r % 8) so a fragment's 16 rows spread over the banks); V^T fragments come
 // from the transposing LDS read. No key ranges across blocks.
 
-// LDS bytes of attention_slice_tile staging up to gkeys keys at once (a multiple of 32); the
-// waves' merge reuses the space.
-__host__ __device__ constexpr int att_lds_bytes(int gkeys) {
-    return 2048 + 256 * gkeys > 4 * 18 * 64 * 4 ? 2048 + 256 * gkeys : 4 * 18 * 64 * 4;
+// LDS bytes of attention_slice_tile staging up to gkeys keys at once (a multiple of 32) with nw
+// waves; the waves' merge reuses the space.
+__host__ __device__ constexpr int att_lds_bytes(int gkeys, int nw = 4) {
+    return 2048 + 256 * gkeys > nw * 18 * 64 * 4 ? 2048 + 256 * gkeys : nw * 18 * 64 * 4;
 }
 
 // Byte offset of 16-byte chunk `ch` of row `r` in a swizzled [rows][64 f16] LDS tile.
 __device__ __forceinline__ int att_swz(int r, int ch) { return (r * 8 + (ch ^ (r & 7))) * 16; }
 
-// Task `task` of (n + 15) / 16 slices x heads (XCD-mapped so a head's slices share an XCD's L2).
-// XL: qkv is read device-coherent; XS: o is stored device-coherent.
-template <bool XL = false, bool XS = false>
+// Task `task` of (n + 15) / 16 slices x heads (XCD-mapped so a head's slices share an XCD's L2),
+// by a block of NW waves. XL: qkv is read device-coherent; XS: o is stored device-coherent.
+template <bool XL = false, bool XS = false, int NW = 4>
 __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int task, char* lds,
                                                      int gkeys, uint64_t* sub = nullptr) {
     auto mark = [&](int i) {  // profiling: thread 0's view of the task's stages
@@ -251,7 +251,8 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
     const int slices = (n + 15) >> 4, T = slices * heads;
     const int L = xcd_task(task, T);
     const int h = L / slices, q0 = (L % slices) * 16;
-    const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, r16 = l & 15, g = l >> 4;
+    const int tid = threadIdx.x, l = tid & 63, r16 = l & 15, g = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int j = r16 >> 2, q = r16 & 3;
     char* qs = lds;
     char* ks = lds + 2048;
@@ -271,7 +272,7 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
     // n - 1, into `dst`: wave load I fills LDS chunks 64 I .. 64 I + 63, lane l chunk 64 I + l,
     // which is row c / 8, logical chunk (c % 8) ^ (row % 8).
     auto stage = [&](char* dst, int r0, int rows, int col) {
-        for (int I = w; I * 64 < rows * 8; I += 4) {
+        for (int I = w; I * 64 < rows * 8; I += NW) {
             const int c = I * 64 + l, row = c >> 3, ch = (c & 7) ^ (row & 7);
             const f16* src = (const f16*)p.qkv + (size_t)min(r0 + row, n - 1) * ld + col + ch * 8;
             lds_dma16<XL>(src, dst + I * 1024);
@@ -306,7 +307,7 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
 #pragma unroll
             for (int k2 = 0; k2 < 2; k2++) qf[k2] = *(const half8*)(qs + att_swz(r16, 4 * k2 + g));
         }
-        for (int st = w * steps / 4; st < (w + 1) * steps / 4; st++) {
+        for (int st = w * steps / NW; st < (w + 1) * steps / NW; st++) {
             const int kb = gk + 32 * st, rb = 32 * st;  // the step's first key and LDS row
             // Every LDS read of the step first (K fragments of its two 16-key S tiles; V^T
             // fragments: lane (g, 4 j + q) addresses key rb + 4 g + j (+ 16), d 16 dt + 4 q), so
@@ -361,14 +362,14 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
             bm = max_xor32(max_xor16(bm));
             const float mnew = fmaxf(mx, bm);
             const float base = mnew == -INFINITY ? 0.0f : mnew;  // no valid key yet: exp2(-inf) = 0
-            const float alpha = exp2f(mx - base);
+            const float alpha = fast_exp2(mx - base);
             mx = mnew;
             float rs = 0.0f;
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    sc[t][e] = exp2f(sc[t][e] - base);
+                    sc[t][e] = fast_exp2(sc[t][e] - base);
                     rs += sc[t][e];
                 }
             lsum = lsum * alpha + rs;
@@ -393,6 +394,7 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
     // The waves' partials (output, max, sum over the query's keys) through LDS; wave 0 merges.
     const float tot = sum_xor32(sum_xor16(lsum));
     float* mg = (float*)lds;  // [wave][18][64]
+    static_assert(NW >= 1 && NW <= 16, "waves");
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
@@ -403,15 +405,15 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
     if (w == 0) {
         float m = -INFINITY;
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) m = fmaxf(m, mg[(ww * 18 + 16) * 64 + l]);
+        for (int ww = 0; ww < NW; ww++) m = fmaxf(m, mg[(ww * 18 + 16) * 64 + l]);
         const float base = m == -INFINITY ? 0.0f : m;
         float sum = 0.0f;
         floatx4 o[4];
 #pragma unroll
         for (int dt = 0; dt < 4; dt++) o[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int ww = 0; ww < 4; ww++) {
-            const float f = exp2f(mg[(ww * 18 + 16) * 64 + l] - base);
+        for (int ww = 0; ww < NW; ww++) {
+            const float f = fast_exp2(mg[(ww * 18 + 16) * 64 + l] - base);
             sum += mg[(ww * 18 + 17) * 64 + l] * f;
 #pragma unroll
             for (int dt = 0; dt < 4; dt++)

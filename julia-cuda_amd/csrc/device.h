@@ -55,6 +55,11 @@ __device__ __forceinline__ LanePair lane_pair32(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return {__uint_as_float(r[0]), __uint_as_float(r[1])};
 }
+// 2^x by the hardware's v_exp_f32 alone: exact at 0 and -inf (-> 0); results below 2^-126 come
+// out as zero rather than denormals, which a softmax weight never misses (exp2f adds a rescaling
+// step for them around the same instruction).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ float max_xor16(float v) { const LanePair p = lane_pair16(v); return fmaxf(p.lo, p.hi); }
 __device__ __forceinline__ float max_xor32(float v) { const LanePair p = lane_pair32(v); return fmaxf(p.lo, p.hi); }
 __device__ __forceinline__ float sum_xor16(float v) { const LanePair p = lane_pair16(v); return p.lo + p.hi; }

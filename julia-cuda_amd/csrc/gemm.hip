@@ -36,6 +36,16 @@ __global__ __launch_bounds__(256, 2) void gemm_lat(GemmParams p) {
     gemm_lat_tile<BM, EPI>(p, blockIdx.x, red, &s_last);
 }
 
+// gemm_lat for grids of at most one block a CU (one request's GEMMs up to ~300 tokens): the
+// block may use every register, and the 48- and 64-row tiles then issue all of a wave's K steps
+// before the first MFMA (one round trip to L2 where the two-block form takes two).
+template <int BM, int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_lat1(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) float red[lat_lds_floats<BM>()];
+    __shared__ uint32_t s_last;
+    gemm_lat_tile<BM, EPI, false, true>(p, blockIdx.x, red, &s_last);
+}
+
 // ---------------------------------------------------------------------------------------------
 // gemm_big: BM x BM tiles (BM = 128 or 256) for large M; see gemm_big.h. Dynamic LDS:
 // Big<BM, BM>::LDS_BYTES.
@@ -56,6 +66,19 @@ std::string cfg_str(GemmConfig c) {
 }
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Compute units of the current device (queried once per device).
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
 
 }  // namespace
 
@@ -128,6 +151,8 @@ static void launch_one(const GemmParams& p, hipStream_t st) {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, Big<B, B>::LDS_BYTES) == hipSuccess;
         if (!lds_ok) throw std::runtime_error("gemm: the throughput kernel cannot have its LDS");
         hipLaunchKernelGGL((gemm_big<B, EPI>), dim3(blocks), dim3(Big<B, B>::THREADS), (Big<B, B>::LDS_BYTES), st, p);
+    } else if ((BM == 48 || BM == 64) && blocks <= device_cus()) {
+        hipLaunchKernelGGL((gemm_lat1<BM == 48 ? 48 : 64, EPI>), dim3(blocks), dim3(256), 0, st, p);
     } else {
         hipLaunchKernelGGL((gemm_lat<BM < 128 ? BM : 64, EPI>), dim3(blocks), dim3(256), 0, st, p);
     }

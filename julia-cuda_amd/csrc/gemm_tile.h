@@ -79,8 +79,9 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
 // Task `task` (of tiles_n * tiles_m * splits; XCD-mapped) of c = epilogue(a . w^T). The four
 // waves split the tile's K steps between them; `red` is lat_lds_floats<BM>() floats of LDS.
 // Every thread of the block calls it; it ends with a block barrier, so the caller may reuse
-// `red` right after.
-template <int BM, int EPI, bool XG = false>
+// `red` right after. ONE: the block has its CU to itself (512 registers a lane), so that the
+// 48- and 64-row tiles hold every K step of a wave in flight at once.
+template <int BM, int EPI, bool XG = false, bool ONE = false>
 __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, float* red,
                                               uint32_t* s_last, uint64_t* sub = nullptr) {
     auto mark = [&](int i) {  // profiling: thread 0's view of the task's stages
@@ -131,7 +132,8 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     // serialise the steps. The chunk guards depend on the wave index only (scalar branches).
     // UC K steps a chunk (2 x UC x (MI + 4) x 4 VGPRs of fragments): four, three or two; five for
     // 16-row tiles whose waves have more than eight K steps (K = 1152), which then take one round
-    // trip instead of two.
+    // trip instead of two. With a CU to itself (ONE), three or five for 32-row tiles and up: one
+    // round trip up to 10 K steps a wave.
     auto kloop = [&](auto uc_) {
         constexpr int UC = decltype(uc_)::value;
         half8 fa0[UC][MI], fw0[UC][4], fa1[UC][MI], fw1[UC][4];
@@ -188,10 +190,16 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
             if (u + 3 * UC < u1) load(fa1, fw1, u + 3 * UC);
         }
     };
-    if (MI == 1 && u1 - u0 > 8)
+    if (ONE && MI > 1) {
+        if (u1 - u0 > 6)
+            kloop(std::integral_constant<int, 5>{});
+        else
+            kloop(std::integral_constant<int, 3>{});
+    } else if (MI == 1 && u1 - u0 > 8) {
         kloop(std::integral_constant<int, 5>{});
-    else
+    } else {
         kloop(std::integral_constant<int, MI == 1 ? 4 : (MI == 2 ? 3 : 2)>{});
+    }
 
     mark(1);
     // acc[i][j] lane: row 16 i + r16, columns 16 j + 4 g + e of the tile. Wave w's partial at
