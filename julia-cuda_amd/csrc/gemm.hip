@@ -199,20 +199,22 @@ void gemm_launch(const Gemm& g, GemmConfig cfg, const Scratch& s, hipStream_t st
         throw std::runtime_error(std::string("gemm (") + cfg_str(cfg) + "): " + hipGetErrorString(e));
 }
 
-// The tiling for one request's GEMMs on a 256-CU GPU. Small M is bound by how fast a CU takes in
-// its tiles' operands: the model is a fixed ~4 us (launch, first round trip, reduction,
-// epilogue) plus the busiest CU's operand bytes, ceil(tiles / CUs) x (BM + 64) x K x 2, at about
-// 55 GB/s into one CU (measured on MI355X: 48-row tiles for qkv and wi at 293 tokens, 16-row for
-// wo and wo_mlp, 32-row from ~400 tokens up). Ties go to the shorter tile. Large M goes to the
-// throughput kernel's 128 x 128 or 256 x 256 tiles.
+// The tiling for a GEMM on a 256-CU GPU: the cheapest of the latency tiles and the two
+// throughput tiles under a cost model fitted to MI355X sweeps (M = 72 .. 18752, the encoder's
+// four shapes; microseconds).
+//  - Latency tiles (BM = 16/32/48/64 x 64): bound by how fast a CU takes in its tiles'
+//    operands: a fixed ~4 us (launch, first round trip, reduction, epilogue) plus the busiest
+//    CU's operand bytes, ceil(tiles / CUs) x (BM + 64) x K x 2, at about 55 GB/s into one CU.
+//    Ties go to the shorter tile.
+//  - 256 x 256 tiles (one a CU): ~2 us plus ~27.5 us per round of tiles at K = 768.
+//  - 128 x 128 tiles (two a CU): ~2 us plus ~12 us at K = 768 for a CU's first tile; a CU's
+//    second tile runs beside it and adds half that, so l tiles on the busiest CU take
+//    1.5 floor(l / 2) + (l odd) of those.
+// Measured winners: 48-row latency tiles for qkv and wi at 293 tokens, 16-row for wo and
+// wo_mlp, 32-row at 2048 for wo and wo_mlp; 128 x 128 for qkv at 2048 and 8192; 256 x 256
+// for qkv at 4096 and everything at 18752.
 GemmConfig gemm_choose(int m, int n, int k, int cus) {
     if (cus <= 0) cus = 256;
-    if (m >= 2048 && n % 128 == 0 && k % 64 == 0) {
-        // 256 x 256 tiles once they fill half the CUs (one tile a CU; measured: 48 of them lose
-        // to 384 tiles of 128 x 128, 144 and up win), else 128 x 128 (two a CU).
-        const long t256 = (n % 256 == 0) ? (long)(n / 256) * ((m + 255) / 256) : 0;
-        return GemmConfig{2 * t256 >= cus ? 256 : 128, 1};
-    }
     GemmConfig best{32, 1};
     double best_cost = 1e30;
     for (int bm : {16, 32, 48, 64}) {
@@ -220,6 +222,17 @@ GemmConfig gemm_choose(int m, int n, int k, int cus) {
         const long per_cu = (tiles + cus - 1) / cus;
         const double cost = 4.0 + (double)per_cu * (bm + 64) * k * 2 / 55e3;
         if (cost < best_cost - 0.05) best_cost = cost, best = GemmConfig{bm, 1};
+    }
+    if (m >= 1024 && n % 128 == 0 && k % 64 == 0) {
+        const double ks = (double)k / 768.0;
+        const long l128 = ((long)(n / 128) * ((m + 127) / 128) + cus - 1) / cus;
+        const double c128 = 2.0 + 12.0 * ks * (1.5 * (double)(l128 / 2) + (double)(l128 % 2));
+        if (c128 < best_cost) best_cost = c128, best = GemmConfig{128, 1};
+        if (n % 256 == 0) {
+            const long l256 = ((long)(n / 256) * ((m + 255) / 256) + cus - 1) / cus;
+            const double c256 = 2.0 + 27.5 * ks * (double)l256;
+            if (c256 < best_cost) best_cost = c256, best = GemmConfig{256, 1};
+        }
     }
     return best;
 }

@@ -212,9 +212,8 @@ def test_chooser_picks_valid_configs(m, n, k):
 
 
 def test_chooser_matches_the_measured_winners():
-    """The latency tiles' picks at the request lengths measured on MI355X (per-step GEMM times,
-    the fastest tile height within ~0.2 us): qkv/wi 48 rows at 293 tokens and 32 at 1024, wo and
-    wo_mlp 16 rows at 293."""
+    """The picks at the shapes measured on MI355X (per-step GEMM times, the fastest config within
+    a few percent): qkv/wi 48-row latency tiles at 293 tokens, wo and wo_mlp 16 rows."""
     assert jh.gemm_choose(293, 2304, 768, 256)[0] == 48
     assert jh.gemm_choose(293, 768, 768, 256)[0] == 16
     assert jh.gemm_choose(293, 768, 1152, 256)[0] == 16
@@ -222,3 +221,11 @@ def test_chooser_matches_the_measured_winners():
     assert jh.gemm_choose(18752, 2304, 768, 256) == (256, 1)
     assert jh.gemm_choose(4096, 768, 768, 256) == (128, 1)
     assert jh.gemm_choose(18752, 768, 768, 256) == (256, 1)
+    # the throughput tiles' round model: 128 x 128 for qkv at 2048 and 8192 tokens (288 and 1152
+    # tiles), 256 x 256 at 4096 (144 tiles); latency tiles for wo and wo_mlp at 2048 (96
+    # throughput tiles would leave 160 CUs idle)
+    assert jh.gemm_choose(2048, 2304, 768, 256) == (128, 1)
+    assert jh.gemm_choose(8192, 2304, 768, 256) == (128, 1)
+    assert jh.gemm_choose(4096, 2304, 768, 256) == (256, 1)
+    assert jh.gemm_choose(2048, 768, 768, 256)[0] < 128
+    assert jh.gemm_choose(2048, 768, 1152, 256)[0] < 128
