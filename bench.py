@@ -208,8 +208,8 @@ def main():
     dk = kern[dom]
     n, k, epi, _ = STEP_SHAPES[dom]
     bm = dk["config"][0]
-    # the latency kernel's one-block-a-CU instance runs 48- and 64-row grids of at most a block a CU
-    one = bm in (48, 64) and (n // 64) * -(-293 // bm) <= info.cus
+    # the latency kernel's eight-wave instance runs grids of at most a block a CU
+    one = bm < 128 and (n // 64) * -(-293 // bm) <= info.cus
     kname = f"gemm_{'big' if bm >= 128 else ('lat1' if one else 'lat')}<{bm}, {jh.EPI[epi]}>"
     # HBM bytes per dispatch from the committed rocprofv3 counter passes (FETCH_SIZE and
     # WRITE_SIZE, scaled by the library's copy kernel: profiles/traffic_<step>_293.*), when they

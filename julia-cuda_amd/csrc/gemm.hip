@@ -36,14 +36,15 @@ __global__ __launch_bounds__(256, 2) void gemm_lat(GemmParams p) {
     gemm_lat_tile<BM, EPI>(p, blockIdx.x, red, &s_last);
 }
 
-// gemm_lat for grids of at most one block a CU (one request's GEMMs up to ~300 tokens): the
-// block may use every register, and the 48- and 64-row tiles then issue all of a wave's K steps
-// before the first MFMA (one round trip to L2 where the two-block form takes two).
+// gemm_lat for grids of at most one block a CU (one request's GEMMs up to ~300 tokens): eight
+// waves split the tile's K steps, each issuing all of its three to five steps' loads at once. A CU takes in its operands from L2 faster with eight waves loading than
+// with four (measured on MI355X: ~86-94 against ~55-79 GB/s), for twice the partial tiles to sum
+// through LDS. Dynamic LDS: lat_lds_floats<BM, 8>() floats.
 template <int BM, int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_lat1(GemmParams p) {
-    __shared__ __attribute__((aligned(16))) float red[lat_lds_floats<BM>()];
+__global__ __launch_bounds__(512, 1) void gemm_lat1(GemmParams p) {
+    extern __shared__ __attribute__((aligned(16))) float red_dyn[];
     __shared__ uint32_t s_last;
-    gemm_lat_tile<BM, EPI, false, true>(p, blockIdx.x, red, &s_last);
+    gemm_lat_tile<BM, EPI, false, false, 8>(p, blockIdx.x, red_dyn, &s_last);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -151,8 +152,14 @@ static void launch_one(const GemmParams& p, hipStream_t st) {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, Big<B, B>::LDS_BYTES) == hipSuccess;
         if (!lds_ok) throw std::runtime_error("gemm: the throughput kernel cannot have its LDS");
         hipLaunchKernelGGL((gemm_big<B, EPI>), dim3(blocks), dim3(Big<B, B>::THREADS), (Big<B, B>::LDS_BYTES), st, p);
-    } else if ((BM == 48 || BM == 64) && blocks <= device_cus()) {
-        hipLaunchKernelGGL((gemm_lat1<BM == 48 ? 48 : 64, EPI>), dim3(blocks), dim3(256), 0, st, p);
+    } else if (p.splits == 1 && blocks <= device_cus()) {
+        constexpr int B = BM < 128 ? BM : 64;
+        constexpr int LDS = lat_lds_floats<B, 8>() * 4;
+        static const bool lds_ok =  // once per instantiation, before its first launch
+            hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_lat1<B, EPI>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS) == hipSuccess;
+        if (!lds_ok) throw std::runtime_error("gemm: the one-block latency kernel cannot have its LDS");
+        hipLaunchKernelGGL((gemm_lat1<B, EPI>), dim3(blocks), dim3(512), LDS, st, p);
     } else {
         hipLaunchKernelGGL((gemm_lat<BM < 128 ? BM : 64, EPI>), dim3(blocks), dim3(256), 0, st, p);
     }

@@ -9,19 +9,20 @@
 
 namespace jh {
 
-// LDS floats gemm_lat_tile<BM> needs: four waves' partial BM x 64 tiles, rows padded to 68.
-template <int BM>
-constexpr int lat_lds_floats() { return 4 * BM * 68; }
+// LDS floats gemm_lat_tile<BM> needs with NW waves: their partial BM x 64 tiles, rows padded
+// to 68.
+template <int BM, int NW = 4>
+constexpr int lat_lds_floats() { return NW * BM * 68; }
 
 // Shared tail: each thread's 8 values (K fully summed within the block) -> the split-K
-// reduction when the grid splits K -> the epilogue. Thread t owns row (pass * 32 + t / 8) of the
-// tile and columns c0 = 4 (t % 8), c0 + 32 of 64-column group `grp`.
+// reduction when the grid splits K -> the epilogue. Thread t of NT owns row (pass * NT / 8 +
+// t / 8) of the tile and columns c0 = 4 (t % 8), c0 + 32 of 64-column group `grp`.
 //
 // Split-K (kernels/src/gemm.rs:355-433): every block writes its partial to the scratch
 // (device-coherent stores), waits for them to complete, then counts its arrival; the last of the
 // tile's splits (which resets the counter) invalidates its caches and sums all partials in split
 // order, so the result does not depend on arrival order.
-template <int NPASS, int EPI, bool XG = false>
+template <int NPASS, int EPI, bool XG = false, int NT = 256>
 __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8], int tile_id,
                                        int z, int row0, int grp, int rows_in_tile,
                                        uint32_t* s_last, const EpiCol& ec,
@@ -29,13 +30,13 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
     const int tid = threadIdx.x;
     if (p.splits > 1) {
         // [tile][split][pass][half][thread] float4s: coalesced stores and loads.
-        float* part = p.ws + (size_t)(tile_id * p.splits) * NPASS * 2 * 256 * 4;
-        float* mine = part + (size_t)z * NPASS * 2 * 256 * 4;
+        float* part = p.ws + (size_t)(tile_id * p.splits) * NPASS * 2 * NT * 4;
+        float* mine = part + (size_t)z * NPASS * 2 * NT * 4;
 #pragma unroll
         for (int ps = 0; ps < NPASS; ps++)
 #pragma unroll
             for (int h = 0; h < 2; h++)
-                xstore16(mine + ((ps * 2 + h) * 256 + tid) * 4,
+                xstore16(mine + ((ps * 2 + h) * NT + tid) * 4,
                          make_float4(v[ps][4 * h], v[ps][4 * h + 1], v[ps][4 * h + 2], v[ps][4 * h + 3]));
         release_wait();
         __syncthreads();
@@ -54,12 +55,12 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
 #pragma unroll
             for (int e = 0; e < 8; e++) v[ps][e] = 0.0f;
         for (int zz = 0; zz < p.splits; zz++) {
-            const float* src = part + (size_t)zz * NPASS * 2 * 256 * 4;
+            const float* src = part + (size_t)zz * NPASS * 2 * NT * 4;
 #pragma unroll
             for (int ps = 0; ps < NPASS; ps++)
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
-                    const float4 q = xload16f(src + ((ps * 2 + h) * 256 + tid) * 4);
+                    const float4 q = xload16f(src + ((ps * 2 + h) * NT + tid) * 4);
                     v[ps][4 * h] += q.x;
                     v[ps][4 * h + 1] += q.y;
                     v[ps][4 * h + 2] += q.z;
@@ -70,18 +71,19 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
     const int c0 = (tid & 7) * 4;
 #pragma unroll
     for (int ps = 0; ps < NPASS; ps++) {
-        const int r = ps * 32 + (tid >> 3);
+        const int r = ps * (NT / 8) + (tid >> 3);
         const int row = row0 + r;
         epi_apply<EPI, XG>(p, row, grp, c0, v[ps], r < rows_in_tile && row < p.m, ec, er[ps]);
     }
 }
 
-// Task `task` (of tiles_n * tiles_m * splits; XCD-mapped) of c = epilogue(a . w^T). The four
-// waves split the tile's K steps between them; `red` is lat_lds_floats<BM>() floats of LDS.
+// Task `task` (of tiles_n * tiles_m * splits; XCD-mapped) of c = epilogue(a . w^T). The NW
+// waves split the tile's K steps between them; `red` is lat_lds_floats<BM, NW>() floats of LDS.
 // Every thread of the block calls it; it ends with a block barrier, so the caller may reuse
-// `red` right after. ONE: the block has its CU to itself (512 registers a lane), so that the
-// 48- and 64-row tiles hold every K step of a wave in flight at once.
-template <int BM, int EPI, bool XG = false, bool ONE = false>
+// `red` right after. ONE: the block has its CU to itself (four waves: 512 registers a lane),
+// so that the 48- and 64-row tiles hold every K step of a wave in flight at once. Eight waves
+// (NW = 8) take a CU's operand loads at a higher rate than four.
+template <int BM, int EPI, bool XG = false, bool ONE = false, int NW = 4>
 __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, float* red,
                                               uint32_t* s_last, uint64_t* sub = nullptr) {
     auto mark = [&](int i) {  // profiling: thread 0's view of the task's stages
@@ -89,7 +91,8 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     };
     mark(0);
     constexpr int MI = BM / 16;
-    constexpr int NPASS = (BM + 31) / 32;
+    constexpr int RPP = 8 * NW;                     // tile rows a pass of the epilogue
+    constexpr int NPASS = (BM + RPP - 1) / RPP;
     const int T = p.tiles_n * p.tiles_m * p.splits;
     const int L = xcd_task(task, T);
     const int z = L % p.splits, t2 = L / p.splits;
@@ -97,10 +100,10 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     const int tid = threadIdx.x, l = tid & 63, r16 = l & 15, g = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
 
-    // This block's K steps (32 wide), then this wave's quarter of them.
+    // This block's K steps (32 wide), then this wave's share of them.
     const int U = p.k >> 5;
     const int ub = z * U / p.splits, ue = (z + 1) * U / p.splits, nu = ue - ub;
-    const int u0 = ub + w * nu / 4, u1 = ub + (w + 1) * nu / 4;
+    const int u0 = ub + w * nu / NW, u1 = ub + (w + 1) * nu / NW;
 
     const f16* ap[MI];
 #pragma unroll
@@ -114,7 +117,7 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     EpiRow er[NPASS];
     epi_load_col<EPI>(p, bx, c0, ec);
 #pragma unroll
-    for (int ps = 0; ps < NPASS; ps++) epi_load_row<EPI, XG>(p, by * BM + ps * 32 + (tid >> 3), bx, c0, er[ps]);
+    for (int ps = 0; ps < NPASS; ps++) epi_load_row<EPI, XG>(p, by * BM + ps * RPP + (tid >> 3), bx, c0, er[ps]);
 
     floatx4 acc[MI][4];
 #pragma unroll
@@ -190,7 +193,40 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
             if (u + 3 * UC < u1) load(fa1, fw1, u + 3 * UC);
         }
     };
-    if (ONE && MI > 1) {
+    // Every K step of the wave in one chunk (eight waves: three to five steps a wave).
+    auto kone = [&](auto uc_) {
+        constexpr int UC = decltype(uc_)::value;
+        half8 fa[UC][MI], fw[UC][4];
+        const auto wr = buffer_rsrc((const f16*)p.w + ((size_t)bx * U + u0) * 2048,
+                                    (uint32_t)(u1 - u0) * 4096);
+#pragma unroll
+        for (int s = 0; s < UC; s++) {
+            const int uu = min(u0 + s, u1 - 1);
+#pragma unroll
+            for (int j = 0; j < 4; j++) fw[s][j] = bload16<false>(wr, (uint32_t)s * 4096 + j * 1024 + l * 16);
+#pragma unroll
+            for (int i = 0; i < MI; i++) fa[s][i] = load16h<XG>(ap[i] + uu * 32);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, c0, er[ps]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < UC; s++) {
+            const uint32_t keep = u0 + s < u1 ? 0xffffffffu : 0u;
+#pragma unroll
+            for (int i = 0; i < MI; i++) {
+                const half8 a = mask16(fa[s][i], keep);
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = mfma16(fw[s][j], a, acc[i][j]);
+            }
+        }
+    };
+    if (NW == 8 && u1 - u0 <= 3) {
+        kone(std::integral_constant<int, 3>{});
+    } else if (NW == 8 && u1 - u0 <= 5) {
+        kone(std::integral_constant<int, 5>{});
+    } else if (ONE && MI > 1) {
         if (u1 - u0 > 6)
             kloop(std::integral_constant<int, 5>{});
         else
@@ -214,12 +250,12 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     float v[NPASS][8];
 #pragma unroll
     for (int ps = 0; ps < NPASS; ps++) {
-        const int r = ps * 32 + (tid >> 3);
+        const int r = ps * RPP + (tid >> 3);
 #pragma unroll
         for (int e = 0; e < 8; e++) v[ps][e] = 0.0f;
         if (r < BM) {
 #pragma unroll
-            for (int ww = 0; ww < 4; ww++) {
+            for (int ww = 0; ww < NW; ww++) {
                 const float4 lo = *(const float4*)&red[(ww * BM + r) * 68 + c0];
                 const float4 hi = *(const float4*)&red[(ww * BM + r) * 68 + 32 + c0];
                 v[ps][0] += lo.x, v[ps][1] += lo.y, v[ps][2] += lo.z, v[ps][3] += lo.w;
@@ -229,7 +265,7 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     }
     __syncthreads();  // red is free again
     mark(2);
-    finish<NPASS, EPI, XG>(p, v, bx * p.tiles_m + by, z, by * BM, bx, BM, s_last, ec, er);
+    finish<NPASS, EPI, XG, 64 * NW>(p, v, bx * p.tiles_m + by, z, by * BM, bx, BM, s_last, ec, er);
     mark(3);
 }
 
