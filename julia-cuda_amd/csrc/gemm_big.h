@@ -135,10 +135,12 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     // ---- the K loop ---------------------------------------------------------------------------
     // Stage copies: copy q of the wave's LOADS is load I = w + NWAVES q of the stage's A_BYTES / 1024
     // a loads then W_BYTES / 1024 w loads.
+    // (Copies q < LOADS / 2 are a's, the rest w's: the test is on the unrolled q, no branch.)
+    static_assert(C::A_BYTES == C::W_BYTES && C::LOADS % 2 == 0, "half the copies a's");
     auto issue_one = [&](int kt, int buf, int q) {
         char* st = lds + buf * C::STAGE;
         const int I = w + C::NWAVES * q;
-        if (I < C::A_BYTES / 1024) {
+        if (q < C::LOADS / 2) {
             const int r = 16 * I + (l >> 2), ch = (l & 3) ^ ((r >> 2) & 3);
             const int row = min(by * BM + r, p.m - 1);
             const f16* src = (const f16*)p.a + (size_t)row * p.k + kt * 32 + ch * 8;
@@ -237,7 +239,12 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     // used. (__syncthreads' release fence would wait for all of this wave's copies.)
     constexpr int NM = MR * NC, PER = C::LOADS, GAP = NM / PER;
     static_assert(GAP >= 1, "copies per K-16 step");
-    for (int s = 0; s < nkt; s++) {
+    // One stage. NEXT: a stage follows (wait for its copies, NEXT_LAST: they are the last ones in
+    // flight); MORE: stage s + 3 exists. The stages up to nkt - 4 take every branch one way, so
+    // the loop over them is straight-line code and the last three are peeled.
+    auto stage_body = [&](int s, auto next_, auto next_last_, auto more_) {
+        constexpr bool NEXT = decltype(next_)::value, NEXT_LAST = decltype(next_last_)::value;
+        constexpr bool MORE = decltype(more_)::value;
 #pragma unroll
         for (int x = 0; x < NM; x++) {
             const int i = x / NC, c = x % NC;
@@ -247,29 +254,34 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
             if (x < NR) rd(s, 1, x);
         }
         __builtin_amdgcn_sched_barrier(0);
-        const bool next = s + 1 < nkt;
-        if (next) {
-            if (s + 2 < nkt)
-                wait_vmcnt<C::LOADS>();
-            else
+        if (NEXT) {
+            if (NEXT_LAST)
                 wait_vmcnt<0>();
+            else
+                wait_vmcnt<C::LOADS>();
             __builtin_amdgcn_s_barrier();
         }
-        const bool more = s + 3 < nkt;
 #pragma unroll
         for (int x = 0; x < NM; x++) {
             const int i = x / NC, c = x % NC;
             __builtin_amdgcn_sched_barrier(0);
             acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fw[1][c], fa[1][i], acc[i][c], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
-            if (next && x < NR) rd(s + 1, 0, x);
-            if (x % GAP == GAP - 1 && x / GAP < PER) {
+            if (NEXT && x < NR) rd(s + 1, 0, x);
+            if (MORE && x % GAP == GAP - 1 && x / GAP < PER) {
                 __builtin_amdgcn_sched_barrier(0);
-                if (more) issue_one(s + 3, (s + 3) % C::NSTAGE, x / GAP);
+                issue_one(s + 3, (s + 3) % C::NSTAGE, x / GAP);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-    }
+    };
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    int s = 0;
+    for (; s + 3 < nkt; s++) stage_body(s, T_{}, F_{}, T_{});
+    if (s + 2 < nkt) stage_body(s++, T_{}, F_{}, F_{});
+    if (s + 1 < nkt) stage_body(s++, T_{}, T_{}, F_{});
+    stage_body(s, F_{}, F_{}, F_{});
     mark(2);
 
     // ---- the epilogue -------------------------------------------------------------------------
