@@ -117,6 +117,14 @@ int julia_hip_gemm(const julia_hip_gemm_args *g, julia_hip_gemm_config cfg,
 int julia_hip_attention(const void *qkv, void *o, int n, int d, int window, int chunks,
                         const julia_hip_scratch *s, void *stream, char *err, size_t err_len);
 
+/* julia_hip_attention over concatenated sequences (config 5's batch): seg [n][2] (int32, on
+ * the device) holds each row's sequence start and end, and a query sees only the keys of its
+ * own sequence. No counterpart in the reference: its batch runs requests one at a time.
+ * chunks must be 1. */
+int julia_hip_attention_seg(const void *qkv, void *o, int n, int d, int window,
+                            const int32_t *seg, const julia_hip_scratch *s, void *stream,
+                            char *err, size_t err_len);
+
 /* src/lib.rs:177-219 `embed_into`: x [n][d] = LN(table[ids]) . gamma (ids on the device). */
 int julia_hip_embed(const uint32_t *ids, int n, const void *table, int vocab, int d,
                     const float *gamma, float eps, void *x, void *stream, char *err,

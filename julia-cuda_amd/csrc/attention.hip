@@ -26,6 +26,12 @@
 
 namespace jh {
 
+// The streaming 64-query tile for long concatenated inputs (one key range).
+__global__ __launch_bounds__(256) void attention_stream_kernel(AttnParams p) {
+    __shared__ __attribute__((aligned(16))) char lds[ATT_STREAM_LDS];
+    attention_stream_tile(p, blockIdx.x, lds);
+}
+
 __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) f16 lds[ATT_LDS_F16];
     __shared__ uint32_t s_last;
@@ -140,6 +146,8 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
             hipLaunchKernelGGL(attention_lds_kernel<8>, grid, dim3(512), att_lds_bytes(gkeys, 8), st, p, gkeys);
         else
             hipLaunchKernelGGL(attention_lds_kernel<4>, grid, dim3(256), att_lds_bytes(gkeys, 4), st, p, gkeys);
+    } else if (chunks == 1) {
+        hipLaunchKernelGGL(attention_stream_kernel, dim3((n + 63) / 64 * (d / 64)), dim3(256), 0, st, p);
     } else {
         hipLaunchKernelGGL(attention_kernel, dim3((n + 63) / 64, d / 64, chunks), dim3(256), 0, st, p);
     }

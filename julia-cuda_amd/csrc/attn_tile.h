@@ -288,6 +288,10 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
     }
     const bool one_seq = !p.seg || p.seg[2 * q0] == p.seg[2 * qlast];
     const int ulo = p.seg ? p.seg[2 * q0] : 0, uhi = p.seg ? p.seg[2 * qlast + 1] : n;  // uniform
+    // The lane's valid keys: its sequence cut to the window, [klo, khi).
+    const int wl = p.window > 0 ? p.window : (1 << 30);
+    const int klo = max(slo, qi - wl), khi = min(shi, qi + wl + 1);
+    const uint32_t kspan = khi > klo ? (uint32_t)(khi - klo) : 0u;
     const float scale = 1.4426950408889634f / 8.0f;  // log2(e) / sqrt(64)
     float mx = -INFINITY, lsum = 0.0f;
     floatx4 oacc[4];
@@ -344,22 +348,21 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
                 for (int t = 0; t < 2; t++)
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        sc[t][e] *= scale;
                         bm = fmaxf(bm, sc[t][e]);
                     }
             } else {
+                // key kb + 16 t + 4 g + e is valid iff it lies in [klo, khi)
+                const int base = kb + 4 * g - klo;
 #pragma unroll
                 for (int t = 0; t < 2; t++)
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        const int key = kb + 16 * t + 4 * g + e;
-                        const int dist = qi > key ? qi - key : key - qi;
-                        const bool ok = key >= slo && key < shi && (p.window == 0 || dist <= p.window);
-                        sc[t][e] = ok ? sc[t][e] * scale : -INFINITY;
+                        const bool ok = (uint32_t)(base + 16 * t + e) < kspan;
+                        sc[t][e] = ok ? sc[t][e] : -INFINITY;
                         bm = fmaxf(bm, sc[t][e]);
                     }
             }
-            bm = max_xor32(max_xor16(bm));
+            bm = max_xor32(max_xor16(bm)) * scale;  // the scores stay unscaled until the exponent
             const float mnew = fmaxf(mx, bm);
             const float base = mnew == -INFINITY ? 0.0f : mnew;  // no valid key yet: exp2(-inf) = 0
             const float alpha = fast_exp2(mx - base);
@@ -369,7 +372,7 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
             for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    sc[t][e] = fast_exp2(sc[t][e] - base);
+                    sc[t][e] = fast_exp2(fmaf(sc[t][e], scale, -base));
                     rs += sc[t][e];
                 }
             lsum = lsum * alpha + rs;
@@ -435,6 +438,195 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
         if (sub) {
             release_wait();
             mark(2);
+        }
+    }
+    __syncthreads();  // LDS is free again
+}
+
+// ---- the streaming 64-query tile: long concatenated inputs -----------------------------------
+// A task is (64 queries, head): each of the four waves runs the online softmax over every key of
+// the tile's range for its own 16 queries (no merge between waves). The key range (cut to the
+// rows' sequences and the window) goes through NS LDS stages of 64 keys, K and V row-major and
+// swizzled as in the slice tile, filled by direct global -> LDS loads two blocks ahead of the
+// MFMAs; a 64-key block is two of the slice tile's 32-key steps. Each key is read once per 64
+// queries, and with three blocks a CU (48 KB of LDS each) the waves hide each other's step
+// latencies.
+constexpr int ATT_STREAM_STAGES = 3;
+constexpr int ATT_STREAM_LDS = ATT_STREAM_STAGES * 16384;
+
+// Task `task` of (n + 63) / 64 query blocks x heads (XCD-mapped); `lds`: ATT_STREAM_LDS bytes.
+// Ends with a block barrier.
+__device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int task, char* lds) {
+    constexpr int NS = ATT_STREAM_STAGES;
+    const int n = p.n, d = p.d, ld = 3 * d, heads = d >> 6;
+    const int tiles = (n + 63) >> 6;
+    const int L = xcd_task(task, tiles * heads);
+    const int h = L / tiles, q0 = (L % tiles) * 64;
+    const int tid = threadIdx.x, l = tid & 63, r16 = l & 15, g = l >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int j = r16 >> 2, q = r16 & 3;
+
+    // The tile's keys: from its first row's sequence start to its last row's sequence end, cut
+    // to the window; 64-aligned blocks.
+    const int qlast = min(q0 + 63, n - 1);
+    int k0 = p.seg ? p.seg[2 * q0] : 0, k1 = p.seg ? p.seg[2 * qlast + 1] : n;
+    if (p.window > 0) {
+        k0 = max(k0, q0 - p.window);
+        k1 = min(k1, q0 + 64 + p.window);
+    }
+    k0 &= ~63;
+    const int nblk = k1 > k0 ? (k1 - k0 + 63) >> 6 : 0;
+
+    // This lane's query and its sequence; the wave's 16 queries' common bounds (uniform).
+    const int qi = q0 + 16 * w + r16;
+    const int qc = min(qi, n - 1);
+    int slo = 0, shi = n;
+    if (p.seg) slo = p.seg[2 * qc], shi = p.seg[2 * qc + 1];
+    const int wq0 = min(q0 + 16 * w, n - 1), wql = min(q0 + 16 * w + 15, n - 1);
+    const bool one_seq = !p.seg || p.seg[2 * wq0] == p.seg[2 * wql];
+    const int ulo = p.seg ? p.seg[2 * wq0] : 0, uhi = p.seg ? p.seg[2 * wql + 1] : n;
+    const int wl = p.window > 0 ? p.window : (1 << 30);  // the lane's valid keys: [klo, khi)
+    const int klo = max(slo, qi - wl), khi = min(shi, qi + wl + 1);
+    const uint32_t kspan = khi > klo ? (uint32_t)(khi - klo) : 0u;
+    half8 qf[2];
+    {
+        const f16* qp = (const f16*)p.qkv + (size_t)qc * ld + h * 64 + 8 * g;
+        qf[0] = load16h<false>(qp);
+        qf[1] = load16h<false>(qp + 32);
+    }
+
+    // Block b (keys k0 + 64 b ..) into stage b % NS: 16 wave loads of 1 KB (8 rows of K, then of
+    // V), four a wave; lane l fills LDS chunk 64 I' + l = row c / 8, logical chunk (c % 8) ^ (row
+    // % 8). Rows past n are clamped (their keys are masked).
+    auto stage = [&](int b) {
+        char* dst = lds + (b % NS) * 16384;
+        const int kb = k0 + 64 * b;
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+            const int I = (w + 4 * qq) & 7;  // copies qq < 2 are K's, the rest V's
+            const int c = I * 64 + l, row = c >> 3, ch = (c & 7) ^ (row & 7);
+            const int col = (qq < 2 ? d : 2 * d) + h * 64;
+            const f16* src = (const f16*)p.qkv + (size_t)min(kb + row, n - 1) * ld + col + ch * 8;
+            lds_dma16<false>(src, dst + (qq < 2 ? 0 : 8192) + I * 1024);
+        }
+    };
+
+    const float scale = 1.4426950408889634f / 8.0f;  // log2(e) / sqrt(64)
+    float mx = -INFINITY, lsum = 0.0f;
+    floatx4 oacc[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) oacc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    if (nblk > 0) stage(0);
+    if (nblk > 1) stage(1);
+    for (int b = 0; b < nblk; b++) {
+        // Block b's copies done (block b + 1's may stay in flight; the query loads came first),
+        // then every wave's: and every wave is done with block b - 1, whose stage block b + 2
+        // takes.
+        if (b + 1 < nblk)
+            wait_vmcnt<4>();
+        else
+            wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        if (b + 2 < nblk) stage(b + 2);
+        const char* ks = lds + (b % NS) * 16384;
+        const char* vs = ks + 8192;
+        // The 64 keys in one step: S^T for keys kb + 16 t + 4 g + e (t < 4), one max and one
+        // rescale; P . V in two K-32 halves.
+        const int kb = k0 + 64 * b;
+        half8 kf[4][2];
+        half4 vlo[2][4], vhi[2][4];
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int k2 = 0; k2 < 2; k2++)
+                kf[t][k2] = *(const half8*)(ks + att_swz(16 * t + r16, 4 * k2 + g));
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++)
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                const int ch = 2 * dt + (q >> 1), off = (q & 1) * 8;
+                vlo[hf][dt] = lds_read_tr16(vs + att_swz(32 * hf + 4 * g + j, ch) + off);
+                vhi[hf][dt] = lds_read_tr16(vs + att_swz(32 * hf + 16 + 4 * g + j, ch) + off);
+            }
+        __builtin_amdgcn_sched_barrier(0);
+        floatx4 sc[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            sc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int k2 = 0; k2 < 2; k2++) sc[t] = mfma16(kf[t][k2], qf[k2], sc[t]);
+        }
+        const bool full = one_seq && kb >= ulo && kb + 64 <= uhi &&
+                          (p.window == 0 || (wql - kb <= p.window && kb + 63 - wq0 <= p.window));
+        float bm = -INFINITY;
+        if (full) {
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    bm = fmaxf(bm, sc[t][e]);
+                }
+        } else {
+            // key kb + 16 t + 4 g + e is valid iff it lies in [klo, khi)
+            const int base = kb + 4 * g - klo;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const bool ok = (uint32_t)(base + 16 * t + e) < kspan;
+                    sc[t][e] = ok ? sc[t][e] : -INFINITY;
+                    bm = fmaxf(bm, sc[t][e]);
+                }
+        }
+        bm = max_xor32(max_xor16(bm)) * scale;  // the scores stay unscaled until the exponent
+        const float mnew = fmaxf(mx, bm);
+        const float base = mnew == -INFINITY ? 0.0f : mnew;  // no valid key yet: exp2(-inf) = 0
+        const float alpha = fast_exp2(mx - base);
+        // The output needs rescaling only where a lane's max rose (alpha < 1): skipped when no
+        // lane of the wave has (a wave-uniform test).
+        const bool rescale = __builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0;
+        mx = mnew;
+        float rs = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                sc[t][e] = fast_exp2(fmaf(sc[t][e], scale, -base));
+                rs += sc[t][e];
+            }
+        lsum = lsum * alpha + rs;
+        if (rescale) {
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) oacc[dt] = oacc[dt] * alpha;
+        }
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++) {
+            half8 pf;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                pf[e] = (f16)sc[2 * hf][e];
+                pf[4 + e] = (f16)sc[2 * hf + 1][e];
+            }
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++) {
+                const half4 lo = vlo[hf][dt], hi = vhi[hf][dt];
+                const half8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                oacc[dt] = mfma16(vf, pf, oacc[dt]);
+            }
+        }
+    }
+
+    const float tot = sum_xor32(sum_xor16(lsum));
+    const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+    if (qi < n) {
+        f16* op = (f16*)p.o + (size_t)qi * d + h * 64 + 4 * g;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            half4 ov;
+#pragma unroll
+            for (int e = 0; e < 4; e++) ov[e] = (f16)(oacc[dt][e] * inv);
+            store8<false>(op + 16 * dt, ov);
         }
     }
     __syncthreads();  // LDS is free again

@@ -226,6 +226,14 @@ __device__ __forceinline__ half8 bload16(__amdgpu_buffer_rsrc_t r, uint32_t byte
     return __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, XG ? 16 : 0));
 }
 
+// s_waitcnt with vmcnt = n (n < 64) and no wait on the other counters (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0 and vmcnt[5:4] in bits 15:14, expcnt in 6:4, lgkmcnt in 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
 // gfx950's direct global -> LDS load: each lane's 16 bytes at `src` land at LDS `base` + 16 lane
 // (base is wave-uniform). Counted like any vector load: s_waitcnt vmcnt covers it. XG: the read
 // is device-coherent (sc1), for data another block wrote in this kernel.

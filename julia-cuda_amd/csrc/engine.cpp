@@ -609,6 +609,16 @@ int julia_hip_attention(const void* qkv, void* o, int n, int d, int window, int 
     });
 }
 
+int julia_hip_attention_seg(const void* qkv, void* o, int n, int d, int window,
+                            const int32_t* seg, const julia_hip_scratch* s, void* stream, char* err,
+                            size_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!seg) throw std::runtime_error("attention: no sequence bounds");
+        attention_launch((const jh_half*)qkv, (jh_half*)o, n, d, window, 1, scratch_of(s),
+                         (hipStream_t)stream, seg);
+    });
+}
+
 int julia_hip_embed(const uint32_t* ids, int n, const void* table, int vocab, int d,
                     const float* gamma, float eps, void* x, void* stream, char* err,
                     size_t err_len) {

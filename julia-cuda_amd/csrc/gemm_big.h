@@ -61,14 +61,6 @@ struct Big {
 // tiles take LayerNorm epilogues for K <= 64 * 2 * BIG_LN_SLOTS.
 constexpr int BIG_LN_SLOTS = 8;
 
-// s_waitcnt with vmcnt = n (n < 64) and no wait on the other counters (gfx9 encoding:
-// vmcnt[3:0] in bits 3:0 and vmcnt[5:4] in bits 15:14, expcnt in 6:4, lgkmcnt in 11:8).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt field");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
-}
-
 // Task `task` of tiles_n * tiles_m (XCD-mapped: an XCD takes a contiguous range of tasks, in the
 // grouped order below). AX: a is read device-coherent; XG: the outputs are stored and the
 // statistics read device-coherent. The residual is read through the caches.

@@ -78,6 +78,7 @@ class EngineInfo(ctypes.Structure):
 EXPORTS = [
     "julia_cuda_tier", "julia_cuda_load", "julia_cuda_free", "julia_cuda_device", "julia_cuda_run",
     "julia_hip_scratch_new", "julia_hip_scratch_free", "julia_hip_gemm", "julia_hip_attention",
+    "julia_hip_attention_seg",
     "julia_hip_embed", "julia_hip_norm_add", "julia_hip_score", "julia_hip_time_gemm",
     "julia_hip_time_attention", "julia_hip_time_copy", "julia_hip_copy", "julia_hip_device_count",
     "julia_hip_prep_fold_layernorm", "julia_hip_prep_fold_layernorm_bias",
@@ -113,6 +114,7 @@ def lib():
         "julia_hip_scratch_free": (None, [_VP]),
         "julia_hip_gemm": (_I, [ctypes.POINTER(GemmArgs), GemmConfig, _VP, _VP, _CP, _SZ]),
         "julia_hip_attention": (_I, [_VP, _VP, _I, _I, _I, _I, _VP, _VP, _CP, _SZ]),
+        "julia_hip_attention_seg": (_I, [_VP, _VP, _I, _I, _I, _VP, _VP, _VP, _CP, _SZ]),
         "julia_hip_embed": (_I, [_VP, _I, _VP, _I, _I, _VP, _F, _VP, _VP, _CP, _SZ]),
         "julia_hip_norm_add": (_I, [_VP, _I, _I, _VP, _VP, _F, _VP, _VP, _VP, _CP, _SZ]),
         "julia_hip_score": (_I, [_VP, _I, _I, _VP, _F, _VP, _I, _VP, _VP, _CP, _SZ]),
@@ -355,6 +357,12 @@ def time_gemm(args, bm=0, splits=1, scratch=None, warmup=20, batches=10, per_bat
 
 def attention(qkv, o, n, d, window=0, chunks=1, scratch=None, stream=0):
     _call(lib().julia_hip_attention, qkv, o, n, d, window, chunks,
+          scratch.ptr if scratch else None, stream or None)
+
+
+def attention_seg(qkv, o, n, d, window, seg, scratch=None, stream=0):
+    """Attention over concatenated sequences: seg is the device address of [n][2] int32 bounds."""
+    _call(lib().julia_hip_attention_seg, qkv, o, n, d, window, seg,
           scratch.ptr if scratch else None, stream or None)
 
 

@@ -223,6 +223,32 @@ def test_config3_attention(torch_cuda, scratch, n, window, chunks):
     say(f"  vs f64 {rel:.2e} (max {mrel:.2e}), vs emulation {erel:.2e}")
 
 
+@pytest.mark.parametrize("lens", [[300, 1024, 17, 700, 1, 513], [70, 130, 45, 200, 64]])
+@pytest.mark.parametrize("window", [0, 64])
+def test_attention_over_concatenated_sequences(torch_cuda, scratch, lens, window):
+    """Config 5's batched attention: sequences concatenated into one set of rows, each query
+    seeing only its own sequence's keys (past 2048 rows the streaming 64-query tile, below it the
+    slice tile), against the f64 attention of each sequence alone."""
+    say(f"attention over {len(lens)} sequences ({sum(lens)} rows) window={window}")
+    torch = torch_cuda
+    n = sum(lens)
+    rng = np.random.default_rng(300 + n + window)
+    qkv16 = rand16(rng, (n, 3 * 768))
+    starts = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    seg = np.zeros((n, 2), np.int32)
+    for a, b in zip(starts[:-1], starts[1:]):
+        seg[a:b, 0], seg[a:b, 1] = a, b
+    q, sg = to_dev(torch, qkv16), to_dev(torch, seg)
+    o = torch.full((n, 768), float("nan"), dtype=torch.float16, device="cuda")
+    jh.attention_seg(q.data_ptr(), o.data_ptr(), n, 768, window, sg.data_ptr(), scratch,
+                     stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    out = f32(f16_bits(o))
+    for a, b in zip(starts[:-1], starts[1:]):
+        ref = O.attention(f32(qkv16[a:b]), window)
+        compare(out[a:b], ref, ATTN_REL, what=f"rows {a}:{b} window {window}")
+
+
 def test_attention_d384_and_tail(torch_cuda, scratch):
     """The real Julia-1 width (6 heads) and a length that is not a multiple of 64."""
     torch = torch_cuda
