@@ -443,8 +443,8 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
     __syncthreads();  // LDS is free again
 }
 
-// ---- the streaming 64-query tile: long concatenated inputs -----------------------------------
-// A task is (64 queries, head): each of the four waves runs the online softmax over every key of
+// ---- the streaming tile: long concatenated inputs ---------------------------------------------
+// A task is (16 NW queries, head): each of the NW waves runs the online softmax over every key of
 // the tile's range for its own 16 queries (no merge between waves). The key range (cut to the
 // rows' sequences and the window) goes through NS LDS stages of 64 keys, K and V row-major and
 // swizzled as in the slice tile, filled by direct global -> LDS loads two blocks ahead of the
@@ -454,25 +454,29 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
 constexpr int ATT_STREAM_STAGES = 3;
 constexpr int ATT_STREAM_LDS = ATT_STREAM_STAGES * 16384;
 
-// Task `task` of (n + 63) / 64 query blocks x heads (XCD-mapped); `lds`: ATT_STREAM_LDS bytes.
-// Ends with a block barrier.
+// Task `task` of (n + 16 NW - 1) / (16 NW) query blocks x heads (XCD-mapped); `lds`:
+// ATT_STREAM_LDS bytes. XS: o is stored device-coherent (the persistent kernel). Ends with a
+// block barrier.
+template <bool XS = false, int NW = 4>
 __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int task, char* lds) {
-    constexpr int NS = ATT_STREAM_STAGES;
+    constexpr int NS = ATT_STREAM_STAGES, QB = 16 * NW;
+    constexpr int LOADS = 16 / NW;  // 1 KB copies a wave per stage
+    static_assert(NW == 4 || NW == 8, "waves");
     const int n = p.n, d = p.d, ld = 3 * d, heads = d >> 6;
-    const int tiles = (n + 63) >> 6;
+    const int tiles = (n + QB - 1) / QB;
     const int L = xcd_task(task, tiles * heads);
-    const int h = L / tiles, q0 = (L % tiles) * 64;
+    const int h = L / tiles, q0 = (L % tiles) * QB;
     const int tid = threadIdx.x, l = tid & 63, r16 = l & 15, g = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int j = r16 >> 2, q = r16 & 3;
 
     // The tile's keys: from its first row's sequence start to its last row's sequence end, cut
     // to the window; 64-aligned blocks.
-    const int qlast = min(q0 + 63, n - 1);
+    const int qlast = min(q0 + QB - 1, n - 1);
     int k0 = p.seg ? p.seg[2 * q0] : 0, k1 = p.seg ? p.seg[2 * qlast + 1] : n;
     if (p.window > 0) {
         k0 = max(k0, q0 - p.window);
-        k1 = min(k1, q0 + 64 + p.window);
+        k1 = min(k1, q0 + QB + p.window);
     }
     k0 &= ~63;
     const int nblk = k1 > k0 ? (k1 - k0 + 63) >> 6 : 0;
@@ -488,6 +492,10 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
     const int wl = p.window > 0 ? p.window : (1 << 30);  // the lane's valid keys: [klo, khi)
     const int klo = max(slo, qi - wl), khi = min(shi, qi + wl + 1);
     const uint32_t kspan = khi > klo ? (uint32_t)(khi - klo) : 0u;
+    // Keys any of the wave's 16 queries may see, [wlo, whi): the wave skips the MFMAs and the
+    // softmax of a block wholly outside (every score masked: the step would change nothing).
+    const int wlo = __builtin_amdgcn_readfirstlane(max(ulo, wq0 - wl));
+    const int whi = __builtin_amdgcn_readfirstlane(min(p.seg ? p.seg[2 * wql + 1] : n, wql + wl + 1));
     half8 qf[2];
     {
         const f16* qp = (const f16*)p.qkv + (size_t)qc * ld + h * 64 + 8 * g;
@@ -496,18 +504,19 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
     }
 
     // Block b (keys k0 + 64 b ..) into stage b % NS: 16 wave loads of 1 KB (8 rows of K, then of
-    // V), four a wave; lane l fills LDS chunk 64 I' + l = row c / 8, logical chunk (c % 8) ^ (row
+    // V), LOADS a wave; lane l fills LDS chunk 64 I + l = row c / 8, logical chunk (c % 8) ^ (row
     // % 8). Rows past n are clamped (their keys are masked).
     auto stage = [&](int b) {
         char* dst = lds + (b % NS) * 16384;
         const int kb = k0 + 64 * b;
 #pragma unroll
-        for (int qq = 0; qq < 4; qq++) {
-            const int I = (w + 4 * qq) & 7;  // copies qq < 2 are K's, the rest V's
+        for (int qq = 0; qq < LOADS; qq++) {
+            const bool kk = qq < LOADS / 2;  // the first half of a wave's copies are K's
+            const int I = (w + NW * qq) & 7;
             const int c = I * 64 + l, row = c >> 3, ch = (c & 7) ^ (row & 7);
-            const int col = (qq < 2 ? d : 2 * d) + h * 64;
+            const int col = (kk ? d : 2 * d) + h * 64;
             const f16* src = (const f16*)p.qkv + (size_t)min(kb + row, n - 1) * ld + col + ch * 8;
-            lds_dma16<false>(src, dst + (qq < 2 ? 0 : 8192) + I * 1024);
+            lds_dma16<false>(src, dst + (kk ? 0 : 8192) + I * 1024);
         }
     };
 
@@ -524,16 +533,17 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
         // then every wave's: and every wave is done with block b - 1, whose stage block b + 2
         // takes.
         if (b + 1 < nblk)
-            wait_vmcnt<4>();
+            wait_vmcnt<LOADS>();
         else
             wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
         if (b + 2 < nblk) stage(b + 2);
+        const int kb = k0 + 64 * b;
+        if (kb + 64 <= wlo || kb >= whi) continue;
         const char* ks = lds + (b % NS) * 16384;
         const char* vs = ks + 8192;
         // The 64 keys in one step: S^T for keys kb + 16 t + 4 g + e (t < 4), one max and one
         // rescale; P . V in two K-32 halves.
-        const int kb = k0 + 64 * b;
         half8 kf[4][2];
         half4 vlo[2][4], vhi[2][4];
 #pragma unroll
@@ -626,7 +636,7 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
             half4 ov;
 #pragma unroll
             for (int e = 0; e < 4; e++) ov[e] = (f16)(oacc[dt][e] * inv);
-            store8<false>(op + 16 * dt, ov);
+            store8<XS>(op + 16 * dt, ov);
         }
     }
     __syncthreads();  // LDS is free again

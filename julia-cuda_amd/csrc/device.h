@@ -226,6 +226,14 @@ __device__ __forceinline__ half8 bload16(__amdgpu_buffer_rsrc_t r, uint32_t byte
     return __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, XG ? 16 : 0));
 }
 
+// 16-byte buffer store at byte_off; with XG device-coherent (sc1) in one instruction, where a
+// coherent global store takes two 8-byte ones.
+template <bool XG>
+__device__ __forceinline__ void bstore16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, half8 v) {
+    typedef int int4_t __attribute__((ext_vector_type(4)));
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4_t, v), r, byte_off, 0, XG ? 16 : 0);
+}
+
 // s_waitcnt with vmcnt = n (n < 64) and no wait on the other counters (gfx9 encoding:
 // vmcnt[3:0] in bits 3:0 and vmcnt[5:4] in bits 15:14, expcnt in 6:4, lgkmcnt in 11:8).
 template <int N>

@@ -295,6 +295,7 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     static_assert(!ROPE || (H16 && C::TABLE_BYTES + C::NWAVES * 32 * PADH * 2 <= C::COLS),
                   "RoPE table and f16 staging in the stages' space");
     const int ncol = GEGLU ? (p.n >> 1) : p.n;
+    const auto cbuf = buffer_rsrc(p.c, (uint32_t)min((size_t)p.m * ncol * 2, (size_t)0xFFFFFFFFu));
     const int col0 = (GEGLU ? g0 * 32 : g0 * 64);   // the wave's first output column
     char* stage_base = lds + (ROPE ? C::TABLE_BYTES : 0);
     float* sg = (float*)stage_base + w * 32 * PAD;
@@ -464,7 +465,12 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
             }
             const int row = by * BM + wm * C::WM + 32 * i + rl;
             const bool valid = row < p.m;
-            if (valid) store16<XG>((f16*)p.c + (size_t)row * ncol + col0 + cl, o);
+            if (valid) {
+                if (XG)  // one coherent 16-byte store (the host checks the output fits 4 GB)
+                    bstore16<true>(cbuf, (uint32_t)(((size_t)row * ncol + col0 + cl) * 2), o);
+                else
+                    store16<false>((f16*)p.c + (size_t)row * ncol + col0 + cl, o);
+            }
             if (EPI & EPI_STATS) {
                 float s = 0.0f, sq = 0.0f;
 #pragma unroll

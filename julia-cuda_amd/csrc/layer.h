@@ -89,9 +89,10 @@ public:
     // A plan for large batches: every GEMM on the 128 x 128 throughput tile and attention on the
     // 64-query tile, run by the kernel's large-batch instance (two blocks a CU).
     static bool is_big(const LayerPlan& plan, int m);
+    static int big_mode(const LayerPlan& plan, int m);  // the kernel instance (layer.hip)
 
 private:
-    int cus_ = 0, per_cu_ = 0, per_cu_big_ = 0, lds_max_ = 0;
+    int cus_ = 0, per_cu_ = 0, per_cu_big_ = 0, per_cu_big256_ = 0, lds_max_ = 0;
     uint32_t* bar_ = nullptr;  // BAR_WORDS words
 };
 

@@ -145,7 +145,7 @@ __device__ __forceinline__ GemmParams make_gemm(const EncParams& P, int g, const
         p.a = P.mid, p.w = L.wo_mlp, p.c = x_out_of(P, l), p.res = x_attn_of(P, l);
         p.n = P.d, p.k = P.inter, p.stats_out = P.stats_mlp;
     }
-    p.tiles_n = p.n / (P.bm[g] >= 128 ? 128 : 64);
+    p.tiles_n = p.n / (P.bm[g] >= 128 ? P.bm[g] : 64);
     p.tiles_m = (P.m + P.bm[g] - 1) / P.bm[g];
     return p;
 }
@@ -154,9 +154,15 @@ __device__ __forceinline__ int gemm_tasks(const GemmParams& g) {
     return g.tiles_n * g.tiles_m * g.splits;
 }
 
-// bm 16/32/64: the latency tile with its weights in LDS; 128: the throughput tile (128 x 128,
-// large batches), which stages both operands itself.
-template <int EPI, bool AX, bool BIG>
+// The kernel's instances: MODE_LAT takes every plan (256 threads, one block a CU); MODE_BIG128
+// and MODE_BIG256 the large-batch plans of 128 x 128 tiles (256 threads, two blocks a CU) and of
+// 256 x 256 tiles (512 threads, one block a CU), with only the throughput tiles and the streaming
+// attention tile compiled in.
+constexpr int MODE_LAT = 0, MODE_BIG128 = 1, MODE_BIG256 = 2;
+
+// bm 16/32/64: the latency tile with its weights in LDS; 128 and 256: the throughput tiles
+// (large batches), which stage both operands themselves.
+template <int EPI, bool AX, int MODE>
 __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* lds, bool pre,
                                            uint32_t* s_last, uint64_t* sub) {
     const int T = gemm_tasks(g);
@@ -164,7 +170,9 @@ __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* ld
         const bool first = t == (int)blockIdx.x;
         const bool ready = pre && first;
         uint64_t* su = first ? sub : nullptr;
-        if (BIG || bm == 128)
+        if (MODE == MODE_BIG256)
+            gemm_big_tile<256, 256, EPI, AX, true>(g, t, lds, su);
+        else if (MODE == MODE_BIG128 || bm == 128)
             gemm_big_tile<128, 128, EPI, AX, true>(g, t, lds, su);
         else if (bm == 16)
             gemm_w_tile<16, EPI, AX>(g, t, lds, ready, s_last, su);
@@ -175,11 +183,10 @@ __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* ld
     }
 }
 
-// BIG: the large-batch instance (LayerKernel::is_big plans): only the throughput tiles and the
-// 64-query attention tile are compiled in, in at most 256 registers a lane, so that two blocks
-// share a CU (the 128 x 128 tile wants eight waves a CU). The other instance takes every plan.
-template <bool BIG>
-__global__ __launch_bounds__(256, BIG ? 2 : 1) void encoder_kernel(EncParams P) {
+template <int MODE>
+__global__ __launch_bounds__(MODE == MODE_BIG256 ? 512 : 256, MODE == MODE_BIG128 ? 2 : 1)
+void encoder_kernel(EncParams P) {
+    constexpr bool BIG = MODE != MODE_LAT;
     extern __shared__ __attribute__((aligned(16))) char lds[];
     uint32_t* s_last = (uint32_t*)(lds + P.lds_main);
     uint32_t g0 = 0, nb = 0;
@@ -215,9 +222,9 @@ __global__ __launch_bounds__(256, BIG ? 2 : 1) void encoder_kernel(EncParams P) 
         if (on(0)) {
             stamp(prof, 0);
             if (gq.colsum)
-                gemm_phase<EPI_K_LNROPE, false, BIG>(gq, P.bm[0], lds, pre, s_last, sub(0));
+                gemm_phase<EPI_K_LNROPE, false, MODE>(gq, P.bm[0], lds, pre, s_last, sub(0));
             else
-                gemm_phase<EPI_K_ROPE, false, BIG>(gq, P.bm[0], lds, pre, s_last, sub(0));
+                gemm_phase<EPI_K_ROPE, false, MODE>(gq, P.bm[0], lds, pre, s_last, sub(0));
             pre = false;
             stamp_end(prof, 0);
             if (on(1)) sync(nothing);
@@ -234,6 +241,11 @@ __global__ __launch_bounds__(256, BIG ? 2 : 1) void encoder_kernel(EncParams P) 
                     uint64_t* su = prof && t == (int)blockIdx.x ? prof + 12 : nullptr;
                     attention_slice_tile<false, true>(at, t, lds, gkeys, su);
                 }
+            } else if (BIG) {  // one key range (LayerKernel::is_big)
+                constexpr int NW = MODE == MODE_BIG256 ? 8 : 4;
+                const int T = ((P.m + 16 * NW - 1) / (16 * NW)) * heads;
+                for (int t = blockIdx.x; t < T; t += gridDim.x)
+                    attention_stream_tile<true, NW>(at, t, lds);
             } else {
                 const int T = ((P.m + 63) >> 6) * heads * chunks;
                 for (int t = blockIdx.x; t < T; t += gridDim.x) {
@@ -249,7 +261,7 @@ __global__ __launch_bounds__(256, BIG ? 2 : 1) void encoder_kernel(EncParams P) 
         }
         if (on(2)) {
             stamp(prof, 4);
-            gemm_phase<EPI_K_RESSTATS, false, BIG>(go, P.bm[1], lds, pre, s_last, sub(1));
+            gemm_phase<EPI_K_RESSTATS, false, MODE>(go, P.bm[1], lds, pre, s_last, sub(1));
             pre = false;
             stamp_end(prof, 2);
             if (on(3)) {
@@ -259,7 +271,7 @@ __global__ __launch_bounds__(256, BIG ? 2 : 1) void encoder_kernel(EncParams P) 
         }
         if (on(3)) {
             stamp(prof, 6);
-            gemm_phase<EPI_K_LNGEGLU, false, BIG>(gi, P.bm[2], lds, pre, s_last, sub(2));
+            gemm_phase<EPI_K_LNGEGLU, false, MODE>(gi, P.bm[2], lds, pre, s_last, sub(2));
             pre = false;
             stamp_end(prof, 3);
             if (on(4)) {
@@ -269,7 +281,7 @@ __global__ __launch_bounds__(256, BIG ? 2 : 1) void encoder_kernel(EncParams P) 
         }
         if (on(4)) {
             stamp(prof, 8);
-            gemm_phase<EPI_K_RESSTATS, true, BIG>(gm, P.bm[3], lds, pre, s_last, sub(3));
+            gemm_phase<EPI_K_RESSTATS, true, MODE>(gm, P.bm[3], lds, pre, s_last, sub(3));
             pre = false;
             stamp_end(prof, 4);
         }
@@ -313,27 +325,31 @@ int LayerKernel::lds_bytes(const LayerPlan& plan, int d, int inter, int m, int w
     return (b + 15) / 16 * 16;
 }
 
-// The large-batch instance's LDS: the 128 x 128 tile or the 64-query attention tile.
-static int big_lds_bytes() {
-    return (std::max<int>(Big<128, 128>::LDS_BYTES, ATT_LDS_F16 * 2) + 15) / 16 * 16;
+// The large-batch instances' LDS: the throughput tile or the streaming attention tile.
+static int big_lds_bytes(int bm) {
+    const int g = bm == 256 ? Big<256, 256>::LDS_BYTES : Big<128, 128>::LDS_BYTES;
+    return (std::max<int>(g, ATT_STREAM_LDS) + 15) / 16 * 16;
 }
 
 void LayerKernel::init(int cus, int lds_max) {
     cus_ = cus > 0 ? cus : 256;
     lds_max_ = lds_max - 16;  // the split-K flag after the main area
-    per_cu_ = per_cu_big_ = 0;
-    auto occupancy = [](const void* k, int lds) {
+    per_cu_ = per_cu_big_ = per_cu_big256_ = 0;
+    auto occupancy = [](const void* k, int threads, int lds) {
         if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) {
             (void)hipGetLastError();
             return 0;
         }
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, 256, lds) != hipSuccess) n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, threads, lds) != hipSuccess) n = 0;
         return n;
     };
     // with the largest LDS a plan may use: one block per CU
-    per_cu_ = occupancy(reinterpret_cast<const void*>(encoder_kernel<false>), lds_max);
-    per_cu_big_ = occupancy(reinterpret_cast<const void*>(encoder_kernel<true>), big_lds_bytes() + 16);
+    per_cu_ = occupancy(reinterpret_cast<const void*>(encoder_kernel<MODE_LAT>), 256, lds_max);
+    per_cu_big_ = occupancy(reinterpret_cast<const void*>(encoder_kernel<MODE_BIG128>), 256,
+                            big_lds_bytes(128) + 16);
+    per_cu_big256_ = occupancy(reinterpret_cast<const void*>(encoder_kernel<MODE_BIG256>), 512,
+                               big_lds_bytes(256) + 16);
 }
 
 // Per GEMM the tile height and split-K with the least modelled time on a grid of one block per
@@ -348,9 +364,10 @@ LayerPlan LayerKernel::default_plan(int m, int d, int inter) const {
     shapes(d, inter, cols, ks);
     const double bw = 67e3;  // bytes per us into one CU
     for (int g = 0; g < 4; g++) {
-        // Large batches: the throughput tile (LayerNorm epilogues, qkv and wi, need K <= 1024).
+        // Large batches: the throughput tile (LayerNorm epilogues, qkv and wi, need K <= 1024),
+        // 256 x 256 where every GEMM's columns allow it (big_tiles below), else 128 x 128.
         const bool ln = g == 0 || g == 2;
-        if (m > ATT_SLICE_ROWS && cols[g] % 128 == 0 && ks[g] % 32 == 0 &&
+        if (m > ATT_SLICE_ROWS && cols[g] % 128 == 0 && ks[g] % 64 == 0 &&
             (!ln || ks[g] <= 128 * BIG_LN_SLOTS) && Big<128, 128>::LDS_BYTES <= lds_max_) {
             p.bm[g] = 128, p.splits[g] = 1;
             continue;
@@ -374,6 +391,11 @@ LayerPlan LayerKernel::default_plan(int m, int d, int inter) const {
     }
     p.kv[0] = attention_chunks(m, d, 0, cus_);
     p.kv[1] = 1;
+    // All four on 256 x 256 tiles (one 512-thread block a CU) when they all take them.
+    bool all256 = per_cu_big256_ > 0 && big_lds_bytes(256) <= lds_max_;
+    for (int g = 0; g < 4; g++) all256 = all256 && p.bm[g] == 128 && cols[g] % 256 == 0;
+    if (all256)
+        for (int g = 0; g < 4; g++) p.bm[g] = 256;
     return p;
 }
 
@@ -404,11 +426,12 @@ int LayerKernel::grid(const LayerArgs& a, const LayerPlan& plan) const {
     long most = (long)((a.m + 15) / 16) * (a.d / 64);  // attention slices
     most = std::max(most, (long)((a.m + 63) / 64) * (a.d / 64) * std::max(plan.kv[0], plan.kv[1]));
     for (int g = 0; g < 4; g++)
-        most = std::max(most, (long)(cols[g] / (plan.bm[g] >= 128 ? 128 : 64)) *
+        most = std::max(most, (long)(cols[g] / (plan.bm[g] >= 128 ? plan.bm[g] : 64)) *
                                   ((a.m + plan.bm[g] - 1) / plan.bm[g]) * plan.splits[g]);
     // Enough blocks for the largest phase's tasks in one round if they fit (a multiple of 8, so
     // that the task-to-XCD map is even), else every resident block.
-    const int per_cu = is_big(plan, a.m) ? per_cu_big_ : per_cu_;
+    const int mode = big_mode(plan, a.m);
+    const int per_cu = mode == MODE_BIG256 ? per_cu_big256_ : mode == MODE_BIG128 ? per_cu_big_ : per_cu_;
     const long grid = std::min<long>((long)per_cu * cus_, (most + 7) / 8 * 8);
     return (int)std::max<long>(grid, 1);
 }
@@ -422,8 +445,9 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
     if (phases == 0 || phases > 0x1f) fail("no phases selected");
     if (phases != 0x1f && a.count != 1) fail("a subset of the phases runs one layer only");
     for (int g = 0; g < 4; g++)
-        if (!(plan.bm[g] == 16 || plan.bm[g] == 32 || plan.bm[g] == 64 || plan.bm[g] == 128) ||
-            plan.splits[g] < 1 || plan.splits[g] > 4 || (plan.bm[g] == 128 && plan.splits[g] != 1))
+        if (!(plan.bm[g] == 16 || plan.bm[g] == 32 || plan.bm[g] == 64 || plan.bm[g] == 128 ||
+              plan.bm[g] == 256) ||
+            plan.splits[g] < 1 || plan.splits[g] > 4 || (plan.bm[g] >= 128 && plan.splits[g] != 1))
             fail("no such plan: " + plan.str());
     if (plan.kv[0] < 1 || plan.kv[0] > 8 || plan.kv[1] < 1 || plan.kv[1] > 8)
         fail("no such plan: " + plan.str());
@@ -432,9 +456,17 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
     if ((a.pos == nullptr) != (a.seg == nullptr)) fail("positions go with sequence bounds");
     int window = 0;
     for (int li = 0; li < a.count; li++) window = std::max(window, a.host_layers[a.first + li].window);
-    const bool big = is_big(plan, a.m);
-    if (big && per_cu_big_ <= 0) fail("the encoder kernel's large-batch instance does not fit on a CU");
-    const int lds = big ? big_lds_bytes() : lds_bytes(plan, a.d, a.inter, a.m, window);
+    const int mode = big_mode(plan, a.m);
+    bool any256 = false;
+    for (int g = 0; g < 4; g++) any256 = any256 || plan.bm[g] == 256;
+    if (any256 && mode != MODE_BIG256)
+        fail("256 x 256 tiles take every GEMM, more than " + std::to_string(ATT_SLICE_ROWS) +
+             " rows and one key range: " + plan.str());
+    if ((mode == MODE_BIG128 && per_cu_big_ <= 0) || (mode == MODE_BIG256 && per_cu_big256_ <= 0))
+        fail("the encoder kernel's large-batch instance does not fit on a CU");
+    const int lds = mode == MODE_BIG256   ? big_lds_bytes(256)
+                    : mode == MODE_BIG128 ? big_lds_bytes(128)
+                                          : lds_bytes(plan, a.d, a.inter, a.m, window);
     if (lds > lds_max_) fail("the plan's weight tiles do not fit the LDS: " + plan.str());
 
     // Every layer's GEMMs pass the per-step launcher's checks (the kernel builds the same ones).
@@ -495,18 +527,25 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
 
     const int grid_blocks = grid(a, plan);
     void* args[] = {&P};
-    const void* kernel = big ? reinterpret_cast<const void*>(encoder_kernel<true>)
-                             : reinterpret_cast<const void*>(encoder_kernel<false>);
-    const hipError_t e = hipLaunchCooperativeKernel(kernel, dim3(grid_blocks), dim3(256), args,
+    const void* kernel = mode == MODE_BIG256   ? reinterpret_cast<const void*>(encoder_kernel<MODE_BIG256>)
+                         : mode == MODE_BIG128 ? reinterpret_cast<const void*>(encoder_kernel<MODE_BIG128>)
+                                               : reinterpret_cast<const void*>(encoder_kernel<MODE_LAT>);
+    const hipError_t e = hipLaunchCooperativeKernel(kernel, dim3(grid_blocks),
+                                                    dim3(mode == MODE_BIG256 ? 512 : 256), args,
                                                     lds + 16, stream);
     if (e != hipSuccess) fail(std::string(hipGetErrorString(e)) + " (" + plan.str() + ", grid " +
                               std::to_string(grid_blocks) + ")");
 }
 
-bool LayerKernel::is_big(const LayerPlan& plan, int m) {
-    for (int g = 0; g < 4; g++)
-        if (plan.bm[g] != 128) return false;
-    return m > ATT_SLICE_ROWS && plan.kv[0] == 1 && plan.kv[1] == 1;
+bool LayerKernel::is_big(const LayerPlan& plan, int m) { return big_mode(plan, m) != MODE_LAT; }
+
+// The instance a plan runs on: the large-batch ones take plans of throughput tiles only, all of
+// one size, over more than ATT_SLICE_ROWS rows with one key range.
+int LayerKernel::big_mode(const LayerPlan& plan, int m) {
+    if (m <= ATT_SLICE_ROWS || plan.kv[0] != 1 || plan.kv[1] != 1) return MODE_LAT;
+    for (int g = 1; g < 4; g++)
+        if (plan.bm[g] != plan.bm[0]) return MODE_LAT;
+    return plan.bm[0] == 256 ? MODE_BIG256 : plan.bm[0] == 128 ? MODE_BIG128 : MODE_LAT;
 }
 
 bool LayerKernel::barrier_timed_out() {

@@ -184,6 +184,25 @@ def test_batched_encoder_matches_each_request(torch_cuda):
     e.close()
 
 
+def test_batched_encoder_on_256_tiles(torch_cuda):
+    """The persistent kernel's 256 x 256 instance (512-thread blocks, the streaming attention
+    tile on eight waves): config 4's widths, a batch past 2048 rows; the layer kernel against
+    the per-step kernels."""
+    c = dict(d=768, layers=2, inter=1152, vocab=1000, head_ff=768, max_positions=4096, seed=11,
+             batch_rows=2600)
+    e = jh.Engine(spec(c), max_length=1024)
+    plan, _ = e.profile_layer(2600, 0)
+    assert list(plan[:4]) == [256, 256, 256, 256], plan
+    rng = np.random.default_rng(23)
+    lens = [300, 1024, 17, 700, 1, 513]
+    seqs = [rng.integers(0, c["vocab"], n).astype(np.uint32) for n in lens]
+    xs, _ = e.encode_batch(seqs, layer_fused=False)
+    xf, ms = e.encode_batch(seqs, layer_fused=True)
+    say(f"256-tile layer kernel: {sum(lens)} rows, {ms:.3f} GPU ms")
+    compare(f32(xf), f32(xs), 1e-2, 5e-2, what="layer kernel vs per-step")
+    e.close()
+
+
 def test_load_errors(torch_cuda):
     with pytest.raises(jh.JuliaHipError, match="max_length"):
         jh.Engine(spec(dict(SMALL, max_positions=512)), max_length=600)
