@@ -13,11 +13,12 @@
 // With `chunks` > 1 the key blocks of each (query block, head) tile are split into ranges, one
 // block each; every range writes its unnormalised output, max and sum to the scratch and the
 // last one of the tile to arrive merges them in range order (kernels/src/attn.rs:92-204).
-// With one range and up to ATT_SLICE_ROWS rows the LDS-resident query-slice tile runs
-// (attn_tile.h: 16 queries per block, the key range staged at once and split between the waves,
-// V^T fragments from the transposing LDS read): the latency shape for one request. Longer inputs
-// (config 5's concatenated requests) take the 64-query tile, which loads each key once per 64
-// queries instead of once per 16.
+// With one range, short key ranges take the LDS-resident query-slice tile (attn_tile.h: 16
+// queries per block, the key range staged at once and split between the waves, V^T fragments
+// from the transposing LDS read): the latency shape for one request of a few hundred tokens.
+// Long ones (global attention from ~400 rows, windows past ~1500 rows, config 5's concatenated
+// requests) take the streaming tile, which loads each key once per 64 queries instead of once
+// per 16 (att_use_stream).
 #include <algorithm>
 #include <stdexcept>
 #include <string>
@@ -64,20 +65,6 @@ bool attention_prepare() {
 
 namespace {
 
-// Blocks of attention_lds_kernel<NW> one CU holds with gkeys keys staged (0 if unknown).
-int slice_blocks_per_cu(int nw, int gkeys) {
-    static int cache[2][17] = {};  // [nw == 8][gkeys / 32]
-    int& c = cache[nw == 8][gkeys / 32];
-    if (c == 0) {
-        int b = 0;
-        const hipError_t e = nw == 8
-            ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, attention_lds_kernel<8>, 512, att_lds_bytes(gkeys, 8))
-            : hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, attention_lds_kernel<4>, 256, att_lds_bytes(gkeys, 4));
-        c = (e == hipSuccess && b > 0) ? b : -1;
-    }
-    return c;
-}
-
 int device_cus() {
     int dev = 0, n = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
@@ -89,16 +76,14 @@ int device_cus() {
 }  // namespace
 
 // Waves per block of the LDS-resident kernel: eight when a slice takes more than four key steps
-// and eight-wave blocks fill the grid in as few rounds as four-wave ones.
+// and the grid is at most a block a CU (measured: with two blocks on some CUs, eight-wave blocks
+// lose to four-wave ones, e.g. a +-64 window over 448 rows, 5.2 against 4.8 us).
 int attention_slice_waves(int n, int d, int window) {
     const int gkeys = attention_gkeys(n, window);
     const int reach = window > 0 ? std::min(n, 16 + 2 * window) + 31 : n;
     if ((std::min(reach, gkeys) + 31) / 32 <= 4) return 4;
-    const int b4 = slice_blocks_per_cu(4, gkeys), b8 = slice_blocks_per_cu(8, gkeys);
-    if (b4 <= 0 || b8 <= 0) return 4;
-    const long blocks = (long)(n + 15) / 16 * (d / 64), cus = device_cus();
-    const long r4 = (blocks + b4 * cus - 1) / (b4 * cus), r8 = (blocks + b8 * cus - 1) / (b8 * cus);
-    return r8 <= r4 ? 8 : 4;
+    const long blocks = (long)(n + 15) / 16 * (d / 64);
+    return blocks <= device_cus() ? 8 : 4;
 }
 
 // Keys the LDS holds at once for an attention over n rows: all a 16-query slice reaches (from a
@@ -138,7 +123,7 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
     if (seg && chunks != 1) fail("concatenated sequences take one key range");
     if (seg && ((uintptr_t)seg % 8)) fail("seg must be 8-byte aligned");
     AttnParams p{qkv, o, n, d, window, chunks, s.ws, s.counters, seg};
-    if (chunks == 1 && n <= ATT_SLICE_ROWS) {
+    if (chunks == 1 && !att_use_stream(n, window)) {
         if (!attention_prepare()) fail("the LDS-resident kernel cannot have its LDS");
         const int gkeys = attention_gkeys(n, window);
         const dim3 grid((n + 15) / 16 * (d / 64));

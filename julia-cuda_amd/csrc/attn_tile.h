@@ -9,8 +9,18 @@ namespace jh {
 
 constexpr int ATT_PART = 18;  // f32 per thread in a key-range partial: 16 outputs, max, sum
 
-// Rows up to which one key range goes to the 16-query slice tile; above, the 64-query tile.
+// Rows up to which one key range may go to the 16-query slice tile; above, the streaming tile.
 constexpr int ATT_SLICE_ROWS = 2048;
+
+// Which tile one key range takes (measured on MI355X, one sequence, heads of 64): the slice
+// tile while a query's keys are few (global attention under ~400 rows: 293 rows 5.2 us against
+// 7.4; a +-64 window up to ~1500 rows: 1024 rows 5.4 against 6.0), the streaming tile past
+// that (global 448 rows 9.0 us against 9.3, 1024 rows 17.1 against 21.3; window 2048 rows 7.2
+// against 9.2), where the slice tile's per-slice restaging of every key costs more than it
+// saves in latency.
+__host__ __device__ constexpr bool att_use_stream(int n, int window) {
+    return n > ATT_SLICE_ROWS || (window == 0 ? n >= 400 : n > 1536);
+}
 
 // LDS f16 attention_tile needs: the K tile [64 keys][72] and the V^T tile [64 d][68].
 constexpr int ATT_LDS_F16 = 64 * 72 + 64 * 68;

@@ -235,13 +235,13 @@ void encoder_kernel(EncParams P) {
             const AttnParams at{P.qa + (size_t)l * P.q_stride, P.oa + (size_t)l * P.o_stride,
                                 P.m, P.d, L.window, chunks, P.ws, P.counters, P.seg};
             const int heads = P.d >> 6;
-            if (!BIG && chunks == 1 && P.m <= ATT_SLICE_ROWS) {  // qkv: own buffer, cached
+            if (!BIG && chunks == 1 && !att_use_stream(P.m, L.window)) {  // qkv: own buffer, cached
                 const int T = ((P.m + 15) >> 4) * heads, gkeys = P.att_gkeys[L.window > 0 ? 1 : 0];
                 for (int t = blockIdx.x; t < T; t += gridDim.x) {
                     uint64_t* su = prof && t == (int)blockIdx.x ? prof + 12 : nullptr;
                     attention_slice_tile<false, true>(at, t, lds, gkeys, su);
                 }
-            } else if (BIG) {  // one key range (LayerKernel::is_big)
+            } else if (BIG || chunks == 1) {  // (the large-batch instances have one key range)
                 constexpr int NW = MODE == MODE_BIG256 ? 8 : 4;
                 const int T = ((P.m + 16 * NW - 1) / (16 * NW)) * heads;
                 for (int t = blockIdx.x; t < T; t += gridDim.x)
@@ -319,6 +319,7 @@ int LayerKernel::lds_bytes(const LayerPlan& plan, int d, int inter, int m, int w
     shapes(d, inter, cols, ks);
     int b = std::max({ATT_LDS_F16 * 2, att_lds_bytes(attention_gkeys(m, 0)),
                       att_lds_bytes(attention_gkeys(m, window))});
+    if (att_use_stream(m, 0) || att_use_stream(m, window)) b = std::max(b, ATT_STREAM_LDS);
     for (int g = 0; g < 4; g++)
         b = plan.bm[g] >= 128 ? std::max(b, Big<128, 128>::LDS_BYTES)
                               : std::max({b, w_tile_bytes(ks[g], plan.splits[g]), red_bytes(plan.bm[g])});
