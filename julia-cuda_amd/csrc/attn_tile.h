@@ -404,10 +404,12 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
         __syncthreads();  // the group's tiles are no longer read
     }
 
-    // The waves' partials (output, max, sum over the query's keys) through LDS; wave 0 merges.
+    // The waves' partials (output, max, sum over the query's keys) through LDS; then every wave
+    // merges 16 / NW of the lane's 16 output values (over the partials in wave order).
     const float tot = sum_xor32(sum_xor16(lsum));
     float* mg = (float*)lds;  // [wave][18][64]
-    static_assert(NW >= 1 && NW <= 16, "waves");
+    static_assert(NW == 4 || NW == 8, "waves");
+    constexpr int VPW = 16 / NW;  // output values a wave merges: dt = f / 4, e = f % 4
 #pragma unroll
     for (int dt = 0; dt < 4; dt++)
 #pragma unroll
@@ -415,34 +417,37 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
     mg[(w * 18 + 16) * 64 + l] = mx;
     mg[(w * 18 + 17) * 64 + l] = tot;
     __syncthreads();
-    if (w == 0) {
+    {
         float m = -INFINITY;
 #pragma unroll
         for (int ww = 0; ww < NW; ww++) m = fmaxf(m, mg[(ww * 18 + 16) * 64 + l]);
         const float base = m == -INFINITY ? 0.0f : m;
-        float sum = 0.0f;
-        floatx4 o[4];
+        float sum = 0.0f, o[VPW];
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++) o[dt] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int v = 0; v < VPW; v++) o[v] = 0.0f;
+        const int f0 = w * VPW;  // the wave's first value
 #pragma unroll
         for (int ww = 0; ww < NW; ww++) {
             const float f = fast_exp2(mg[(ww * 18 + 16) * 64 + l] - base);
             sum += mg[(ww * 18 + 17) * 64 + l] * f;
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) o[dt][e] += mg[(ww * 18 + dt * 4 + e) * 64 + l] * f;
+            for (int v = 0; v < VPW; v++) o[v] += mg[(ww * 18 + f0 + v) * 64 + l] * f;
         }
         mark(1);
         const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
         if (qi < n) {
-            f16* op = (f16*)p.o + (size_t)qi * d + h * 64 + 4 * g;
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++) {
+            // value f0 + v is dimension 16 (f / 4) + 4 g + f % 4 of query qi
+            f16* op = (f16*)p.o + (size_t)qi * d + h * 64 + 4 * g + 16 * (f0 >> 2) + (f0 & 3);
+            if (VPW == 4) {
                 half4 ov;
 #pragma unroll
-                for (int e = 0; e < 4; e++) ov[e] = (f16)(o[dt][e] * inv);
-                store8<XS>(op + 16 * dt, ov);
+                for (int v = 0; v < 4; v++) ov[v] = (f16)(o[v] * inv);
+                store8<XS>(op, ov);
+            } else {
+                half2 ov;
+                ov[0] = (f16)(o[0] * inv);
+                ov[1] = (f16)(o[VPW > 1 ? 1 : 0] * inv);
+                store4<XS>(op, ov);
             }
         }
         if (sub) {

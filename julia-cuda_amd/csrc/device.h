@@ -10,6 +10,7 @@
 typedef _Float16 f16;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
@@ -114,6 +115,18 @@ __device__ __forceinline__ void release_wait() {
 
 __device__ __forceinline__ void xstore64(void* p, uint64_t v) {
     __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 4-byte store, device-coherent when XG.
+template <bool XG>
+__device__ __forceinline__ void store4(void* p, half2 v) {
+    if (XG) {
+        uint32_t u;
+        __builtin_memcpy(&u, &v, 4);
+        __hip_atomic_store((uint32_t*)p, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        *(half2*)p = v;
+    }
 }
 
 // 8-byte stores, device-coherent when XG (the data is read by another block in this kernel).
