@@ -236,6 +236,55 @@ def main():
                            "algorithmic_flops": dk["flops"], "us": dk["us"]}
     log("kernels at 293 tokens:", json.dumps(kern))
 
+    # ---- config 2: the per-layer GEMM set at M=512 over tile heights x split-K ----
+    # (random operands; its own scratch for the split-K partials, which the engine's chooser
+    # never picks at this size)
+    c2 = {}
+    scr = jh.Scratch(1 << 24, 1 << 16)
+    M2 = 512
+    for step in ("wo", "wi", "wo_mlp"):
+        n, k, epi, _ = STEP_SHAPES[step]
+        nout = n // 2 if epi == "lngeglu" else n
+        a = torch.randn(M2, k, device="cuda").half()
+        w = (torch.randn(n * k, device="cuda") * 0.02).half()
+        c = torch.randn(M2, nout, device="cuda").half()
+        st_in = torch.ones(M2, k // 64, 2, device="cuda")
+        cs = torch.zeros(n, device="cuda")
+        st_out = torch.zeros(M2, n // 64, 2, device="cuda")
+        kw = dict(stats_in=st_in.data_ptr(), colsum=cs.data_ptr()) if epi == "lngeglu" else \
+            dict(stats_out=st_out.data_ptr())
+        args = jh.gemm_args(epi, a.data_ptr(), w.data_ptr(), c.data_ptr(), M2, n, k, **kw)
+        grid = {}
+        for bm in (32, 64, 128):
+            for sp in (1, 2, 4):
+                try:
+                    _, md = jh.time_gemm(args, bm=bm, splits=sp, scratch=scr, warmup=5, batches=5,
+                                         per_batch=20)
+                    grid[f"{bm}/{sp}"] = round(md, 2)
+                except jh.JuliaHipError:  # a combination the kernels do not take (128: no split)
+                    grid[f"{bm}/{sp}"] = None
+        _, md = jh.time_gemm(args, scratch=scr, warmup=5, batches=5, per_batch=20)
+        c2[step] = {"epilogue": epi, "us_by_bm_split": grid,
+                    "chosen": list(jh.gemm_choose(M2, n, k, info.cus)), "chosen_us": round(md, 2),
+                    "TFLOPs": round(2 * M2 * n * k / (md * 1e-6) / 1e12, 1)}
+    scr.close()
+    out["config2_512"] = c2
+    log("config 2:", json.dumps(c2))
+
+    # ---- config 3: attention alone, global and +-64 window ----
+    c3 = {}
+    for n_att in (72, 293, 1024):
+        q = (torch.randn(n_att, 3 * D, device="cuda")).half()
+        o = torch.empty(n_att, D, dtype=torch.float16, device="cuda")
+        for window in (0, 64):
+            _, md = jh.time_attention(q.data_ptr(), o.data_ptr(), n_att, D, window, 1,
+                                      warmup=10, batches=5, per_batch=40)
+            fl = attention_flops(n_att, window)
+            c3[f"n{n_att}_{'global' if window == 0 else 'window64'}"] = {
+                "us": round(md, 2), "TFLOPs": round(fl / (md * 1e-6) / 1e12, 1)}
+    out["config3_attention"] = c3
+    log("config 3:", json.dumps(c3))
+
     # ---- the fused GEMMs at M >= 4096 (the metric's TFLOP/s and % of f16 MFMA peak) ----
     big = {}
     eng_big = jh.Engine("synthetic:layers=4,vocab=1000,max_positions=20480", max_length=18752)
