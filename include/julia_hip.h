@@ -35,12 +35,19 @@ typedef struct Engine Engine;
 const char *julia_cuda_tier(void);
 
 /* src/capi.rs:70-84 (Engine::load, src/engine.rs:124-161): opens the model in `dir` on GPU 0.
- * `dir` is a checkpoint directory in the reference; here the model is the seeded synthetic
- * Julia-1-shaped one named by a spec "synthetic[:key=value,...]" with keys d, layers, inter,
- * vocab, head_layers, head_ff, window, global_every, max_positions, seed (defaults: the
- * ModernBERT-base shapes d=768, layers=22, inter=1152, vocab=50368, head_ff=1536, seed=42).
- * `max_length` sizes the activation buffers and scratch; 0 means the model's maximum.
- * Returns NULL with the error in `err` on failure. */
+ * `dir` is a checkpoint directory, as in the reference (src/checkpoint.rs:27-62):
+ * model.safetensors (F32, F16 or BF16 tensors, memory-mapped), encoder/config.json
+ * (ModernBertConfig's fields hidden_size, num_hidden_layers, intermediate_size, vocab_size,
+ * max_position_embeddings, num_attention_heads, global_rope_theta, local_rope_theta,
+ * global_attn_every_n_layers, local_attention, norm_eps), optionally julia_config.json
+ * (head_norm_eps) and julia_hip_names.json (tensor-name overrides: the reference's names come
+ * from julia-rs, which is not vendored; the defaults follow ModernBERT for the encoder and
+ * torch's TransformerEncoderLayer for the head, see csrc/checkpoint.h). Or the seeded
+ * synthetic Julia-1-shaped model named by a spec "synthetic[:key=value,...]" with keys d,
+ * layers, inter, vocab, head_layers, head_ff, window, global_every, max_positions, seed,
+ * batch_rows (defaults: the ModernBERT-base shapes d=768, layers=22, inter=1152, vocab=50368,
+ * head_ff=1536, seed=42). `max_length` sizes the activation buffers and scratch; 0 means the
+ * model's maximum. Returns NULL with the error in `err` on failure. */
 Engine *julia_cuda_load(const char *dir, size_t max_length, char *err, size_t err_len);
 
 /* src/capi.rs:91-96: frees an engine from julia_cuda_load (NULL is fine). */
@@ -204,6 +211,11 @@ typedef struct {
     size_t weight_bytes_f16, weight_bytes_f32;
 } julia_hip_engine_info;
 int julia_hip_engine_info_get(const Engine *e, julia_hip_engine_info *out);
+/* src/checkpoint.rs:27-62 `Checkpoint::open` (without a GPU): opens and checks a checkpoint
+ * directory (model.safetensors, encoder/config.json; tensor names as documented with
+ * julia_cuda_load) and fills the model fields of *out (the engine fields stay zero). */
+int julia_hip_checkpoint_config(const char *dir, julia_hip_engine_info *out, char *err,
+                                size_t err_len);
 /* A prepared weight tensor's device address and size in bytes: name is one of tok_emb,
  * emb_norm, rope_global, rope_local, wqkv, qkv_colsum, wo, wi, wi_colsum, wo_mlp, final_norm,
  * type_emb, in_proj, in_proj_colsum, in_proj_b, out_proj, out_proj_b, linear1, linear1_colsum,

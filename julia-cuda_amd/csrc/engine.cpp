@@ -21,6 +21,7 @@
 #include "kernels.h"
 #include "layer.h"
 #include "weights.h"
+#include "checkpoint.h"
 
 using namespace jh;
 
@@ -279,7 +280,10 @@ namespace {
 
 Engine* load_engine(const char* dir, size_t max_length) {
     if (!dir) throw std::runtime_error("no model given");
-    const ModelConfig spec = parse_model_spec(dir);
+    // A checkpoint directory, or the seeded synthetic model (checked before any device work).
+    std::unique_ptr<Checkpoint> ck;
+    if (Checkpoint::is_checkpoint(dir)) ck.reset(new Checkpoint(dir));
+    const ModelConfig spec = ck ? ck->config() : parse_model_spec(dir);
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
         throw std::runtime_error("no HIP device is available");
@@ -302,7 +306,8 @@ Engine* load_engine(const char* dir, size_t max_length) {
                                  std::to_string(c.max_positions));
     e->max_length = (int)ml;
     e->rows = (int)std::max<size_t>(ml, (size_t)c.batch_rows);
-    HostWeights hw = prepare_synthetic(c);
+    HostWeights hw = ck ? prepare(c, ck->source()) : prepare_synthetic(c);
+    ck.reset();  // the mapping is no longer needed
     e->layout = hw.layout;
     e->n16 = hw.f16.size(), e->n32 = hw.f32.size();
     hip_check(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking), "hipStreamCreate");
@@ -808,6 +813,21 @@ julia_hip_gemm_config julia_hip_gemm_choose_2080ti(int m, int n, int k, int sms)
     int z = 2 * tiles > sms ? 1 : 4;
     z = std::min(z, std::max(k / 32 / 3, 1));
     return julia_hip_gemm_config{bm, z};
+}
+
+int julia_hip_checkpoint_config(const char* dir, julia_hip_engine_info* out, char* err,
+                                size_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!dir || !out) throw std::runtime_error("no directory or output");
+        const Checkpoint ck(dir);
+        const ModelConfig& c = ck.config();
+        *out = julia_hip_engine_info{};
+        out->d = c.d, out->layers = c.layers, out->inter = c.inter, out->vocab = c.vocab;
+        out->head_layers = c.head_layers, out->head_ff = c.head_ff, out->n_qtypes = c.n_qtypes;
+        out->window = c.window, out->global_every = c.global_every;
+        out->max_positions = c.max_positions;
+        out->norm_eps = c.norm_eps, out->head_eps = c.head_eps;
+    });
 }
 
 int julia_hip_engine_info_get(const Engine* e, julia_hip_engine_info* out) {

@@ -87,7 +87,6 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
     const int wm = w / C::WAVES_N, wn = w % C::WAVES_N;
     const int U = p.k >> 5, nkt = U;               // K units of 32 = stages
-    const int row0 = by * BM + wm * C::WM + l32;   // the lane's row of fragment i: row0 + 32 i
     const int g0 = (bx * BN + wn * C::WN) >> 6;    // the wave's first 64-column group
 
     // ---- epilogue inputs that go with the first stage -----------------------------------------

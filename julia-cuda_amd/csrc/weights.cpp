@@ -72,14 +72,6 @@ void tensor_dist(uint32_t id, double* mean, double* std) {
     *std = s;
 }
 
-static std::vector<float> gen(uint64_t seed, uint32_t id, size_t count) {
-    std::vector<float> v(count);
-    double m, s;
-    tensor_dist(id, &m, &s);
-    synth(seed, id, 0, count, m, s, v.data());
-    return v;
-}
-
 // ---- src/prep.rs ----
 // src/prep.rs:22-35: W' = f16(W . diag(gamma)); colsum[j] = sum_k W'[j][k] of the rounded values
 // in f64 (so mu . colsum cancels the mean part of x . W'^T as the GEMM computes it).
@@ -238,7 +230,7 @@ void run_parallel(std::vector<std::function<void()>>& tasks) {
 
 }  // namespace
 
-HostWeights prepare_synthetic(const ModelConfig& c) {
+HostWeights prepare(const ModelConfig& c, const TensorSource& src) {
     HostWeights hw;
     Layout& L = hw.layout;
     Arena a;
@@ -274,31 +266,29 @@ HostWeights prepare_synthetic(const ModelConfig& c) {
 
     uint16_t* H = hw.f16.data();
     float* Fv = hw.f32.data();
-    const uint64_t seed = c.seed;
     std::vector<std::function<void()>> tasks;
+    auto gen = [&src](uint32_t id, size_t count) {
+        std::vector<float> v(count);
+        src(id, 0, count, v.data());
+        return v;
+    };
     auto conv16 = [&](Span s, uint32_t id) {
-        tasks.push_back([=] {
-            const std::vector<float> v = gen(seed, id, s.len);
+        tasks.push_back([=, &gen] {
+            const std::vector<float> v = gen(id, s.len);
             for (size_t i = 0; i < s.len; i++) H[s.start + i] = f32_to_f16(v[i]);
         });
     };
     auto copy32 = [&](Span s, uint32_t id) {
-        tasks.push_back([=] {
-            double m, sd;
-            tensor_dist(id, &m, &sd);
-            synth(seed, id, 0, s.len, m, sd, Fv + s.start);
-        });
+        tasks.push_back([=, &src] { src(id, 0, s.len, Fv + s.start); });
     };
-    // The embedding table in row blocks: it is most of the generation work.
+    // The embedding table in row blocks: it is most of the work.
     {
         const size_t rows = c.vocab, per = 512, emb0 = L.tok_embeddings.start;
         for (size_t r0 = 0; r0 < rows; r0 += per) {
             const size_t r1 = std::min(rows, r0 + per);
-            tasks.push_back([=] {
-                double m, sd;
-                tensor_dist(T_TOK_EMB, &m, &sd);
+            tasks.push_back([=, &src] {
                 std::vector<float> v((r1 - r0) * d);
-                synth(seed, T_TOK_EMB, r0 * d, v.size(), m, sd, v.data());
+                src(T_TOK_EMB, r0 * d, v.size(), v.data());
                 for (size_t i = 0; i < v.size(); i++) H[emb0 + r0 * d + i] = f32_to_f16(v[i]);
             });
         }
@@ -318,15 +308,15 @@ HostWeights prepare_synthetic(const ModelConfig& c) {
         if (l == 0) {
             conv16(e.wqkv, b + 1);  // no attention LayerNorm in layer 0: converted only
         } else {
-            tasks.push_back([=] {
-                const std::vector<float> w = gen(seed, b + 1, 3 * d * d), g = gen(seed, b + 0, d);
+            tasks.push_back([=, &gen] {
+                const std::vector<float> w = gen(b + 1, 3 * d * d), g = gen(b + 0, d);
                 fold_layernorm(w.data(), g.data(), (int)(3 * d), (int)d, H + e.wqkv.start,
                                Fv + e.qkv_colsum.start);
             });
         }
         conv16(e.wo, b + 2);
-        tasks.push_back([=] {
-            const std::vector<float> w = gen(seed, b + 4, 2 * I * d), g = gen(seed, b + 3, d);
+        tasks.push_back([=, &gen] {
+            const std::vector<float> w = gen(b + 4, 2 * I * d), g = gen(b + 3, d);
             std::vector<uint16_t> w16(2 * I * d);
             std::vector<float> cs(2 * I);
             fold_layernorm(w.data(), g.data(), (int)(2 * I), (int)d, w16.data(), cs.data());
@@ -344,17 +334,17 @@ HostWeights prepare_synthetic(const ModelConfig& c) {
     for (int hl = 0; hl < c.head_layers; hl++) {
         const HeadLayer h = L.head[hl];
         const uint32_t b = T_HEAD + 32u * (uint32_t)hl;
-        tasks.push_back([=] {
-            const std::vector<float> w = gen(seed, b + 2, 3 * d * d), g = gen(seed, b + 0, d),
-                                     be = gen(seed, b + 1, d), bi = gen(seed, b + 3, 3 * d);
+        tasks.push_back([=, &gen] {
+            const std::vector<float> w = gen(b + 2, 3 * d * d), g = gen(b + 0, d),
+                                     be = gen(b + 1, d), bi = gen(b + 3, 3 * d);
             fold_layernorm_bias(w.data(), g.data(), be.data(), bi.data(), (int)(3 * d), (int)d,
                                 H + h.in_proj.start, Fv + h.in_proj_colsum.start, Fv + h.in_proj_b.start);
         });
         conv16(h.out_proj, b + 4);
         copy32(h.out_proj_b, b + 5);
-        tasks.push_back([=] {
-            const std::vector<float> w = gen(seed, b + 8, F * d), g = gen(seed, b + 6, d),
-                                     be = gen(seed, b + 7, d), bi = gen(seed, b + 9, F);
+        tasks.push_back([=, &gen] {
+            const std::vector<float> w = gen(b + 8, F * d), g = gen(b + 6, d),
+                                     be = gen(b + 7, d), bi = gen(b + 9, F);
             fold_layernorm_bias(w.data(), g.data(), be.data(), bi.data(), (int)F, (int)d,
                                 H + h.linear1.start, Fv + h.linear1_colsum.start, Fv + h.linear1_b.start);
         });
@@ -363,9 +353,9 @@ HostWeights prepare_synthetic(const ModelConfig& c) {
     }
     {
         const Scorer s = L.scorer;
-        tasks.push_back([=] {
-            const std::vector<float> w = gen(seed, T_SCORER + 2, d * d), g = gen(seed, T_SCORER + 0, d),
-                                     be = gen(seed, T_SCORER + 1, d), bi = gen(seed, T_SCORER + 3, d);
+        tasks.push_back([=, &gen] {
+            const std::vector<float> w = gen(T_SCORER + 2, d * d), g = gen(T_SCORER + 0, d),
+                                     be = gen(T_SCORER + 1, d), bi = gen(T_SCORER + 3, d);
             fold_layernorm_bias(w.data(), g.data(), be.data(), bi.data(), (int)d, (int)d,
                                 H + s.lin1.start, Fv + s.lin1_colsum.start, Fv + s.lin1_b.start);
         });
@@ -394,8 +384,17 @@ HostWeights prepare_synthetic(const ModelConfig& c) {
     }
     pack(L.scorer.lin1, (int)d, (int)d);
     run_parallel(tasks);
-    L.scorer.lin2_b = gen(seed, T_SCORER + 5, 1)[0];
+    L.scorer.lin2_b = gen(T_SCORER + 5, 1)[0];
     return hw;
+}
+
+HostWeights prepare_synthetic(const ModelConfig& c) {
+    const uint64_t seed = c.seed;
+    return prepare(c, [seed](uint32_t id, size_t start, size_t count, float* out) {
+        double m, sd;
+        tensor_dist(id, &m, &sd);
+        synth(seed, id, start, count, m, sd, out);
+    });
 }
 
 }  // namespace jh

@@ -8,6 +8,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -66,7 +67,15 @@ struct HostWeights {
     std::vector<float> f32;
 };
 
-// The synthetic model for `c`, prepared (src/weights.rs:143-238 for a checkpoint).
+// Where the raw (unprepared) tensors come from: values start .. start + count of tensor `id` (the
+// T_* ids below, in the checkpoint's own row-major layout) as f32 into `out`. Called from
+// several threads at once.
+using TensorSource = std::function<void(uint32_t id, size_t start, size_t count, float* out)>;
+
+// The model for `c` from `src`, prepared (src/weights.rs:143-238).
+HostWeights prepare(const ModelConfig& c, const TensorSource& src);
+
+// The seeded synthetic model for `c`, prepared.
 HostWeights prepare_synthetic(const ModelConfig& c);
 
 // ---- the pieces (also behind the C ABI's julia_hip_prep_* for tests) ----

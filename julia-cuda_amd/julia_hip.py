@@ -88,7 +88,7 @@ EXPORTS = [
     "julia_hip_gemm_choose_2080ti", "julia_hip_engine_info_get", "julia_hip_engine_tensor",
     "julia_hip_time_encoder_step", "julia_hip_profile_layer", "julia_hip_run_trace",
     "julia_hip_encode_batch",
-    "julia_hip_encode_batch_phases",
+    "julia_hip_encode_batch_phases", "julia_hip_checkpoint_config",
 ]
 
 _VP, _SZ, _I, _F, _CP = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_char_p
@@ -141,6 +141,7 @@ def lib():
                                               ctypes.POINTER(_I)]),
         "julia_hip_gemm_choose_2080ti": (GemmConfig, [_I, _I, _I, _I]),
         "julia_hip_engine_info_get": (_I, [_VP, ctypes.POINTER(EngineInfo)]),
+        "julia_hip_checkpoint_config": (_I, [_CP, ctypes.POINTER(EngineInfo), _CP, _SZ]),
         "julia_hip_engine_tensor": (_VP, [_VP, _CP, _I, ctypes.POINTER(_SZ)]),
         "julia_hip_time_encoder_step": (_I, [_VP, _I, _I, _I, _I, _I, _I, _I, ctypes.POINTER(_F),
                                              ctypes.POINTER(_F), _CP, _SZ]),
@@ -309,6 +310,13 @@ class Engine:
         out = np.empty(nb // np.dtype(dtype).itemsize, dtype)
         copy(_np_ptr(out).value, p, nb, kind=2)
         return out
+
+
+def checkpoint_config(path):
+    """The model config a checkpoint directory implies (checked, without a GPU)."""
+    i = EngineInfo()
+    _call(lib().julia_hip_checkpoint_config, path.encode(), ctypes.byref(i))
+    return i
 
 
 def copy(dst, src, nbytes, kind=4):
