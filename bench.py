@@ -114,6 +114,40 @@ def config5_batched(lens, seed=55):
     return res
 
 
+def config4_throughput(reqs, fused, spec, per_step_engine):
+    """Multi-request throughput on config 4's requests: one by one through julia_cuda_run's
+    queue, against julia_hip_run_batched's passes over concatenated rows (all requests in one
+    pass, and passes of at most 4096 rows). Requests/s and tokens/s over the host's wall clock
+    around the call (inputs from host memory, logits back), the summed pass GPU ms beside it,
+    and the largest logit difference to the one-by-one results."""
+    tokens = sum(len(r[0]) for r in reqs)
+    res = {"requests": len(reqs), "tokens": tokens, "path": "layer kernel" if fused else "per step"}
+
+    def measure(eng, batched, reps=3):
+        eng.run(reqs, layer_fused=fused, batched=batched)
+        best, out = None, None
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            lg, ms = eng.run(reqs, layer_fused=fused, batched=batched)
+            wall = time.perf_counter() - t0
+            if best is None or wall < best[0]:
+                best, out = (wall, ms), lg
+        wall, ms = best
+        gpu = float(np.sum(np.unique(ms))) if batched else float(np.sum(ms))
+        return out, {"wall_ms": round(wall * 1e3, 3), "gpu_ms": round(gpu, 3),
+                     "requests_per_s": round(len(reqs) / wall, 1),
+                     "tokens_per_s": round(tokens / wall, 0)}
+
+    ref, res["one_by_one"] = measure(per_step_engine, False)
+    for rows in (tokens, 4096):
+        eng = jh.Engine(spec, max_length=1024, batch_rows=rows)
+        lg, r = measure(eng, True)
+        eng.close()
+        r["max_logit_diff"] = float(np.max(np.abs(np.concatenate(lg) - np.concatenate(ref))))
+        res[f"batched_{rows}_rows"] = r
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -253,17 +287,17 @@ def main():
         st_out = torch.zeros(M2, n // 64, 2, device="cuda")
         kw = dict(stats_in=st_in.data_ptr(), colsum=cs.data_ptr()) if epi == "lngeglu" else \
             dict(stats_out=st_out.data_ptr())
-        args = jh.gemm_args(epi, a.data_ptr(), w.data_ptr(), c.data_ptr(), M2, n, k, **kw)
+        gargs = jh.gemm_args(epi, a.data_ptr(), w.data_ptr(), c.data_ptr(), M2, n, k, **kw)
         grid = {}
         for bm in (32, 64, 128):
             for sp in (1, 2, 4):
                 try:
-                    _, md = jh.time_gemm(args, bm=bm, splits=sp, scratch=scr, warmup=5, batches=5,
+                    _, md = jh.time_gemm(gargs, bm=bm, splits=sp, scratch=scr, warmup=5, batches=5,
                                          per_batch=20)
                     grid[f"{bm}/{sp}"] = round(md, 2)
                 except jh.JuliaHipError:  # a combination the kernels do not take (128: no split)
                     grid[f"{bm}/{sp}"] = None
-        _, md = jh.time_gemm(args, scratch=scr, warmup=5, batches=5, per_batch=20)
+        _, md = jh.time_gemm(gargs, scratch=scr, warmup=5, batches=5, per_batch=20)
         c2[step] = {"epilogue": epi, "us_by_bm_split": grid,
                     "chosen": list(jh.gemm_choose(M2, n, k, info.cus)), "chosen_us": round(md, 2),
                     "TFLOPs": round(2 * M2 * n * k / (md * 1e-6) / 1e12, 1)}
@@ -325,6 +359,8 @@ def main():
                               "mean_ms": round(float(np.mean(ms)), 4),
                               "p50_ms": round(percentile(ms, 0.5), 4),
                               "p99_ms": round(percentile(ms, 0.99), 4)}
+    out["config4_throughput"] = config4_throughput(reqs, path_fused, "synthetic", eng)
+    log("config 4 throughput:", json.dumps(out["config4_throughput"]))
     eng.close()
 
     # ---- the CPU baseline: the f32 oracle on the host cores, a bounded sample ----

@@ -67,6 +67,24 @@ int julia_cuda_run(const Engine *engine, size_t b, const uint32_t *ids, const si
                    const uint32_t *markers, const size_t *n_markers, const uint32_t *qtypes,
                    int layer_fused, float *logits, float *gpu_ms, char *err, size_t err_len);
 
+/* Multi-request throughput (the varlen batching the reference plans beyond Engine::run,
+ * src/engine.rs:170-196, which queues requests one by one). */
+/* julia_cuda_load with room for batch_rows concatenated rows (0: max_length, or the synthetic
+ * spec's batch_rows): the most rows julia_hip_run_batched puts into one pass. */
+Engine *julia_hip_load(const char *dir, size_t max_length, size_t batch_rows, char *err,
+                       size_t err_len);
+/* julia_cuda_run's arguments, checks and outputs, but consecutive requests are packed into
+ * passes of at most the engine's rows (julia_hip_load's batch_rows), each run as one forward
+ * pass over the concatenated rows: RoPE positions restart in every request, attention (the
+ * encoder's and the head's) stays within each request, every row adds its request's type
+ * embedding. gpu_ms[i] is the GPU time of the pass request i ran in (shared by the requests of
+ * a pass). Results equal julia_cuda_run's within the logit tolerance (the GEMMs' tiles, and so
+ * their summation order, depend on the rows). Returns 0, or -1 with the error in err. */
+int julia_hip_run_batched(const Engine *engine, size_t b, const uint32_t *ids, const size_t *lens,
+                          const uint32_t *markers, const size_t *n_markers,
+                          const uint32_t *qtypes, int layer_fused, float *logits, float *gpu_ms,
+                          char *err, size_t err_len);
+
 /* ================= Part 2: the per-op surface (device pointers) ======================== */
 
 /* Epilogue flags (kernels/src/main.rs:870-877) and the eight combinations (src/gemm.rs:56-124). */

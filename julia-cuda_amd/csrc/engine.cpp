@@ -40,6 +40,15 @@ T* dalloc(size_t count, const char* what) {
 
 constexpr int QUEUE = 16;  // requests queued before waiting (src/engine.rs:26)
 
+// One request of julia_cuda_run: its ids, markers (row indices < n) and question type.
+struct Request {
+    const uint32_t* ids;
+    size_t n;
+    const uint32_t* markers;
+    size_t nm;
+    uint32_t qtype;
+};
+
 }  // namespace
 
 struct Engine {
@@ -55,14 +64,18 @@ struct Engine {
     int rows = 0;  // activation rows: max_length, or more for concatenated requests (batch_rows)
     // The batched encoder's inputs: ids, each row's position in its request and its request's
     // rows (first, one past last).
+    // Batched requests also carry each row's question type.
     uint32_t* bids_d = nullptr;
-    int32_t *pos_d = nullptr, *seg_d = nullptr;
+    int32_t *pos_d = nullptr, *seg_d = nullptr, *qt_d = nullptr;
     // Activations for max_length rows.
     jh_half *x = nullptr, *qkv = nullptr, *o = nullptr, *mid = nullptr, *hx = nullptr;
     float *stats_a = nullptr, *stats_b = nullptr;
-    // Per queued request: ids, markers and logits on the device and in pinned host memory.
+    // Per queued request: ids (max_length each), on the device and in pinned host memory; the
+    // queued requests' markers and logits, mcap of each (grown on demand: a request may repeat
+    // markers, so its count has no bound).
     uint32_t *ids_d = nullptr, *markers_d = nullptr, *ids_h = nullptr, *markers_h = nullptr;
     float *logits_d = nullptr, *logits_h = nullptr;
+    size_t mcap = 0;
     hipEvent_t ev_start[QUEUE] = {}, ev_end[QUEUE] = {};
     Scratch scratch{};
     LayerKernel layer_kernel;
@@ -83,6 +96,23 @@ struct Engine {
     const jh_half* h(const Span& s) const { return s.present ? w16 + s.start : nullptr; }
     const float* f(const Span& s) const { return s.present ? w32 + s.start : nullptr; }
 
+    // Room for `need` markers and logits (waits for the stream before it reallocates).
+    void ensure_markers(size_t need) {
+        if (need <= mcap) return;
+        hip_check(hipStreamSynchronize(stream), "markers");
+        const size_t cap = std::max(need, 2 * mcap);
+        hip_check(hipFree(markers_d), "hipFree"), markers_d = nullptr;
+        hip_check(hipFree(logits_d), "hipFree"), logits_d = nullptr;
+        hip_check(hipHostFree(markers_h), "hipHostFree"), markers_h = nullptr;
+        hip_check(hipHostFree(logits_h), "hipHostFree"), logits_h = nullptr;
+        mcap = 0;
+        markers_d = dalloc<uint32_t>(cap, "markers");
+        logits_d = dalloc<float>(cap, "logits");
+        hip_check(hipHostMalloc((void**)&markers_h, cap * 4, hipHostMallocDefault), "pinned markers");
+        hip_check(hipHostMalloc((void**)&logits_h, cap * 4, hipHostMallocDefault), "pinned logits");
+        mcap = cap;
+    }
+
     ~Engine() {
         if (device >= 0) hipSetDevice(device);
         if (stream) hipStreamSynchronize(stream);
@@ -97,7 +127,7 @@ struct Engine {
                         (void*)hx, (void*)stats_a, (void*)stats_b, (void*)ids_d,
                         (void*)markers_d, (void*)logits_d, (void*)scratch.ws,
                         (void*)scratch.counters, (void*)layers_d, (void*)xa, (void*)qa,
-                        (void*)oa, (void*)bids_d, (void*)pos_d, (void*)seg_d})
+                        (void*)oa, (void*)bids_d, (void*)pos_d, (void*)seg_d, (void*)qt_d})
             if (p) hipFree(p);
         if (ids_h) hipHostFree(ids_h);
         if (markers_h) hipHostFree(markers_h);
@@ -170,16 +200,38 @@ struct Engine {
         for (size_t j = 0; j < n; j++)
             if (ids[j] >= (uint32_t)cfg.vocab)
                 throw std::runtime_error("token id " + std::to_string(ids[j]) + " is past the vocabulary");
-        std::vector<int32_t> pos(n), seg(2 * n);
-        for (size_t i = 0, r0 = 0; i < b; r0 += lens[i], i++)
-            for (size_t r = r0; r < r0 + lens[i]; r++) {
-                pos[r] = (int32_t)(r - r0);
-                seg[2 * r] = (int32_t)r0, seg[2 * r + 1] = (int32_t)(r0 + lens[i]);
+        std::vector<Request> reqs(b);
+        for (size_t i = 0, at = 0; i < b; at += lens[i], i++)
+            reqs[i] = Request{ids + at, lens[i], nullptr, 0, 0};
+        return upload_batch(reqs.data(), b).first;
+    }
+
+    // Checked requests r[0, b) as one set of concatenated rows on the device: ids (bids_d), each
+    // row's position in its request (pos_d), its request's rows [first, last) (seg_d) and
+    // question type (qt_d), and the markers as row indices (markers_d, after ensure_markers).
+    // Returns (rows, markers); the rows fit (the caller has checked).
+    std::pair<int, size_t> upload_batch(const Request* r, size_t b) {
+        size_t n = 0, nm = 0;
+        for (size_t i = 0; i < b; i++) n += r[i].n, nm += r[i].nm;
+        std::vector<uint32_t> ids(n), marks(nm);
+        std::vector<int32_t> pos(n), seg(2 * n), qt(n);
+        for (size_t i = 0, r0 = 0, m0 = 0; i < b; r0 += r[i].n, m0 += r[i].nm, i++) {
+            memcpy(ids.data() + r0, r[i].ids, r[i].n * 4);
+            for (size_t j = 0; j < r[i].nm; j++) marks[m0 + j] = (uint32_t)(r0 + r[i].markers[j]);
+            for (size_t k = r0; k < r0 + r[i].n; k++) {
+                pos[k] = (int32_t)(k - r0), qt[k] = (int32_t)r[i].qtype;
+                seg[2 * k] = (int32_t)r0, seg[2 * k + 1] = (int32_t)(r0 + r[i].n);
             }
-        hip_check(hipMemcpy(bids_d, ids, n * 4, hipMemcpyHostToDevice), "ids");
+        }
+        hip_check(hipMemcpy(bids_d, ids.data(), n * 4, hipMemcpyHostToDevice), "ids");
         hip_check(hipMemcpy(pos_d, pos.data(), n * 4, hipMemcpyHostToDevice), "positions");
         hip_check(hipMemcpy(seg_d, seg.data(), n * 8, hipMemcpyHostToDevice), "sequences");
-        return (int)n;
+        hip_check(hipMemcpy(qt_d, qt.data(), n * 4, hipMemcpyHostToDevice), "question types");
+        if (nm) {
+            ensure_markers(nm);
+            hip_check(hipMemcpy(markers_d, marks.data(), nm * 4, hipMemcpyHostToDevice), "markers");
+        }
+        return {(int)n, nm};
     }
 
     // The persistent encoder kernel: layers [first, first + count) as one cooperative launch,
@@ -211,15 +263,20 @@ struct Engine {
     // with bias from stats_a; global attention, no RoPE; out_proj + bias + residual, statistics
     // into stats_b; linear1: LN from stats_b, bias, ReLU; linear2 + bias + residual, statistics
     // into stats_a), the scorer's lin1 (LN from stats_a, bias, GELU) and the score.
+    // Concatenated requests: seg bounds each row's attention to its request, row_type gives its
+    // question type (qtype is then unused) and the markers are row indices into the whole set.
     void launch_head(const jh_half* x, int n, int qtype, const uint32_t* markers, int nm,
-                     float* logits) {
+                     float* logits, const int32_t* seg = nullptr,
+                     const int32_t* row_type = nullptr) {
         const int d = cfg.d, F = cfg.head_ff;
-        norm_add_launch(x, n, d, f(layout.final_norm), f(layout.type_emb) + (size_t)qtype * d,
-                        cfg.norm_eps, hx, stats_a, stream);
+        const float* add = f(layout.type_emb) + (row_type ? 0 : (size_t)qtype * d);
+        norm_add_launch(x, n, d, f(layout.final_norm), add, cfg.norm_eps, hx, stats_a, stream,
+                        row_type);
         for (const HeadLayer& H : layout.head) {
             gemm(EPI_K_LNBIAS, hx, h(H.in_proj), qkv, n, 3 * d, d, stats_a, f(H.in_proj_colsum),
                  cfg.head_eps, f(H.in_proj_b), nullptr, nullptr);
-            attention_launch(qkv, o, n, d, 0, attention_chunks(n, d, 0, cus), scratch, stream);
+            attention_launch(qkv, o, n, d, 0, attention_chunks(n, d, 0, cus), scratch, stream,
+                             seg);
             gemm(EPI_K_BIASRESSTATS, o, h(H.out_proj), hx, n, d, d, nullptr, nullptr, 0.0f,
                  f(H.out_proj_b), nullptr, stats_b);
             gemm(EPI_K_LNBIASRELU, hx, h(H.linear1), mid, n, F, d, stats_b, f(H.linear1_colsum),
@@ -278,7 +335,7 @@ struct Engine {
 
 namespace {
 
-Engine* load_engine(const char* dir, size_t max_length) {
+Engine* load_engine(const char* dir, size_t max_length, size_t batch_rows = 0) {
     if (!dir) throw std::runtime_error("no model given");
     // A checkpoint directory, or the seeded synthetic model (checked before any device work).
     std::unique_ptr<Checkpoint> ck;
@@ -304,8 +361,9 @@ Engine* load_engine(const char* dir, size_t max_length) {
     if (ml > (size_t)c.max_positions)
         throw std::runtime_error("max_length " + std::to_string(ml) + " is over the model's " +
                                  std::to_string(c.max_positions));
+    if (batch_rows > (1u << 20)) throw std::runtime_error("batch_rows out of range");
     e->max_length = (int)ml;
-    e->rows = (int)std::max<size_t>(ml, (size_t)c.batch_rows);
+    e->rows = (int)std::max({ml, (size_t)c.batch_rows, batch_rows});
     HostWeights hw = ck ? prepare(c, ck->source()) : prepare_synthetic(c);
     ck.reset();  // the mapping is no longer needed
     e->layout = hw.layout;
@@ -332,10 +390,12 @@ Engine* load_engine(const char* dir, size_t max_length) {
     e->bids_d = dalloc<uint32_t>(n, "batch ids");
     e->pos_d = dalloc<int32_t>(n, "batch positions");
     e->seg_d = dalloc<int32_t>(2 * n, "batch sequences");
+    e->qt_d = dalloc<int32_t>(n, "batch question types");
     if (const char* g = getenv("JULIA_HIP_GRAPHS")) e->use_graphs = strcmp(g, "0") != 0;
     hip_check(hipHostMalloc((void**)&e->ids_h, QUEUE * ml * 4, hipHostMallocDefault), "pinned ids");
     hip_check(hipHostMalloc((void**)&e->markers_h, QUEUE * ml * 4, hipHostMallocDefault), "pinned markers");
     hip_check(hipHostMalloc((void**)&e->logits_h, QUEUE * ml * 4, hipHostMallocDefault), "pinned logits");
+    e->mcap = QUEUE * ml;
     for (int i = 0; i < QUEUE; i++) {
         hip_check(hipEventCreate(&e->ev_start[i]), "hipEventCreate");
         hip_check(hipEventCreate(&e->ev_end[i]), "hipEventCreate");
@@ -385,14 +445,6 @@ Engine* load_engine(const char* dir, size_t max_length) {
     return e.release();
 }
 
-struct Request {
-    const uint32_t* ids;
-    size_t n;
-    const uint32_t* markers;
-    size_t nm;
-    uint32_t qtype;
-};
-
 void check_request(const Engine& e, const Request& r, size_t i) {
     if (r.qtype > 2 || (int)r.qtype >= e.cfg.n_qtypes)
         throw std::runtime_error("sequence " + std::to_string(i) + ": no question type " +
@@ -416,22 +468,25 @@ void run_requests(Engine& e, const std::vector<Request>& reqs, bool fused, float
     size_t out_at = 0;
     for (size_t c0 = 0; c0 < reqs.size(); c0 += QUEUE) {
         const size_t c1 = std::min(reqs.size(), c0 + QUEUE);
-        for (size_t i = c0; i < c1; i++) check_request(e, reqs[i], i);
-        for (size_t i = c0; i < c1; i++) {
+        size_t chunk_markers = 0;
+        for (size_t i = c0; i < c1; i++) check_request(e, reqs[i], i), chunk_markers += reqs[i].nm;
+        e.ensure_markers(chunk_markers);  // the stream is idle here
+        for (size_t i = c0, m0 = 0; i < c1; m0 += reqs[i].nm, i++) {
             const Request& r = reqs[i];
             const size_t q = i - c0, slot = q * e.max_length;
             memcpy(e.ids_h + slot, r.ids, r.n * 4);
-            if (r.nm) memcpy(e.markers_h + slot, r.markers, r.nm * 4);
-            const bool graph = e.use_graphs && !fused;
-            // The graph reads its request from gin; otherwise the request has its own slot.
+            if (r.nm) memcpy(e.markers_h + m0, r.markers, r.nm * 4);
+            // The graph reads its request from gin (ids, then up to max_length markers) and
+            // writes glogits; otherwise the request has its own ids slot and marker range.
+            const bool graph = e.use_graphs && !fused && r.nm <= (size_t)e.max_length;
             uint32_t* ids_dst = graph ? e.gin : e.ids_d + slot;
-            uint32_t* markers_dst = graph ? e.gin + e.max_length : e.markers_d + slot;
-            float* logits_src = graph ? e.glogits : e.logits_d + slot;
+            uint32_t* markers_dst = graph ? e.gin + e.max_length : e.markers_d + m0;
+            float* logits_src = graph ? e.glogits : e.logits_d + m0;
             hipGraphExec_t ex = graph ? e.graph_for((int)r.n, (int)r.nm, (int)r.qtype) : nullptr;
             hip_check(hipMemcpyAsync(ids_dst, e.ids_h + slot, r.n * 4, hipMemcpyHostToDevice,
                                      e.stream), "ids");
             if (r.nm)
-                hip_check(hipMemcpyAsync(markers_dst, e.markers_h + slot, r.nm * 4,
+                hip_check(hipMemcpyAsync(markers_dst, e.markers_h + m0, r.nm * 4,
                                          hipMemcpyHostToDevice, e.stream), "markers");
             hip_check(hipEventRecord(e.ev_start[q], e.stream), "hipEventRecord");
             if (graph)
@@ -440,25 +495,88 @@ void run_requests(Engine& e, const std::vector<Request>& reqs, bool fused, float
                 e.launch(ids_dst, (int)r.n, (int)r.qtype, markers_dst, (int)r.nm, logits_src, fused);
             hip_check(hipEventRecord(e.ev_end[q], e.stream), "hipEventRecord");
             if (r.nm)
-                hip_check(hipMemcpyAsync(e.logits_h + slot, logits_src, r.nm * 4,
+                hip_check(hipMemcpyAsync(e.logits_h + m0, logits_src, r.nm * 4,
                                          hipMemcpyDeviceToHost, e.stream), "logits");
         }
         hip_check(hipStreamSynchronize(e.stream), "the forward pass");
         if (fused && e.layer_kernel.barrier_timed_out())
             throw std::runtime_error("layer: a grid barrier timed out (blocks not co-resident)");
-        for (size_t i = c0; i < c1; i++) {
+        for (size_t i = c0, m0 = 0; i < c1; m0 += reqs[i].nm, i++) {
             const Request& r = reqs[i];
-            const size_t q = i - c0, slot = q * e.max_length;
+            const size_t q = i - c0;
             float ms = 0.0f;
             hip_check(hipEventElapsedTime(&ms, e.ev_start[q], e.ev_end[q]), "hipEventElapsedTime");
             for (size_t j = 0; j < r.nm; j++)
-                if (!std::isfinite(e.logits_h[slot + j]))
+                if (!std::isfinite(e.logits_h[m0 + j]))
                     throw std::runtime_error("inference returned nonfinite logits");
-            if (r.nm) memcpy(logits_out + out_at, e.logits_h + slot, r.nm * 4);
+            if (r.nm) memcpy(logits_out + out_at, e.logits_h + m0, r.nm * 4);
             out_at += r.nm;
             if (gpu_ms) gpu_ms[i] = ms;
         }
     }
+}
+
+// Multi-request throughput: the requests and outputs of run_requests, but consecutive requests
+// are packed into sets of at most e.rows rows and each set runs as one forward pass over its
+// concatenated rows: RoPE at each row's position in its request, attention (encoder and head)
+// bounded to the row's request, norm_add with the row's question type, markers as row indices.
+// Each request's gpu_ms is the time of the pass it ran in.
+void run_batched(Engine& e, const std::vector<Request>& reqs, bool fused, float* logits_out,
+                 float* gpu_ms) {
+    hip_check(hipSetDevice(e.device), "hipSetDevice");
+    for (size_t i = 0; i < reqs.size(); i++) check_request(e, reqs[i], i);
+    size_t out_at = 0;
+    for (size_t b0 = 0; b0 < reqs.size();) {
+        size_t b1 = b0, rows = 0;  // every request fits alone: n <= max_length <= e.rows
+        while (b1 < reqs.size() && rows + reqs[b1].n <= (size_t)e.rows) rows += reqs[b1++].n;
+        const std::pair<int, size_t> nr = e.upload_batch(reqs.data() + b0, b1 - b0);
+        const int n = nr.first;
+        const size_t nm = nr.second;
+        hip_check(hipEventRecord(e.ev_start[0], e.stream), "hipEventRecord");
+        embed_launch(e.bids_d, n, e.h(e.layout.tok_embeddings), e.cfg.vocab, e.cfg.d,
+                     e.f(e.layout.emb_norm), e.cfg.norm_eps, e.x, e.stream);
+        const jh_half* xf = e.x;
+        if (fused)
+            xf = e.launch_encoder_fused(0, e.cfg.layers, n, e.x, e.pos_d, e.seg_d);
+        else
+            for (int l = 0; l < e.cfg.layers; l++) e.launch_layer(l, n, e.pos_d, e.seg_d);
+        e.launch_head(xf, n, 0, e.markers_d, (int)nm, e.logits_d, e.seg_d, e.qt_d);
+        hip_check(hipEventRecord(e.ev_end[0], e.stream), "hipEventRecord");
+        if (nm)
+            hip_check(hipMemcpyAsync(e.logits_h, e.logits_d, nm * 4, hipMemcpyDeviceToHost,
+                                     e.stream), "logits");
+        hip_check(hipStreamSynchronize(e.stream), "the forward pass");
+        if (fused && e.layer_kernel.barrier_timed_out())
+            throw std::runtime_error("layer: a grid barrier timed out (blocks not co-resident)");
+        float ms = 0.0f;
+        hip_check(hipEventElapsedTime(&ms, e.ev_start[0], e.ev_end[0]), "hipEventElapsedTime");
+        for (size_t j = 0; j < nm; j++)
+            if (!std::isfinite(e.logits_h[j]))
+                throw std::runtime_error("inference returned nonfinite logits");
+        if (nm) memcpy(logits_out + out_at, e.logits_h, nm * 4);
+        out_at += nm;
+        for (size_t i = b0; i < b1; i++)
+            if (gpu_ms) gpu_ms[i] = ms;
+        b0 = b1;
+    }
+}
+
+// julia_cuda_run's arguments as requests (src/capi.rs:134-177); checks the pointers.
+std::vector<Request> gather_requests(size_t b, const uint32_t* ids, const size_t* lens,
+                                     const uint32_t* markers, const size_t* n_markers,
+                                     const uint32_t* qtypes, const float* logits) {
+    if (!ids || !lens || !n_markers || !qtypes) throw std::runtime_error("null argument");
+    std::vector<Request> reqs(b);
+    size_t at_id = 0, at_m = 0;
+    for (size_t i = 0; i < b; i++) {
+        reqs[i] = Request{ids + at_id, lens[i], markers ? markers + at_m : nullptr, n_markers[i],
+                          qtypes[i]};
+        if (n_markers[i] && !markers) throw std::runtime_error("null markers");
+        at_id += lens[i];
+        at_m += n_markers[i];
+    }
+    if (at_m && !logits) throw std::runtime_error("null logits");
+    return reqs;
 }
 
 void report(char* err, size_t len, const std::string& msg) {
@@ -537,18 +655,29 @@ int julia_cuda_run(const Engine* engine, size_t b, const uint32_t* ids, const si
     return guarded(err, err_len, [&] {
         if (!engine) throw std::runtime_error("no engine");
         if (b == 0) return;
-        if (!ids || !lens || !n_markers || !qtypes) throw std::runtime_error("null argument");
-        std::vector<Request> reqs(b);
-        size_t at_id = 0, at_m = 0;
-        for (size_t i = 0; i < b; i++) {
-            reqs[i] = Request{ids + at_id, lens[i], markers ? markers + at_m : nullptr, n_markers[i],
-                              qtypes[i]};
-            if (n_markers[i] && !markers) throw std::runtime_error("null markers");
-            at_id += lens[i];
-            at_m += n_markers[i];
-        }
-        if (at_m && !logits) throw std::runtime_error("null logits");
+        const std::vector<Request> reqs =
+            gather_requests(b, ids, lens, markers, n_markers, qtypes, logits);
         run_requests(*const_cast<Engine*>(engine), reqs, layer_fused != 0, logits, gpu_ms);
+    });
+}
+
+Engine* julia_hip_load(const char* dir, size_t max_length, size_t batch_rows, char* err,
+                       size_t err_len) {
+    Engine* e = nullptr;
+    guarded(err, err_len, [&] { e = load_engine(dir, max_length, batch_rows); });
+    return e;
+}
+
+int julia_hip_run_batched(const Engine* engine, size_t b, const uint32_t* ids, const size_t* lens,
+                          const uint32_t* markers, const size_t* n_markers,
+                          const uint32_t* qtypes, int layer_fused, float* logits, float* gpu_ms,
+                          char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        if (!engine) throw std::runtime_error("no engine");
+        if (b == 0) return;
+        const std::vector<Request> reqs =
+            gather_requests(b, ids, lens, markers, n_markers, qtypes, logits);
+        run_batched(*const_cast<Engine*>(engine), reqs, layer_fused != 0, logits, gpu_ms);
     });
 }
 

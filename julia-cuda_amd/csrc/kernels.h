@@ -126,8 +126,11 @@ int attention_slice_waves(int n, int d, int window);  // 4 or 8 (needs the devic
 
 void embed_launch(const uint32_t* ids, int n, const jh_half* table, int vocab, int d,
                   const float* gamma, float eps, jh_half* x, hipStream_t stream);
+// row_type (nullable): each row's question type; the row adds add + row_type[row] * d (the
+// caller has checked the types against the table), else add.
 void norm_add_launch(const jh_half* x, int n, int d, const float* gamma, const float* add,
-                     float eps, jh_half* out, float* stats, hipStream_t stream);
+                     float eps, jh_half* out, float* stats, hipStream_t stream,
+                     const int32_t* row_type = nullptr);
 void score_launch(const jh_half* y, int n, int d, const jh_half* w, float b,
                   const uint32_t* markers, int k, float* logits, hipStream_t stream);
 void stream_copy_launch(void* dst, const void* src, size_t bytes, hipStream_t stream);

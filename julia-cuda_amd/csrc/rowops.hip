@@ -77,9 +77,11 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* ids, int n, 
 template <int NC>
 __global__ __launch_bounds__(256) void norm_add_kernel(const f16* x, int n, int d,
                                                        const float* gamma, const float* add,
-                                                       float eps, f16* out, float* stats) {
+                                                       const int32_t* row_type, float eps,
+                                                       f16* out, float* stats) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (row >= n) return;
+    if (row_type) add += (size_t)row_type[row] * d;
     float v[NC][4];
     load_row<NC>(x + (size_t)row * d, d, lane, v);
     const float2 st = ln_two_pass<NC>(v, d, lane, eps);
@@ -185,13 +187,14 @@ void embed_launch(const uint32_t* ids, int n, const jh_half* table, int vocab, i
 }
 
 void norm_add_launch(const jh_half* x, int n, int d, const float* gamma, const float* add,
-                     float eps, jh_half* out, float* stats, hipStream_t st) {
+                     float eps, jh_half* out, float* stats, hipStream_t st,
+                     const int32_t* row_type) {
     check_row("norm_add", n, d, x, out);
     if (!gamma || !add || !stats || ((uintptr_t)gamma % 16) || ((uintptr_t)add % 16) ||
         ((uintptr_t)stats % 8) || x == out)
         throw std::runtime_error("norm_add: bad gamma, add or stats, or out aliases x");
-    JH_ROW_DISPATCH(norm_add_kernel, dim3((n + 3) / 4), st, (const f16*)x, n, d, gamma, add, eps,
-                    (f16*)out, stats);
+    JH_ROW_DISPATCH(norm_add_kernel, dim3((n + 3) / 4), st, (const f16*)x, n, d, gamma, add,
+                    row_type, eps, (f16*)out, stats);
     check_launch("norm_add");
 }
 

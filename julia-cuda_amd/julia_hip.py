@@ -77,6 +77,7 @@ class EngineInfo(ctypes.Structure):
 # Every symbol include/julia_hip.h declares.
 EXPORTS = [
     "julia_cuda_tier", "julia_cuda_load", "julia_cuda_free", "julia_cuda_device", "julia_cuda_run",
+    "julia_hip_load", "julia_hip_run_batched",
     "julia_hip_scratch_new", "julia_hip_scratch_free", "julia_hip_gemm", "julia_hip_attention",
     "julia_hip_attention_seg",
     "julia_hip_embed", "julia_hip_norm_add", "julia_hip_score", "julia_hip_time_gemm",
@@ -110,6 +111,8 @@ def lib():
         "julia_cuda_free": (None, [_VP]),
         "julia_cuda_device": (None, [_VP, _CP, _SZ]),
         "julia_cuda_run": (_I, [_VP, _SZ, _VP, _VP, _VP, _VP, _VP, _I, _VP, _VP, _CP, _SZ]),
+        "julia_hip_load": (_VP, [_CP, _SZ, _SZ, _CP, _SZ]),
+        "julia_hip_run_batched": (_I, [_VP, _SZ, _VP, _VP, _VP, _VP, _VP, _I, _VP, _VP, _CP, _SZ]),
         "julia_hip_scratch_new": (_VP, [_SZ, _SZ, _CP, _SZ]),
         "julia_hip_scratch_free": (None, [_VP]),
         "julia_hip_gemm": (_I, [ctypes.POINTER(GemmArgs), GemmConfig, _VP, _VP, _CP, _SZ]),
@@ -188,9 +191,13 @@ def device_count():
 class Engine:
     """julia_cuda_load / julia_cuda_run / julia_cuda_free (src/capi.rs)."""
 
-    def __init__(self, spec="synthetic", max_length=0):
+    def __init__(self, spec="synthetic", max_length=0, batch_rows=0):
+        """batch_rows: room for that many concatenated rows (julia_hip_load), for run_batched."""
         e = _err()
-        self.ptr = lib().julia_cuda_load(spec.encode(), max_length, e, ERR_LEN)
+        if batch_rows:
+            self.ptr = lib().julia_hip_load(spec.encode(), max_length, batch_rows, e, ERR_LEN)
+        else:
+            self.ptr = lib().julia_cuda_load(spec.encode(), max_length, e, ERR_LEN)
         if not self.ptr:
             raise JuliaHipError(e.value.decode(errors="replace"))
 
@@ -218,8 +225,10 @@ class Engine:
             raise JuliaHipError("no engine")
         return i
 
-    def run(self, requests, layer_fused=False):
-        """requests: [(ids, markers, qtype)]. Returns ([logits per request], [gpu ms])."""
+    def run(self, requests, layer_fused=False, batched=False):
+        """requests: [(ids, markers, qtype)]. Returns ([logits per request], [gpu ms]).
+        batched: julia_hip_run_batched (requests packed into passes over concatenated rows; a
+        request's gpu ms is its pass's)."""
         ids = np.ascontiguousarray(np.concatenate([np.asarray(r[0], np.uint32) for r in requests])
                                    if requests else np.zeros(0), np.uint32)
         lens = np.array([len(r[0]) for r in requests], np.uintp)
@@ -229,7 +238,8 @@ class Engine:
         qt = np.array([r[2] for r in requests], np.uint32)
         logits = np.zeros(max(len(markers), 1), np.float32)
         ms = np.zeros(max(len(requests), 1), np.float32)
-        _call(lib().julia_cuda_run, self.ptr, len(requests), _np_ptr(ids), _np_ptr(lens),
+        fn = lib().julia_hip_run_batched if batched else lib().julia_cuda_run
+        _call(fn, self.ptr, len(requests), _np_ptr(ids), _np_ptr(lens),
               _np_ptr(markers), _np_ptr(nm), _np_ptr(qt), int(bool(layer_fused)),
               _np_ptr(logits), _np_ptr(ms))
         out, at = [], 0

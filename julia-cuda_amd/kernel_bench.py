@@ -4,10 +4,13 @@ plain device-to-device copy of a known size to calibrate byte counters against.
 
     python julia-cuda_amd/kernel_bench.py --step wi --tokens 293 --iters 200 --copy-mb 64
     python julia-cuda_amd/kernel_bench.py --batch 64 --iters 3 --copy-mb 0
+    python julia-cuda_amd/kernel_bench.py --requests 64 --iters 3
 
 Prints the step's median time per call (HIP events) and the copy's bytes. With --batch N: config
 5's batched encoder instead (N requests of config 4's seeded lengths concatenated, per-step
-kernels then the persistent kernel, --iters times each).
+kernels then the persistent kernel, --iters times each). With --requests N: N such requests
+(6 markers each, question types in turn) through julia_hip_run_batched as one pass, the whole
+forward pass (embed, encoder, head, scorer), --iters times.
 """
 
 import argparse
@@ -28,7 +31,23 @@ def main():
     ap.add_argument("--copy-mb", type=int, default=64)
     ap.add_argument("--spec", default="synthetic")
     ap.add_argument("--batch", type=int, default=0)
+    ap.add_argument("--requests", type=int, default=0)
     args = ap.parse_args()
+    if args.requests:
+        import numpy as np
+        rng = np.random.default_rng(4)
+        lens = np.clip(np.round(rng.lognormal(np.log(260.0), 0.5, args.requests)), 72, 1024).astype(int)
+        reqs = []
+        for i, n in enumerate(lens):
+            ids = rng.integers(0, 50368, int(n)).astype(np.uint32)
+            reqs.append((ids, np.sort(rng.choice(int(n), 6, replace=False)).astype(np.uint32), i % 3))
+        e = jh.Engine("synthetic", max_length=1024, batch_rows=int(lens.sum()))
+        for _ in range(args.iters):
+            _, ms = e.run(reqs, batched=True)
+            print(f"{args.requests} requests ({int(lens.sum())} rows) in one pass: {ms[0]:.3f} ms",
+                  flush=True)
+        e.close()
+        return
     if args.batch:
         import numpy as np
         rng = np.random.default_rng(4)
