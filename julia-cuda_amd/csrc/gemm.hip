@@ -50,10 +50,16 @@ __global__ __launch_bounds__(512, 1) void gemm_lat1(GemmParams p) {
 // ---------------------------------------------------------------------------------------------
 // gemm_big: BM x BM tiles (BM = 128 or 256) for large M; see gemm_big.h. Dynamic LDS:
 // Big<BM, BM>::LDS_BYTES.
+// Persistent: the grid is the resident blocks (one 256 x 256 or two 128 x 128 a CU), and block
+// b takes tasks b, b + grid, ...: a CU goes from one tile's epilogue to the next tile's copies
+// without a block dispatch in between. (The grid is a multiple of 8, so a block's tasks stay on
+// its XCD's range of xcd_task.)
 template <int BM, int EPI>
 __global__ __launch_bounds__((Big<BM, BM>::THREADS)) void gemm_big(GemmParams p) {
     extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
-    gemm_big_tile<BM, BM, EPI, false, false>(p, blockIdx.x, lds_dyn);
+    const int T = p.tiles_n * p.tiles_m;
+    for (int task = blockIdx.x; task < T; task += gridDim.x)
+        gemm_big_tile<BM, BM, EPI, false, false>(p, task, lds_dyn);  // ends with a block barrier
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -153,7 +159,8 @@ static void launch_one(const GemmParams& p, hipStream_t st) {
             hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_big<B, EPI>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, Big<B, B>::LDS_BYTES) == hipSuccess;
         if (!lds_ok) throw std::runtime_error("gemm: the throughput kernel cannot have its LDS");
-        hipLaunchKernelGGL((gemm_big<B, EPI>), dim3(blocks), dim3(Big<B, B>::THREADS), (Big<B, B>::LDS_BYTES), st, p);
+        const int grid = std::min(blocks, (B == 256 ? 1 : 2) * device_cus());
+        hipLaunchKernelGGL((gemm_big<B, EPI>), dim3(grid), dim3(Big<B, B>::THREADS), (Big<B, B>::LDS_BYTES), st, p);
     } else if (p.splits == 1 && blocks <= device_cus()) {
         constexpr int B = BM < 128 ? BM : 64;
         constexpr int LDS = lat_lds_floats<B, 8>() * 4;
