@@ -60,12 +60,20 @@ void julia_cuda_device(const Engine *engine, char *buf, size_t len);
  * Sequence i is lens[i] token ids (all concatenated in ids) with n_markers[i] marker positions
  * (concatenated in markers) and question type qtypes[i] (0 choice, 1 score, 2 noul). Writes each
  * sequence's logits, one per marker, concatenated into logits, and its GPU time in ms (embed to
- * logits) into gpu_ms[i]. layer_fused: the persistent layer kernel instead of the per-step
- * kernels. Requests are queued 16 at a time and waited for once per 16. Not thread-safe per
+ * logits) into gpu_ms[i]. layer_fused: the persistent kernels instead of the per-step ones (the
+ * whole model in one launch where julia_hip_model_kernel says so). Requests are queued 16 at a
+ * time and waited for once per 16. Not thread-safe per
  * engine (the reference's contract). Returns 0, or -1 with the error in err. */
 int julia_cuda_run(const Engine *engine, size_t b, const uint32_t *ids, const size_t *lens,
                    const uint32_t *markers, const size_t *n_markers, const uint32_t *qtypes,
                    int layer_fused, float *logits, float *gpu_ms, char *err, size_t err_len);
+
+/* layer_fused = 1 runs the whole forward pass (embed, every layer, the head, the score) as one
+ * cooperative launch, the reference's stated next step (README.md:12-13), when the plan's kernel
+ * instance takes the head's GEMMs; otherwise the encoder kernel and the head's own launches.
+ * Returns 1 if the one-launch path takes `rows` rows (a request's tokens, or a batched pass's),
+ * else 0. */
+int julia_hip_model_kernel(const Engine *engine, size_t rows);
 
 /* Multi-request throughput (the varlen batching the reference plans beyond Engine::run,
  * src/engine.rs:170-196, which queues requests one by one). */

@@ -85,6 +85,11 @@ struct Engine {
     // Its write-once activation buffers (LayerArgs): x after each residual step, each layer's
     // qkv and o, max_length rows each.
     jh_half *xa = nullptr, *qa = nullptr, *oa = nullptr;
+    // The whole-model launch's own buffers (ModelArgs): the head's residual stream, its layers'
+    // qkv and attention outputs, the scorer's hidden rows; and the head-layer table.
+    jh_half *hxa = nullptr, *hqa = nullptr, *hoa = nullptr, *hs = nullptr;
+    HeadDesc* heads_d = nullptr;
+    std::vector<HeadDesc> heads_h;
     // The per-step forward pass as HIP graphs, one per (tokens, markers, question type): 124
     // launches submitted as one. They read the request from fixed buffers (gin: ids, then
     // markers at max_length) and write glogits; stream order keeps queued requests apart.
@@ -127,7 +132,8 @@ struct Engine {
                         (void*)hx, (void*)stats_a, (void*)stats_b, (void*)ids_d,
                         (void*)markers_d, (void*)logits_d, (void*)scratch.ws,
                         (void*)scratch.counters, (void*)layers_d, (void*)xa, (void*)qa,
-                        (void*)oa, (void*)bids_d, (void*)pos_d, (void*)seg_d, (void*)qt_d})
+                        (void*)oa, (void*)bids_d, (void*)pos_d, (void*)seg_d, (void*)qt_d,
+                        (void*)hxa, (void*)hqa, (void*)hoa, (void*)hs, (void*)heads_d})
             if (p) hipFree(p);
         if (ids_h) hipHostFree(ids_h);
         if (markers_h) hipHostFree(markers_h);
@@ -258,6 +264,32 @@ struct Engine {
         return LayerKernel::x_out(a);
     }
 
+    // The whole forward pass as one cooperative launch (embed, every layer, the head, the score)
+    // when the plan's kernel instance takes the head's GEMMs; false if not (the caller then runs
+    // the encoder kernel and the head's own launches). ids, markers: device, row indices.
+    bool launch_model(const uint32_t* ids, int n, int qtype, const uint32_t* markers, int nm,
+                      float* logits, const int32_t* pos = nullptr, const int32_t* seg = nullptr,
+                      const int32_t* row_type = nullptr) {
+        const LayerPlan plan = layer_kernel.default_plan(n, cfg.d, cfg.inter);
+        if (!layer_kernel.model_fits(plan, n, cfg.d, cfg.head_ff)) return false;
+        const Scorer& S = layout.scorer;
+        ModelArgs M{};
+        M.ids = ids, M.tok_emb = h(layout.tok_embeddings), M.emb_norm = f(layout.emb_norm);
+        M.vocab = cfg.vocab;
+        M.heads = heads_d, M.host_heads = heads_h.data(), M.head_layers = (int)heads_h.size();
+        M.head_ff = cfg.head_ff, M.head_eps = cfg.head_eps, M.final_norm = f(layout.final_norm);
+        M.type_add = f(layout.type_emb) + (row_type ? 0 : (size_t)qtype * cfg.d);
+        M.row_type = row_type;
+        M.hxa = hxa, M.hqa = hqa, M.hoa = hoa, M.hs = hs;
+        M.lin1 = h(S.lin1), M.lin1_colsum = f(S.lin1_colsum), M.lin1_b = f(S.lin1_b);
+        M.lin2 = h(S.lin2), M.lin2_b = S.lin2_b;
+        M.markers = markers, M.n_markers = nm, M.logits = logits;
+        LayerArgs a = layer_args(0, cfg.layers, n, x, pos, seg);
+        a.model = &M;
+        layer_kernel.launch(a, plan, scratch, stream);
+        return true;
+    }
+
     // ---- the head (src/forward.rs GpuHead) -------------------------------------------------
     // The final norm + type embedding (statistics into stats_a), the head layers (in_proj: LN
     // with bias from stats_a; global attention, no RoPE; out_proj + bias + residual, statistics
@@ -322,6 +354,7 @@ struct Engine {
     // One request's forward pass (src/engine.rs:66-112 `launch`): ids already on the device.
     void launch(const uint32_t* ids, int n, int qtype, const uint32_t* markers, int nm,
                 float* logits, bool fused) {
+        if (fused && launch_model(ids, n, qtype, markers, nm, logits)) return;
         embed_launch(ids, n, h(layout.tok_embeddings), cfg.vocab, cfg.d, f(layout.emb_norm),
                      cfg.norm_eps, x, stream);
         const jh_half* xf = x;
@@ -428,12 +461,30 @@ Engine* load_engine(const char* dir, size_t max_length, size_t batch_rows = 0) {
     e->xa = dalloc<jh_half>(2 * (size_t)c.layers * n * d, "encoder activations");
     e->qa = dalloc<jh_half>((size_t)c.layers * n * 3 * d, "encoder activations");
     e->oa = dalloc<jh_half>((size_t)c.layers * n * d, "encoder activations");
+    const size_t H = e->layout.head.size();
+    e->hxa = dalloc<jh_half>((1 + 2 * H) * n * d, "head activations");
+    e->hqa = dalloc<jh_half>(H * n * 3 * d, "head activations");
+    e->hoa = dalloc<jh_half>(H * n * d, "head activations");
+    e->hs = dalloc<jh_half>(n * d, "scorer activations");
+    for (const HeadLayer& L : e->layout.head) {
+        HeadDesc hd{};
+        hd.in_proj = e->h(L.in_proj), hd.out_proj = e->h(L.out_proj);
+        hd.linear1 = e->h(L.linear1), hd.linear2 = e->h(L.linear2);
+        hd.in_proj_colsum = e->f(L.in_proj_colsum), hd.in_proj_b = e->f(L.in_proj_b);
+        hd.out_proj_b = e->f(L.out_proj_b), hd.linear1_colsum = e->f(L.linear1_colsum);
+        hd.linear1_b = e->f(L.linear1_b), hd.linear2_b = e->f(L.linear2_b);
+        e->heads_h.push_back(hd);
+    }
+    e->heads_d = dalloc<HeadDesc>(std::max<size_t>(H, 1), "head table");
+    if (H)
+        hip_check(hipMemcpy(e->heads_d, e->heads_h.data(), H * sizeof(HeadDesc),
+                            hipMemcpyHostToDevice), "head table");
     hip_check(hipMemcpy(e->layers_d, e->layers_h.data(), e->layers_h.size() * sizeof(LayerDesc),
                         hipMemcpyHostToDevice), "layer table");
     e->layer_kernel.init(e->cus, (int)prop.sharedMemPerBlock);
     if (!attention_prepare()) throw std::runtime_error("attention: cannot set the kernel's LDS size");
-    ws = std::max(ws, e->layer_kernel.ws_floats((int)n, (int)d, c.inter));
-    counters = std::max(counters, e->layer_kernel.counters((int)n, (int)d, c.inter));
+    ws = std::max(ws, e->layer_kernel.ws_floats((int)n, (int)d, c.inter, c.head_ff));
+    counters = std::max(counters, e->layer_kernel.counters((int)n, (int)d, c.inter, c.head_ff));
     e->scratch.ws = dalloc<float>(ws, "scratch");
     e->scratch.ws_floats = ws;
     counters = (counters + 31) / 32 * 32;  // the barrier's words start on a 128-byte line
@@ -533,14 +584,17 @@ void run_batched(Engine& e, const std::vector<Request>& reqs, bool fused, float*
         const int n = nr.first;
         const size_t nm = nr.second;
         hip_check(hipEventRecord(e.ev_start[0], e.stream), "hipEventRecord");
-        embed_launch(e.bids_d, n, e.h(e.layout.tok_embeddings), e.cfg.vocab, e.cfg.d,
-                     e.f(e.layout.emb_norm), e.cfg.norm_eps, e.x, e.stream);
-        const jh_half* xf = e.x;
-        if (fused)
-            xf = e.launch_encoder_fused(0, e.cfg.layers, n, e.x, e.pos_d, e.seg_d);
-        else
-            for (int l = 0; l < e.cfg.layers; l++) e.launch_layer(l, n, e.pos_d, e.seg_d);
-        e.launch_head(xf, n, 0, e.markers_d, (int)nm, e.logits_d, e.seg_d, e.qt_d);
+        if (!fused || !e.launch_model(e.bids_d, n, 0, e.markers_d, (int)nm, e.logits_d, e.pos_d,
+                                      e.seg_d, e.qt_d)) {
+            embed_launch(e.bids_d, n, e.h(e.layout.tok_embeddings), e.cfg.vocab, e.cfg.d,
+                         e.f(e.layout.emb_norm), e.cfg.norm_eps, e.x, e.stream);
+            const jh_half* xf = e.x;
+            if (fused)
+                xf = e.launch_encoder_fused(0, e.cfg.layers, n, e.x, e.pos_d, e.seg_d);
+            else
+                for (int l = 0; l < e.cfg.layers; l++) e.launch_layer(l, n, e.pos_d, e.seg_d);
+            e.launch_head(xf, n, 0, e.markers_d, (int)nm, e.logits_d, e.seg_d, e.qt_d);
+        }
         hip_check(hipEventRecord(e.ev_end[0], e.stream), "hipEventRecord");
         if (nm)
             hip_check(hipMemcpyAsync(e.logits_h, e.logits_d, nm * 4, hipMemcpyDeviceToHost,
@@ -957,6 +1011,13 @@ int julia_hip_checkpoint_config(const char* dir, julia_hip_engine_info* out, cha
         out->max_positions = c.max_positions;
         out->norm_eps = c.norm_eps, out->head_eps = c.head_eps;
     });
+}
+
+int julia_hip_model_kernel(const Engine* e, size_t rows) {
+    if (!e || rows == 0 || rows > (size_t)e->rows) return 0;
+    const int n = (int)rows;
+    const LayerPlan plan = e->layer_kernel.default_plan(n, e->cfg.d, e->cfg.inter);
+    return e->layer_kernel.model_fits(plan, n, e->cfg.d, e->cfg.head_ff) ? 1 : 0;
 }
 
 int julia_hip_engine_info_get(const Engine* e, julia_hip_engine_info* out) {

@@ -32,6 +32,44 @@ struct LayerDesc {
     int pad_;
 };
 
+// One head layer's weights (a pre-LayerNorm encoder layer with biases, src/forward.rs:551-658),
+// as the whole-model kernel reads them (an array of these lives in device memory).
+struct HeadDesc {
+    const jh_half *in_proj, *out_proj, *linear1, *linear2;  // fragment order, biases folded
+    const float *in_proj_colsum, *in_proj_b, *out_proj_b, *linear1_colsum, *linear1_b, *linear2_b;
+};
+
+// The rest of the model around the encoder, for one launch of the whole forward pass (the
+// reference's stated next step, README.md:12-13): embed writes the encoder's x_in first; after
+// the last layer norm_add, the head layers, the scorer's lin1 and the score. Outputs that other
+// blocks read through their caches have buffers of their own, as LayerArgs': the head's
+// residual stream hxa (1 + 2 head_layers slots of x_stride: norm_add's output, then per head
+// layer after out_proj and after linear2), each head layer's qkv (hqa, q_stride) and attention
+// output (hoa, o_stride), the scorer's hidden rows hs; linear1's output goes to LayerArgs' mid.
+struct ModelArgs {
+    const uint32_t* ids;  // the rows' token ids (device)
+    const jh_half* tok_emb;
+    const float* emb_norm;
+    int vocab;
+    const HeadDesc* heads;       // device array of head_layers
+    const HeadDesc* host_heads;  // the same on the host (for the checks)
+    int head_layers, head_ff;
+    float head_eps;
+    const float* final_norm;
+    // The type embedding added by norm_add: the request's row (row_type null), or the table,
+    // each row adding row row_type[row] of it.
+    const float* type_add;
+    const int32_t* row_type;
+    jh_half *hxa, *hqa, *hoa, *hs;
+    const jh_half* lin1;
+    const float *lin1_colsum, *lin1_b;
+    const jh_half* lin2;
+    float lin2_b;
+    const uint32_t* markers;  // row indices (device)
+    int n_markers;
+    float* logits;  // n_markers (device)
+};
+
 // The activations of a launch: every output of a phase that other blocks read through their
 // caches goes to a buffer of its own, written once per launch (no L2 can hold a stale copy):
 // layer l reads x_in (its first layer) or xa[2 l - 1], writes xa[2 l] (after wo) and
@@ -52,6 +90,7 @@ struct LayerArgs {
     int m, d, inter;
     float eps;
     int rope_rows;
+    const ModelArgs* model = nullptr;  // the whole model: embed into x_in first, the head after
 };
 
 // src/forward.rs:737-757: per GEMM (qkv, wo, wi, wo_mlp) the tile height and split-K, and the
@@ -68,15 +107,21 @@ public:
     void init(int cus, int lds_bytes);
     void bind(uint32_t* barrier) { bar_ = barrier; }
     LayerPlan default_plan(int m, int d, int inter) const;
-    size_t ws_floats(int max_m, int d, int inter) const;
-    size_t counters(int max_m, int d, int inter) const;
+    // Split-K and key-range scratch for any m up to max_m (head_ff > 0: the whole-model
+    // launch's head GEMMs too).
+    size_t ws_floats(int max_m, int d, int inter, int head_ff = 0) const;
+    size_t counters(int max_m, int d, int inter, int head_ff = 0) const;
     // Phases: bits 0-4 select qkv, attention, wo, wi, wo_mlp (0x1f: whole layers; a subset only
     // with one layer). prof: null, or PROF_WORDS u64 per block of the grid and layer run.
+    // a.model: the whole forward pass (all layers and phases, from layer 0).
     void launch(const LayerArgs& a, const LayerPlan& plan, const Scratch& s, hipStream_t stream,
                 unsigned phases = 0x1f, uint64_t* prof = nullptr);
     int grid(const LayerArgs& a, const LayerPlan& plan) const;
     // LDS bytes a plan needs on m rows (weight tile, reduction and attention share it).
     static int lds_bytes(const LayerPlan& plan, int d, int inter, int m, int window);
+    // Whether the whole-model launch takes this plan on m rows: its head GEMMs fit the plan's
+    // kernel instance (the throughput instances need every head GEMM on their tile).
+    bool model_fits(const LayerPlan& plan, int m, int d, int head_ff) const;
     // Whether a grid barrier gave up waiting since the last call (then clears the words).
     // Synchronizes with the device.
     bool barrier_timed_out();

@@ -3,6 +3,9 @@
 // whole encoder in the forward pass. Each layer's five steps are phases (qkv, attention, wo, wi,
 // wo_mlp) with a grid barrier between two phases; every block strides over a phase's tasks. The
 // grid is at most the number of blocks resident at once (the cooperative launch checks it).
+// With EncParams::model the launch is the whole forward pass: embed before the first layer
+// (a wave a row), then after the last layer norm_add, each head layer's in_proj, attention,
+// out_proj, linear1 and linear2, the scorer's lin1 and the score, each a phase of its own.
 //
 // A GEMM task stages its weight tile in LDS (gemm_w_tile). The weights do not depend on the
 // previous phase, so a block copies the weight tile of its first task in the next GEMM phase
@@ -23,6 +26,7 @@
 #include "gemm_big.h"
 #include "gemm_tile.h"
 #include "layer.h"
+#include "rowops.h"
 
 namespace jh {
 
@@ -45,6 +49,11 @@ struct EncParams {
     int att_gkeys[2];  // keys the attention tile stages at once: global, window layers
     uint32_t* bar;    // the barrier's words (BAR_WORDS, zero between launches)
     uint64_t* prof;   // null, or PROF_WORDS per block and layer: see stamp()
+    // The whole model (model != 0): ModelArgs, and the head GEMMs' tile heights and splits
+    // (in_proj, out_proj, linear1, linear2, the scorer's lin1).
+    int model;
+    ModelArgs M;
+    int hbm[5], hsplits[5];
 };
 
 // Per-phase timestamps (the reference's kernels/src/prof.rs): thread 0 of each block writes the
@@ -150,6 +159,37 @@ __device__ __forceinline__ GemmParams make_gemm(const EncParams& P, int g, const
     return p;
 }
 
+// Head GEMM g (in_proj, out_proj, linear1, linear2; 4: the scorer's lin1) of head layer h, on
+// the head's buffers (ModelArgs): hx slot 2h in, 2h + 1 after out_proj, 2h + 2 after linear2.
+__device__ __forceinline__ GemmParams make_head_gemm(const EncParams& P, int g, const HeadDesc& H,
+                                                     int h) {
+    const ModelArgs& M = P.M;
+    auto hx = [&](int i) { return M.hxa + (size_t)i * P.x_stride; };
+    GemmParams p{};
+    p.m = P.m, p.ws = P.ws, p.counters = P.counters, p.eps = M.head_eps;
+    p.splits = P.hsplits[g];
+    if (g == 0) {
+        p.a = hx(2 * h), p.w = H.in_proj, p.c = M.hqa + (size_t)h * P.q_stride;
+        p.n = 3 * P.d, p.k = P.d;
+        p.stats_in = P.stats_attn, p.colsum = H.in_proj_colsum, p.bias = H.in_proj_b;
+    } else if (g == 1) {
+        p.a = M.hoa + (size_t)h * P.o_stride, p.w = H.out_proj, p.c = hx(2 * h + 1), p.res = hx(2 * h);
+        p.n = P.d, p.k = P.d, p.bias = H.out_proj_b, p.stats_out = P.stats_mlp;
+    } else if (g == 2) {
+        p.a = hx(2 * h + 1), p.w = H.linear1, p.c = P.mid, p.n = M.head_ff, p.k = P.d;
+        p.stats_in = P.stats_mlp, p.colsum = H.linear1_colsum, p.bias = H.linear1_b;
+    } else if (g == 3) {
+        p.a = P.mid, p.w = H.linear2, p.c = hx(2 * h + 2), p.res = hx(2 * h + 1);
+        p.n = P.d, p.k = M.head_ff, p.bias = H.linear2_b, p.stats_out = P.stats_attn;
+    } else {
+        p.a = hx(2 * M.head_layers), p.w = M.lin1, p.c = M.hs, p.n = P.d, p.k = P.d;
+        p.stats_in = P.stats_attn, p.colsum = M.lin1_colsum, p.bias = M.lin1_b;
+    }
+    p.tiles_n = p.n / (P.hbm[g] >= 128 ? P.hbm[g] : 64);
+    p.tiles_m = (P.m + P.hbm[g] - 1) / P.hbm[g];
+    return p;
+}
+
 __device__ __forceinline__ int gemm_tasks(const GemmParams& g) {
     return g.tiles_n * g.tiles_m * g.splits;
 }
@@ -209,9 +249,41 @@ void encoder_kernel(EncParams P) {
         return !BIG && bm < 128 && (int)blockIdx.x < gemm_tasks(g);
     };
 
+    // An attention phase: the tasks of the tile the plan and the instance take (qkv in a buffer of
+    // its own, read through the caches).
+    auto attend = [&](const AttnParams& at, uint64_t* su0) {
+        const int heads = P.d >> 6;
+        if (!BIG && at.chunks == 1 && !att_use_stream(P.m, at.window)) {
+            const int T = ((P.m + 15) >> 4) * heads, gkeys = P.att_gkeys[at.window > 0 ? 1 : 0];
+            for (int t = blockIdx.x; t < T; t += gridDim.x)
+                attention_slice_tile<false, true>(at, t, lds, gkeys, t == (int)blockIdx.x ? su0 : nullptr);
+        } else if (BIG || at.chunks == 1) {  // (the large-batch instances have one key range)
+            constexpr int NW = MODE == MODE_BIG256 ? 8 : 4;
+            const int T = ((P.m + 16 * NW - 1) / (16 * NW)) * heads;
+            for (int t = blockIdx.x; t < T; t += gridDim.x)
+                attention_stream_tile<true, NW>(at, t, lds);
+        } else {
+            const int T = ((P.m + 63) >> 6) * heads * at.chunks;
+            for (int t = blockIdx.x; t < T; t += gridDim.x) {
+                const int tile = t / at.chunks;
+                attention_tile<true>(at, tile / heads, tile % heads, t % at.chunks, (f16*)lds, s_last);
+            }
+        }
+    };
+    // A row phase: a wave a row (or marker), the grid's waves striding over them.
+    const int lane = threadIdx.x & 63, nwv = blockDim.x >> 6;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
     LayerDesc L = P.layers[P.first];
     GemmParams gq = make_gemm(P, 0, L, P.first);
     bool pre = false;  // the weight tile of this block's first task in the coming phase is fetched
+    if (P.model) {  // embed, into the first layer's x_in
+        for (int r = blockIdx.x * nwv + wv; r < P.m; r += gridDim.x * nwv)
+            embed_row<4, true>(P.M.ids, r, (const f16*)P.M.tok_emb, P.M.vocab, P.d, P.M.emb_norm,
+                               P.eps, (f16*)P.x_in, lane);
+        pre = prefetch(gq, P.bm[0]);
+        if (pre) sync(fetch_first(gq)); else sync(nothing);
+    }
     for (int li = 0; li < P.count; li++) {
         uint64_t* prof = P.prof ? P.prof + ((size_t)blockIdx.x * P.count + li) * PROF_WORDS : nullptr;
         if (prof && threadIdx.x == 0) prof[10] = __smid();
@@ -232,27 +304,9 @@ void encoder_kernel(EncParams P) {
         if (on(1)) {
             stamp(prof, 2);
             const int chunks = L.window > 0 ? P.kv[1] : P.kv[0];
-            const AttnParams at{P.qa + (size_t)l * P.q_stride, P.oa + (size_t)l * P.o_stride,
-                                P.m, P.d, L.window, chunks, P.ws, P.counters, P.seg};
-            const int heads = P.d >> 6;
-            if (!BIG && chunks == 1 && !att_use_stream(P.m, L.window)) {  // qkv: own buffer, cached
-                const int T = ((P.m + 15) >> 4) * heads, gkeys = P.att_gkeys[L.window > 0 ? 1 : 0];
-                for (int t = blockIdx.x; t < T; t += gridDim.x) {
-                    uint64_t* su = prof && t == (int)blockIdx.x ? prof + 12 : nullptr;
-                    attention_slice_tile<false, true>(at, t, lds, gkeys, su);
-                }
-            } else if (BIG || chunks == 1) {  // (the large-batch instances have one key range)
-                constexpr int NW = MODE == MODE_BIG256 ? 8 : 4;
-                const int T = ((P.m + 16 * NW - 1) / (16 * NW)) * heads;
-                for (int t = blockIdx.x; t < T; t += gridDim.x)
-                    attention_stream_tile<true, NW>(at, t, lds);
-            } else {
-                const int T = ((P.m + 63) >> 6) * heads * chunks;
-                for (int t = blockIdx.x; t < T; t += gridDim.x) {
-                    const int tile = t / chunks;
-                    attention_tile<true>(at, tile / heads, tile % heads, t % chunks, (f16*)lds, s_last);
-                }
-            }
+            attend(AttnParams{P.qa + (size_t)l * P.q_stride, P.oa + (size_t)l * P.o_stride, P.m,
+                              P.d, L.window, chunks, P.ws, P.counters, P.seg},
+                   prof ? prof + 12 : nullptr);
             stamp_end(prof, 1);
             if (on(2)) {
                 pre = prefetch(go, P.bm[1]);
@@ -292,6 +346,46 @@ void encoder_kernel(EncParams P) {
             if (pre) sync(fetch_first(gq)); else sync(nothing);
         }
     }
+    if (!P.model) return;
+
+    // ---- the head (src/forward.rs:504-717): norm_add, the head layers, lin1, the score ----
+    const ModelArgs& M = P.M;
+    sync(nothing);  // the last layer's residual stream is complete
+    {
+        const jh_half* xl = x_out_of(P, P.first + P.count - 1);
+        for (int r = blockIdx.x * nwv + wv; r < P.m; r += gridDim.x * nwv)
+            norm_add_row<4, true>((const f16*)xl, r, P.d, M.final_norm, M.type_add, M.row_type,
+                                  P.eps, (f16*)M.hxa, P.stats_attn, lane);
+    }
+    for (int h = 0; h < M.head_layers; h++) {
+        const HeadDesc H = M.heads[h];
+        const GemmParams gi = make_head_gemm(P, 0, H, h), go = make_head_gemm(P, 1, H, h),
+                         g1 = make_head_gemm(P, 2, H, h), g2 = make_head_gemm(P, 3, H, h);
+        pre = prefetch(gi, P.hbm[0]);
+        if (pre) sync(fetch_first(gi)); else sync(nothing);
+        gemm_phase<EPI_K_LNBIAS, false, MODE>(gi, P.hbm[0], lds, pre, s_last, nullptr);
+        sync(nothing);
+        attend(AttnParams{M.hqa + (size_t)h * P.q_stride, M.hoa + (size_t)h * P.o_stride, P.m, P.d,
+                          0, P.kv[0], P.ws, P.counters, P.seg},
+               nullptr);
+        pre = prefetch(go, P.hbm[1]);
+        if (pre) sync(fetch_first(go)); else sync(nothing);
+        gemm_phase<EPI_K_BIASRESSTATS, false, MODE>(go, P.hbm[1], lds, pre, s_last, nullptr);
+        pre = prefetch(g1, P.hbm[2]);
+        if (pre) sync(fetch_first(g1)); else sync(nothing);
+        gemm_phase<EPI_K_LNBIASRELU, false, MODE>(g1, P.hbm[2], lds, pre, s_last, nullptr);
+        pre = prefetch(g2, P.hbm[3]);
+        if (pre) sync(fetch_first(g2)); else sync(nothing);
+        gemm_phase<EPI_K_BIASRESSTATS, true, MODE>(g2, P.hbm[3], lds, pre, s_last, nullptr);
+    }
+    const GemmParams gs = make_head_gemm(P, 4, HeadDesc{}, 0);
+    pre = prefetch(gs, P.hbm[4]);
+    if (pre) sync(fetch_first(gs)); else sync(nothing);
+    gemm_phase<EPI_K_LNBIASGELU, false, MODE>(gs, P.hbm[4], lds, pre, s_last, nullptr);
+    sync(nothing);
+    for (int i = blockIdx.x * nwv + wv; i < M.n_markers; i += gridDim.x * nwv)
+        score_row<4>((const f16*)M.hs, P.m, P.d, (const f16*)M.lin2, M.lin2_b, M.markers, i,
+                     M.logits, lane);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -359,11 +453,65 @@ void LayerKernel::init(int cus, int lds_max) {
 // weight tile is fetched during the barrier, later rounds fetch their own; a split costs a
 // partial exchange. The weight tile must fit the LDS. Key ranges for global attention as the
 // per-step attention's, none for sliding-window layers (src/forward.rs:173-189's rule).
+// The latency tile's height and split-K for an m x cols x k GEMM (the cost model above).
+static void lat_tile(int m, int cols, int k, int cus, int lds_max, int& bm_out, int& splits_out) {
+    const double bw = 67e3;  // bytes per us into one CU
+    double best = 1e30;
+    bm_out = 16, splits_out = k / 32 >= 8 ? 2 : 1;
+    for (int bm : {16, 32, 64}) {
+        for (int s = 1; s <= 4; s++) {
+            if (k / 32 < 4 * s) continue;  // every wave needs a K unit
+            if (w_tile_bytes(k, s) > lds_max) continue;
+            const long tasks = (long)(cols / 64) * ((m + bm - 1) / bm) * s;
+            const long rounds = (tasks + cus - 1) / cus;
+            const double a_us = (double)bm * (k / s) * 2 / bw;
+            const double w_us = (double)w_tile_bytes(k, s) / bw;
+            const double mma_us = (bm / 16) * (k / s / 32 / 4.0) * 4 * 16 / 2400.0;
+            const double task = 1.2 + a_us + mma_us + 0.1 * (bm / 16) + 0.4;
+            const double cost = rounds * task + (rounds - 1) * w_us + (s > 1 ? 1.5 : 0.0);
+            if (cost < best - 1e-9) best = cost, bm_out = bm, splits_out = s;
+        }
+    }
+}
+
+// The head GEMMs' shapes (in_proj, out_proj, linear1, linear2, the scorer's lin1) and whether
+// each has a LayerNorm epilogue.
+static void head_shapes(int d, int ff, int cols[5], int ks[5], bool ln[5]) {
+    const int c[5] = {3 * d, d, ff, d, d}, k[5] = {d, d, d, ff, d};
+    const bool l[5] = {true, false, true, false, true};
+    for (int g = 0; g < 5; g++) cols[g] = c[g], ks[g] = k[g], ln[g] = l[g];
+}
+
+// The head GEMMs' tiles under `plan` on m rows: the throughput instances' tile (every head GEMM
+// must take it: false if one does not), else the latency tile's cost model.
+static bool head_plan(const LayerPlan& plan, int m, int d, int ff, int cus, int lds_max,
+                      int bm[5], int splits[5]) {
+    int cols[5], ks[5];
+    bool ln[5];
+    head_shapes(d, ff, cols, ks, ln);
+    const int mode = LayerKernel::big_mode(plan, m);
+    for (int g = 0; g < 5; g++) {
+        if (mode != MODE_LAT) {
+            const int t = mode == MODE_BIG256 ? 256 : 128;
+            if (cols[g] % t || ks[g] % 64 || (ln[g] && ks[g] > 128 * BIG_LN_SLOTS)) return false;
+            bm[g] = t, splits[g] = 1;
+        } else {
+            lat_tile(m, cols[g], ks[g], cus, lds_max, bm[g], splits[g]);
+            if (w_tile_bytes(ks[g], splits[g]) > lds_max) return false;
+        }
+    }
+    return true;
+}
+
+bool LayerKernel::model_fits(const LayerPlan& plan, int m, int d, int head_ff) const {
+    int bm[5], splits[5];
+    return d <= 1024 && head_plan(plan, m, d, head_ff, cus_, lds_max_, bm, splits);
+}
+
 LayerPlan LayerKernel::default_plan(int m, int d, int inter) const {
     LayerPlan p{};
     int cols[4], ks[4];
     shapes(d, inter, cols, ks);
-    const double bw = 67e3;  // bytes per us into one CU
     for (int g = 0; g < 4; g++) {
         // Large batches: the throughput tile (LayerNorm epilogues, qkv and wi, need K <= 1024),
         // 256 x 256 where every GEMM's columns allow it (big_tiles below), else 128 x 128.
@@ -373,22 +521,7 @@ LayerPlan LayerKernel::default_plan(int m, int d, int inter) const {
             p.bm[g] = 128, p.splits[g] = 1;
             continue;
         }
-        double best = 1e30;
-        p.bm[g] = 16, p.splits[g] = ks[g] / 32 >= 8 ? 2 : 1;
-        for (int bm : {16, 32, 64}) {
-            for (int s = 1; s <= 4; s++) {
-                if (ks[g] / 32 < 4 * s) continue;  // every wave needs a K unit
-                if (w_tile_bytes(ks[g], s) > lds_max_) continue;
-                const long tasks = (long)(cols[g] / 64) * ((m + bm - 1) / bm) * s;
-                const long rounds = (tasks + cus_ - 1) / cus_;
-                const double a_us = (double)bm * (ks[g] / s) * 2 / bw;
-                const double w_us = (double)w_tile_bytes(ks[g], s) / bw;
-                const double mma_us = (bm / 16) * (ks[g] / s / 32 / 4.0) * 4 * 16 / 2400.0;
-                const double task = 1.2 + a_us + mma_us + 0.1 * (bm / 16) + 0.4;
-                const double cost = rounds * task + (rounds - 1) * w_us + (s > 1 ? 1.5 : 0.0);
-                if (cost < best - 1e-9) best = cost, p.bm[g] = bm, p.splits[g] = s;
-            }
-        }
+        lat_tile(m, cols[g], ks[g], cus_, lds_max_, p.bm[g], p.splits[g]);
     }
     p.kv[0] = attention_chunks(m, d, 0, cus_);
     p.kv[1] = 1;
@@ -400,24 +533,35 @@ LayerPlan LayerKernel::default_plan(int m, int d, int inter) const {
     return p;
 }
 
-size_t LayerKernel::ws_floats(int max_m, int d, int inter) const {
+size_t LayerKernel::ws_floats(int max_m, int d, int inter, int head_ff) const {
     size_t ws = 0;
-    int cols[4], ks[4];
+    int cols[4], ks[4], hc[5], hk[5];
+    bool hl[5];
     shapes(d, inter, cols, ks);
+    if (head_ff > 0) head_shapes(d, head_ff, hc, hk, hl);
     for (int m = 1; m <= max_m; m++) {
         const LayerPlan p = default_plan(m, d, inter);
         for (int g = 0; g < 4; g++)
             ws = std::max(ws, gemm_ws_floats(m, cols[g], GemmConfig{p.bm[g], p.splits[g]}));
         ws = std::max(ws, attention_ws_floats(m, d, p.kv[0]));
+        int hbm[5], hsp[5];
+        if (head_ff > 0 && head_plan(p, m, d, head_ff, cus_, lds_max_, hbm, hsp))
+            for (int g = 0; g < 5; g++)
+                ws = std::max(ws, gemm_ws_floats(m, hc[g], GemmConfig{hbm[g], hsp[g]}));
     }
     return ws;
 }
 
-size_t LayerKernel::counters(int max_m, int d, int inter) const {
+size_t LayerKernel::counters(int max_m, int d, int inter, int head_ff) const {
     size_t c = attention_counters(max_m, d);
-    int cols[4], ks[4];
+    int cols[4], ks[4], hc[5], hk[5];
+    bool hl[5];
     shapes(d, inter, cols, ks);
     for (int g = 0; g < 4; g++) c = std::max(c, gemm_counters(max_m, cols[g], GemmConfig{16, 2}));
+    if (head_ff > 0) {
+        head_shapes(d, head_ff, hc, hk, hl);
+        for (int g = 0; g < 5; g++) c = std::max(c, gemm_counters(max_m, hc[g], GemmConfig{16, 2}));
+    }
     return c;
 }
 
@@ -465,7 +609,7 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
              " rows and one key range: " + plan.str());
     if ((mode == MODE_BIG128 && per_cu_big_ <= 0) || (mode == MODE_BIG256 && per_cu_big256_ <= 0))
         fail("the encoder kernel's large-batch instance does not fit on a CU");
-    const int lds = mode == MODE_BIG256   ? big_lds_bytes(256)
+    int lds = mode == MODE_BIG256   ? big_lds_bytes(256)
                     : mode == MODE_BIG128 ? big_lds_bytes(128)
                                           : lds_bytes(plan, a.d, a.inter, a.m, window);
     if (lds > lds_max_) fail("the plan's weight tiles do not fit the LDS: " + plan.str());
@@ -505,6 +649,58 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
             fail("the key-range scratch is too small for " + std::to_string(a.m) + " tokens");
     }
 
+    // The whole model: embed before layer 0, the head after the last layer.
+    int hbm[5] = {}, hsplits[5] = {};
+    int lds_model = lds;
+    const ModelArgs* M = a.model;
+    if (M) {
+        auto al16 = [](const void* q) { return ((uintptr_t)q % 16) == 0; };
+        if (a.first != 0 || phases != 0x1f) fail("the whole model runs every phase from layer 0");
+        if (a.d > 1024) fail("the whole model takes d up to 1024");
+        if (!M->ids || !M->tok_emb || !M->emb_norm || M->vocab <= 0 || !M->final_norm ||
+            !M->type_add || !M->hxa || !M->hs || !M->lin1 || !M->lin1_colsum || !M->lin1_b ||
+            !M->lin2 || M->head_layers < 0 || M->head_ff <= 0 || M->n_markers < 0 ||
+            (M->head_layers > 0 && (!M->heads || !M->host_heads || !M->hqa || !M->hoa)) ||
+            (M->n_markers > 0 && (!M->markers || !M->logits)))
+            fail("bad model arguments");
+        if (!al16(M->tok_emb) || !al16(M->emb_norm) || !al16(M->final_norm) || !al16(M->type_add) ||
+            !al16(M->hxa) || !al16(M->hs) || !al16(M->lin2))
+            fail("the model's tables and buffers must be 16-byte aligned");
+        if (!head_plan(plan, a.m, a.d, M->head_ff, cus_, lds_max_, hbm, hsplits))
+            fail("the head's GEMMs do not take the plan's tiles: " + plan.str());
+        int hc[5], hk[5];
+        bool hl[5];
+        head_shapes(a.d, M->head_ff, hc, hk, hl);
+        auto hx = [&](int i) { return M->hxa + (size_t)i * a.x_stride; };
+        auto check = [&](int g, int epi, const jh_half* in, const jh_half* w, jh_half* out,
+                         const float* st_in, const float* colsum, const float* bias, float* st_out) {
+            Gemm q{};
+            q.epi = epi, q.a = in, q.w = w, q.c = out, q.m = a.m, q.n = hc[g], q.k = hk[g];
+            q.stats_in = st_in, q.colsum = colsum, q.bias = bias, q.stats_out = st_out;
+            q.eps = M->head_eps;
+            gemm_check(q, GemmConfig{hbm[g], hsplits[g]}, s);
+            if (mode == MODE_LAT)
+                lds_model = std::max({lds_model, w_tile_bytes(hk[g], hsplits[g]), red_bytes(hbm[g])});
+        };
+        for (int h = 0; h < M->head_layers; h++) {
+            const HeadDesc& H = M->host_heads[h];
+            jh_half* hq = M->hqa + (size_t)h * a.q_stride;
+            jh_half* ho = M->hoa + (size_t)h * a.o_stride;
+            check(0, EPI_K_LNBIAS, hx(2 * h), H.in_proj, hq, a.stats_attn, H.in_proj_colsum,
+                  H.in_proj_b, nullptr);
+            check(1, EPI_K_BIASRESSTATS, ho, H.out_proj, hx(2 * h + 1), nullptr, nullptr,
+                  H.out_proj_b, a.stats_mlp);
+            check(2, EPI_K_LNBIASRELU, hx(2 * h + 1), H.linear1, a.mid, a.stats_mlp,
+                  H.linear1_colsum, H.linear1_b, nullptr);
+            check(3, EPI_K_BIASRESSTATS, a.mid, H.linear2, hx(2 * h + 2), nullptr, nullptr,
+                  H.linear2_b, a.stats_attn);
+        }
+        check(4, EPI_K_LNBIASGELU, hx(2 * M->head_layers), M->lin1, M->hs, a.stats_attn,
+              M->lin1_colsum, M->lin1_b, nullptr);
+        lds_model = (lds_model + 15) / 16 * 16;
+        if (lds_model > lds_max_) fail("the head's weight tiles do not fit the LDS");
+    }
+
     EncParams P{};
     P.layers = a.layers, P.first = a.first, P.count = a.count;
     P.x_in = a.x_in, P.xa = a.xa, P.qa = a.qa, P.oa = a.oa, P.mid = a.mid;
@@ -520,6 +716,12 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
     for (int ph = 1; ph < 5; ph++)
         if (((phases >> ph) & 1) && ((phases >> (ph - 1)) & 1)) barriers++;
     P.barriers = barriers * a.count + (a.count - 1);
+    if (M) {  // after embed, after the last layer, five a head layer, before lin1 and the score
+        P.model = 1, P.M = *M;
+        for (int g = 0; g < 5; g++) P.hbm[g] = hbm[g], P.hsplits[g] = hsplits[g];
+        P.barriers += 4 + 5 * M->head_layers;
+        lds = lds_model;
+    }
     P.lds_main = lds;
     P.att_gkeys[0] = attention_gkeys(a.m, 0);
     P.att_gkeys[1] = attention_gkeys(a.m, window);

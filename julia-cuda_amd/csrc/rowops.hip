@@ -1,132 +1,39 @@
-// The bandwidth-bound row kernels, one wave64 per row: embed (table gather + LayerNorm),
-// norm_add (the head's input: LayerNorm + type embedding, and the row statistics) and score
-// (the scorer's last linear on the marker rows). The reference's are kernels/src/main.rs:47-200
-// (one 32-lane warp per row, D fixed at 384); here D is any multiple of 64 and a lane takes
-// 4 f16 (8 bytes) at a time, 64 lanes covering 512 contiguous bytes per step.
+// The bandwidth-bound row kernels, one wave64 per row (the row functions of rowops.h): embed,
+// norm_add and score (the reference's kernels/src/main.rs:47-200).
 #include <algorithm>
 #include <stdexcept>
 #include <string>
 
-#include "device.h"
+#include "rowops.h"
 
 namespace jh {
-
-// Loads row `src` (d f16) as chunks c = lane + 64 j of 4 values, j < NC (chunks past d/4 are 0).
-template <int NC>
-__device__ __forceinline__ void load_row(const f16* src, int d, int lane, float (&v)[NC][4]) {
-#pragma unroll
-    for (int j = 0; j < NC; j++) {
-        const int c = lane + 64 * j;
-        if (c < (d >> 2)) {
-            const half4 q = *(const half4*)(src + 4 * c);
-#pragma unroll
-            for (int e = 0; e < 4; e++) v[j][e] = (float)q[e];
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; e++) v[j][e] = 0.0f;
-        }
-    }
-}
-
-// Two-pass LayerNorm statistics over d values (src/check.rs:62-83's emulation; the mean first,
-// then the mean square deviation), as (mean, 1 / sqrt(var + eps)).
-template <int NC>
-__device__ __forceinline__ float2 ln_two_pass(const float (&v)[NC][4], int d, int lane, float eps) {
-    float s = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NC; j++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) s += v[j][e];
-    const float mean = wave_sum(s) / (float)d;
-    float q = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NC; j++)
-        if (lane + 64 * j < (d >> 2))
-#pragma unroll
-            for (int e = 0; e < 4; e++) q += (v[j][e] - mean) * (v[j][e] - mean);
-    const float var = wave_sum(q) / (float)d;
-    return make_float2(mean, 1.0f / sqrtf(var + eps));
-}
 
 template <int NC>
 __global__ __launch_bounds__(256) void embed_kernel(const uint32_t* ids, int n, const f16* table,
                                                     int vocab, int d, const float* gamma, float eps,
                                                     f16* x) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= n) return;  // whole waves
-    const uint32_t id = min(ids[row], (uint32_t)(vocab - 1));  // the host checks ids < vocab
-    float v[NC][4];
-    load_row<NC>(table + (size_t)id * d, d, lane, v);
-    const float2 st = ln_two_pass<NC>(v, d, lane, eps);
-#pragma unroll
-    for (int j = 0; j < NC; j++) {
-        const int c = lane + 64 * j;
-        if (c < (d >> 2)) {
-            const float4 gm = *(const float4*)(gamma + 4 * c);
-            const float gs[4] = {gm.x, gm.y, gm.z, gm.w};
-            half4 o;
-#pragma unroll
-            for (int e = 0; e < 4; e++) o[e] = (f16)((v[j][e] - st.x) * st.y * gs[e]);
-            *(half4*)(x + (size_t)row * d + 4 * c) = o;
-        }
-    }
+    embed_row<NC, false>(ids, row, table, vocab, d, gamma, eps, x, threadIdx.x & 63);
 }
 
-// out = LN(x) . gamma + add; stats[row][g] = (sum, sum of squares) of the stored f16 values of
-// 64-column group g (chunks 16 g .. 16 g + 15: lanes 16 (g % 4) .. + 15 of step g / 4).
 template <int NC>
 __global__ __launch_bounds__(256) void norm_add_kernel(const f16* x, int n, int d,
                                                        const float* gamma, const float* add,
                                                        const int32_t* row_type, float eps,
                                                        f16* out, float* stats) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= n) return;
-    if (row_type) add += (size_t)row_type[row] * d;
-    float v[NC][4];
-    load_row<NC>(x + (size_t)row * d, d, lane, v);
-    const float2 st = ln_two_pass<NC>(v, d, lane, eps);
-#pragma unroll
-    for (int j = 0; j < NC; j++) {
-        const int c = lane + 64 * j;
-        float s = 0.0f, q = 0.0f;
-        if (c < (d >> 2)) {
-            const float4 gm = *(const float4*)(gamma + 4 * c);
-            const float4 ad = *(const float4*)(add + 4 * c);
-            const float gs[4] = {gm.x, gm.y, gm.z, gm.w}, as[4] = {ad.x, ad.y, ad.z, ad.w};
-            half4 o;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                o[e] = (f16)((v[j][e] - st.x) * st.y * gs[e] + as[e]);
-                const float y = (float)o[e];
-                s += y;
-                q += y * y;
-            }
-            *(half4*)(out + (size_t)row * d + 4 * c) = o;
-        }
-        s = group_sum<16>(s);
-        q = group_sum<16>(q);
-        if ((lane & 15) == 0 && c < (d >> 2))
-            *(float2*)(stats + ((size_t)row * (d >> 6) + (c >> 4)) * 2) = make_float2(s, q);
-    }
+    norm_add_row<NC, false>(x, row, d, gamma, add, row_type, eps, out, stats, threadIdx.x & 63);
 }
 
 template <int NC>
 __global__ __launch_bounds__(256) void score_kernel(const f16* y, int n, int d, const f16* w,
                                                     float b, const uint32_t* markers, int k,
                                                     float* logits) {
-    const int i = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (i >= k) return;
-    const uint32_t r = min(markers[i], (uint32_t)(n - 1));  // the host checks markers < n
-    float v[NC][4], u[NC][4];
-    load_row<NC>(y + (size_t)r * d, d, lane, v);
-    load_row<NC>(w, d, lane, u);
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NC; j++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) acc += v[j][e] * u[j][e];
-    acc = wave_sum(acc);
-    if (lane == 0) logits[i] = acc + b;
+    score_row<NC>(y, n, d, w, b, markers, i, logits, threadIdx.x & 63);
 }
 
 // dst = src, 16 bytes per thread per step, grid-stride: the plain copy kernel the byte counters

@@ -77,7 +77,7 @@ class EngineInfo(ctypes.Structure):
 # Every symbol include/julia_hip.h declares.
 EXPORTS = [
     "julia_cuda_tier", "julia_cuda_load", "julia_cuda_free", "julia_cuda_device", "julia_cuda_run",
-    "julia_hip_load", "julia_hip_run_batched",
+    "julia_hip_load", "julia_hip_run_batched", "julia_hip_model_kernel",
     "julia_hip_scratch_new", "julia_hip_scratch_free", "julia_hip_gemm", "julia_hip_attention",
     "julia_hip_attention_seg",
     "julia_hip_embed", "julia_hip_norm_add", "julia_hip_score", "julia_hip_time_gemm",
@@ -112,6 +112,7 @@ def lib():
         "julia_cuda_device": (None, [_VP, _CP, _SZ]),
         "julia_cuda_run": (_I, [_VP, _SZ, _VP, _VP, _VP, _VP, _VP, _I, _VP, _VP, _CP, _SZ]),
         "julia_hip_load": (_VP, [_CP, _SZ, _SZ, _CP, _SZ]),
+        "julia_hip_model_kernel": (_I, [_VP, _SZ]),
         "julia_hip_run_batched": (_I, [_VP, _SZ, _VP, _VP, _VP, _VP, _VP, _I, _VP, _VP, _CP, _SZ]),
         "julia_hip_scratch_new": (_VP, [_SZ, _SZ, _CP, _SZ]),
         "julia_hip_scratch_free": (None, [_VP]),
@@ -247,6 +248,10 @@ class Engine:
             out.append(logits[at:at + m].copy())
             at += m
         return out, ms[: len(requests)].copy()
+
+    def model_kernel(self, rows):
+        """Whether layer_fused runs `rows` rows as one whole-model launch."""
+        return bool(lib().julia_hip_model_kernel(self.ptr, rows))
 
     def run_trace(self, ids, markers, qtype, layer_fused=False, trace=True, head_x=False):
         inf = self.info()

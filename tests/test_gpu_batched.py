@@ -76,6 +76,8 @@ def test_batched_matches_one_by_one(engine, fused):
     rng = np.random.default_rng(21 + fused)
     reqs = requests(rng, 24)
     say(f"batched run: {len(reqs)} requests, {sum(len(r[0]) for r in reqs)} rows, fused={fused}")
+    if fused:  # the passes run as whole-model launches
+        assert all(e.model_kernel(sum(len(reqs[i][0]) for i in g)) for g in passes(reqs, ROWS))
     got, ms = e.run(reqs, layer_fused=fused, batched=True)
     alone, _ = e.run(reqs, layer_fused=fused)
     path_diff(got, alone, "batched vs julia_cuda_run")

@@ -113,6 +113,27 @@ def test_layer_kernel_matches_per_step(small):
         check_logits(lf, want, "layer kernel logits")
 
 
+def test_whole_model_kernel(small):
+    """layer_fused through julia_cuda_run: the whole forward pass as one cooperative launch
+    (embed, the layers, the head, the score; the reference's stated next step, README.md:12-13),
+    against the oracle and the per-step kernels, every question type, up to max_length."""
+    e, m = small
+    rng = np.random.default_rng(13)
+    for n in (72, 363, 1024):
+        assert e.model_kernel(n), n
+        ids, markers = request(rng, n, SMALL["vocab"], nm=5)
+        q = n % 3
+        say(f"whole-model kernel n={n} qtype={q}")
+        lf, ms = e.run([(ids, markers, q), (ids, markers, q)], layer_fused=True)
+        ls, _ = e.run([(ids, markers, q)])
+        np.testing.assert_array_equal(lf[0], lf[1])  # deterministic launch to launch
+        d = np.abs(lf[0] - ls[0]).max()
+        mean, mx = check_logits(lf[0], m.forward(ids, q, markers), "whole-model logits")
+        say(f"  oracle mean |d| {mean:.2e} max {mx:.2e}; per-step max |d| {d:.2e}; {ms[0]:.3f} ms")
+        assert d <= 1e-2
+    assert not e.model_kernel(0) and not e.model_kernel(1025)
+
+
 def test_batch_of_requests(small):
     """Engine::run's queue (src/engine.rs:170-196): more requests than one queue of 16, mixed
     lengths and question types, against each request run alone."""
