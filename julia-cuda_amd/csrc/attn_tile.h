@@ -3,6 +3,8 @@
 // LDS. See attention.hip for the design.
 #pragma once
 
+#include <type_traits>
+
 #include "device.h"
 
 namespace jh {
@@ -518,11 +520,11 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
         qf[1] = load16h<false>(qp + 32);
     }
 
-    // Block b (keys k0 + 64 b ..) into stage b % NS: 16 wave loads of 1 KB (8 rows of K, then of
-    // V), LOADS a wave; lane l fills LDS chunk 64 I + l = row c / 8, logical chunk (c % 8) ^ (row
-    // % 8). Rows past n are clamped (their keys are masked).
-    auto stage = [&](int b) {
-        char* dst = lds + (b % NS) * 16384;
+    // Block b (keys k0 + 64 b ..) into stage st = b % NS: 16 wave loads of 1 KB (8 rows of K,
+    // then of V), LOADS a wave; lane l fills LDS chunk 64 I + l = row c / 8, logical chunk
+    // (c % 8) ^ (row % 8). Rows past n are clamped (their keys are masked).
+    auto stage = [&](int b, int st) {
+        char* dst = lds + st * 16384;
         const int kb = k0 + 64 * b;
 #pragma unroll
         for (int qq = 0; qq < LOADS; qq++) {
@@ -541,9 +543,19 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
 #pragma unroll
     for (int t = 0; t < 4; t++) oacc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    if (nblk > 0) stage(0);
-    if (nblk > 1) stage(1);
-    for (int b = 0; b < nblk; b++) {
+    // The lane's LDS offsets within a stage, loop-invariant: with the stage a constant in each
+    // unrolled step below, every read is a base register plus an immediate. (Rows 16 t, and
+    // 32 hf + 16 x, keep the swizzle of their row % 8: offsets 2048 t, 4096 hf + 2048 x.)
+    int koff[2], voff[4];
+#pragma unroll
+    for (int k2 = 0; k2 < 2; k2++) koff[k2] = att_swz(r16, 4 * k2 + g);
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+        voff[dt] = 8192 + att_swz(4 * g + j, 2 * dt + (q >> 1)) + (q & 1) * 8;
+
+    // Block b, in stage ST = b % NS (a constant).
+    auto step = [&](int b, auto st_) {
+        constexpr int ST = decltype(st_)::value;
         // Block b's copies done (block b + 1's may stay in flight; the query loads came first),
         // then every wave's: and every wave is done with block b - 1, whose stage block b + 2
         // takes.
@@ -552,11 +564,10 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
         else
             wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
-        if (b + 2 < nblk) stage(b + 2);
+        if (b + 2 < nblk) stage(b + 2, (ST + 2) % NS);
         const int kb = k0 + 64 * b;
-        if (kb + 64 <= wlo || kb >= whi) continue;
-        const char* ks = lds + (b % NS) * 16384;
-        const char* vs = ks + 8192;
+        if (kb + 64 <= wlo || kb >= whi) return;
+        const char* st = lds + ST * 16384;
         // The 64 keys in one step: S^T for keys kb + 16 t + 4 g + e (t < 4), one max and one
         // rescale; P . V in two K-32 halves.
         half8 kf[4][2];
@@ -564,15 +575,13 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
 #pragma unroll
         for (int t = 0; t < 4; t++)
 #pragma unroll
-            for (int k2 = 0; k2 < 2; k2++)
-                kf[t][k2] = *(const half8*)(ks + att_swz(16 * t + r16, 4 * k2 + g));
+            for (int k2 = 0; k2 < 2; k2++) kf[t][k2] = *(const half8*)(st + koff[k2] + 2048 * t);
 #pragma unroll
         for (int hf = 0; hf < 2; hf++)
 #pragma unroll
             for (int dt = 0; dt < 4; dt++) {
-                const int ch = 2 * dt + (q >> 1), off = (q & 1) * 8;
-                vlo[hf][dt] = lds_read_tr16(vs + att_swz(32 * hf + 4 * g + j, ch) + off);
-                vhi[hf][dt] = lds_read_tr16(vs + att_swz(32 * hf + 16 + 4 * g + j, ch) + off);
+                vlo[hf][dt] = lds_read_tr16(st + voff[dt] + 4096 * hf);
+                vhi[hf][dt] = lds_read_tr16(st + voff[dt] + 4096 * hf + 2048);
             }
         __builtin_amdgcn_sched_barrier(0);
         floatx4 sc[4];
@@ -640,6 +649,15 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
                 oacc[dt] = mfma16(vf, pf, oacc[dt]);
             }
         }
+    };
+
+    static_assert(NS == 3, "the loop below is unrolled by the stages");
+    if (nblk > 0) stage(0, 0);
+    if (nblk > 1) stage(1, 1);
+    for (int b = 0; b < nblk; b += NS) {
+        step(b, std::integral_constant<int, 0>{});
+        if (b + 1 < nblk) step(b + 1, std::integral_constant<int, 1>{});
+        if (b + 2 < nblk) step(b + 2, std::integral_constant<int, 2>{});
     }
 
     const float tot = sum_xor32(sum_xor16(lsum));
