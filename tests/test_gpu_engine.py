@@ -224,6 +224,35 @@ def test_batched_encoder_on_256_tiles(torch_cuda):
     e.close()
 
 
+def test_whole_model_on_256_tiles(torch_cuda):
+    """The whole-model launch on the 256 x 256 instance (config 4's widths, head_ff 1536, a
+    batched pass past 2048 rows): every head GEMM on the throughput tile, attention bounded to
+    each request, every question type; against the per-step kernels on the same pass and the
+    oracle on single requests."""
+    c = dict(d=768, layers=2, inter=1152, vocab=1000, head_ff=1536, max_positions=4096, seed=11)
+    e = jh.Engine(spec(c), max_length=1024, batch_rows=2600)
+    m = O.Model(O.cfg(**c))
+    rng = np.random.default_rng(29)
+    lens = [300, 1024, 17, 700, 1, 513]
+    reqs = []
+    for i, n in enumerate(lens):
+        ids = rng.integers(0, c["vocab"], n).astype(np.uint32)
+        reqs.append((ids, rng.integers(0, n, 4).astype(np.uint32), i % 3))
+    assert e.model_kernel(sum(lens))
+    plan, _ = e.profile_layer(sum(lens), 0)
+    assert list(plan[:4]) == [256, 256, 256, 256], plan
+    lf, ms = e.run(reqs, layer_fused=True, batched=True)
+    ls, _ = e.run(reqs, batched=True)
+    a, b = np.concatenate(lf), np.concatenate(ls)
+    say(f"whole model, 256 tiles: {sum(lens)} rows {ms[0]:.3f} ms; max |d| to per-step "
+        f"{np.abs(a - b).max():.2e}")
+    assert np.isfinite(a).all() and np.abs(a - b).max() <= 1e-2
+    for i in (0, 2, 5):
+        ids, markers, q = reqs[i]
+        check_logits(lf[i], m.forward(ids, q, markers), f"request {i} against the oracle")
+    e.close()
+
+
 def test_load_errors(torch_cuda):
     with pytest.raises(jh.JuliaHipError, match="max_length"):
         jh.Engine(spec(dict(SMALL, max_positions=512)), max_length=600)
