@@ -134,6 +134,26 @@ def test_whole_model_kernel(small):
     assert not e.model_kernel(0) and not e.model_kernel(1025)
 
 
+def test_no_head_layers(torch_cuda):
+    """A model with no head layers (norm_add straight into the scorer): the per-step path, the
+    whole-model launch and the batched pass against the oracle."""
+    c = dict(SMALL, head_layers=0)
+    e = jh.Engine(spec(c), max_length=512, batch_rows=1024)
+    m = O.Model(O.cfg(**c))
+    rng = np.random.default_rng(31)
+    reqs = []
+    for n in (40, 300, 129):
+        ids, markers = request(rng, n, c["vocab"])
+        reqs.append((ids, markers, n % 3))
+    for fused in (False, True):
+        for batched in (False, True):
+            out, _ = e.run(reqs, layer_fused=fused, batched=batched)
+            for (ids, markers, q), lg in zip(reqs, out):
+                check_logits(lg, m.forward(ids, q, markers), f"fused={fused} batched={batched}")
+    assert e.model_kernel(300)
+    e.close()
+
+
 def test_batch_of_requests(small):
     """Engine::run's queue (src/engine.rs:170-196): more requests than one queue of 16, mixed
     lengths and question types, against each request run alone."""
