@@ -297,29 +297,50 @@ struct Engine {
     // into stats_a), the scorer's lin1 (LN from stats_a, bias, GELU) and the score.
     // Concatenated requests: seg bounds each row's attention to its request, row_type gives its
     // question type (qtype is then unused) and the markers are row indices into the whole set.
-    void launch_head(const jh_half* x, int n, int qtype, const uint32_t* markers, int nm,
+    // After the last head layer's attention every step is row-wise and only the marker rows are
+    // scored, so unless all_rows (or the markers are not fewer than the rows) those steps run on
+    // the marker rows alone, gathered into rows 0 .. nm - 1 of spare buffers: the same values
+    // for those rows (up to the GEMM tiles' summation order, which depends on the row count).
+    void launch_head(const jh_half* xin, int n, int qtype, const uint32_t* markers, int nm,
                      float* logits, const int32_t* seg = nullptr,
-                     const int32_t* row_type = nullptr) {
+                     const int32_t* row_type = nullptr, bool all_rows = false) {
         const int d = cfg.d, F = cfg.head_ff;
         const float* add = f(layout.type_emb) + (row_type ? 0 : (size_t)qtype * d);
-        norm_add_launch(x, n, d, f(layout.final_norm), add, cfg.norm_eps, hx, stats_a, stream,
+        norm_add_launch(xin, n, d, f(layout.final_norm), add, cfg.norm_eps, hx, stats_a, stream,
                         row_type);
-        for (const HeadLayer& H : layout.head) {
+        const bool compact = !all_rows && nm > 0 && nm < n;
+        // The marker rows' residual stream: x is free once norm_add has read the encoder's
+        // output; their attention output goes to qkv (free once attention has read it).
+        jh_half* hr = hx;
+        int m = n;
+        const size_t L = layout.head.size();
+        if (compact && L == 0) {  // straight into the scorer: its LN statistics go along
+            gather_rows_launch(hx, nullptr, stats_a, n, d, markers, nm, x, nullptr, stats_b, stream);
+            hr = x, m = nm;
+        }
+        for (size_t i = 0; i < L; i++) {
+            const HeadLayer& H = layout.head[i];
             gemm(EPI_K_LNBIAS, hx, h(H.in_proj), qkv, n, 3 * d, d, stats_a, f(H.in_proj_colsum),
                  cfg.head_eps, f(H.in_proj_b), nullptr, nullptr);
             attention_launch(qkv, o, n, d, 0, attention_chunks(n, d, 0, cus), scratch, stream,
                              seg);
-            gemm(EPI_K_BIASRESSTATS, o, h(H.out_proj), hx, n, d, d, nullptr, nullptr, 0.0f,
+            const jh_half* ao = o;
+            if (compact && i + 1 == L) {
+                gather_rows_launch(o, hx, nullptr, n, d, markers, nm, qkv, x, nullptr, stream);
+                ao = qkv, hr = x, m = nm;
+            }
+            gemm(EPI_K_BIASRESSTATS, ao, h(H.out_proj), hr, m, d, d, nullptr, nullptr, 0.0f,
                  f(H.out_proj_b), nullptr, stats_b);
-            gemm(EPI_K_LNBIASRELU, hx, h(H.linear1), mid, n, F, d, stats_b, f(H.linear1_colsum),
+            gemm(EPI_K_LNBIASRELU, hr, h(H.linear1), mid, m, F, d, stats_b, f(H.linear1_colsum),
                  cfg.head_eps, f(H.linear1_b), nullptr, nullptr);
-            gemm(EPI_K_BIASRESSTATS, mid, h(H.linear2), hx, n, d, F, nullptr, nullptr, 0.0f,
+            gemm(EPI_K_BIASRESSTATS, mid, h(H.linear2), hr, m, d, F, nullptr, nullptr, 0.0f,
                  f(H.linear2_b), nullptr, stats_a);
         }
         const Scorer& S = layout.scorer;
-        gemm(EPI_K_LNBIASGELU, hx, h(S.lin1), o, n, d, d, stats_a, f(S.lin1_colsum), cfg.head_eps,
+        const float* st = compact && L == 0 ? stats_b : stats_a;
+        gemm(EPI_K_LNBIASGELU, hr, h(S.lin1), o, m, d, d, st, f(S.lin1_colsum), cfg.head_eps,
              f(S.lin1_b), nullptr, nullptr);
-        score_launch(o, n, d, h(S.lin2), S.lin2_b, markers, nm, logits, stream);
+        score_launch(o, m, d, h(S.lin2), S.lin2_b, compact ? nullptr : markers, nm, logits, stream);
     }
 
     // The per-step forward pass for (n, nm, qtype) as an executable graph (captured and
@@ -1268,7 +1289,8 @@ int julia_hip_run_trace(const Engine* ce, const uint32_t* ids, size_t n, const u
                 hip_check(hipStreamSynchronize(e.stream), "trace");
             }
         }
-        e.launch_head(xl, (int)n, (int)qtype, e.markers_d, (int)n_markers, e.logits_d);
+        e.launch_head(xl, (int)n, (int)qtype, e.markers_d, (int)n_markers, e.logits_d, nullptr,
+                      nullptr, head_x != nullptr);
         hip_check(hipStreamSynchronize(e.stream), "forward");
         if (layer_fused && e.layer_kernel.barrier_timed_out())
             throw std::runtime_error("layer: a grid barrier timed out (blocks not co-resident)");

@@ -131,6 +131,12 @@ void embed_launch(const uint32_t* ids, int n, const jh_half* table, int vocab, i
 void norm_add_launch(const jh_half* x, int n, int d, const float* gamma, const float* add,
                      float eps, jh_half* out, float* stats, hipStream_t stream,
                      const int32_t* row_type = nullptr);
+// Rows markers[i] (i < k) of a, and of b and the row statistics when given, into row i of
+// a_out (b_out, stats_out).
+void gather_rows_launch(const jh_half* a, const jh_half* b, const float* stats, int n, int d,
+                        const uint32_t* markers, int k, jh_half* a_out, jh_half* b_out,
+                        float* stats_out, hipStream_t stream);
+// logits[i] = y[markers[i]] . w + b for i < k; markers null: row i.
 void score_launch(const jh_half* y, int n, int d, const jh_half* w, float b,
                   const uint32_t* markers, int k, float* logits, hipStream_t stream);
 void stream_copy_launch(void* dst, const void* src, size_t bytes, hipStream_t stream);

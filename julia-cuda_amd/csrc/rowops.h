@@ -107,11 +107,12 @@ __device__ __forceinline__ void norm_add_row(const f16* x, int row, int d, const
     }
 }
 
-// logits[i] = y[markers[i]] . w + b (kernels/src/main.rs:180-200).
+// logits[i] = y[markers[i]] . w + b (kernels/src/main.rs:180-200); markers null: row i.
 template <int NC>
 __device__ __forceinline__ void score_row(const f16* y, int n, int d, const f16* w, float b,
                                           const uint32_t* markers, int i, float* logits, int lane) {
-    const uint32_t r = min(markers[i], (uint32_t)(n - 1));  // the host checks markers < n
+    // (the host checks markers < n)
+    const uint32_t r = markers ? min(markers[i], (uint32_t)(n - 1)) : (uint32_t)i;
     float v[NC][4], u[NC][4];
     load_row<NC>(y + (size_t)r * d, d, lane, v);
     load_row<NC>(w, d, lane, u);

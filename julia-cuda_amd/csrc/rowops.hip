@@ -27,6 +27,24 @@ __global__ __launch_bounds__(256) void norm_add_kernel(const f16* x, int n, int 
     norm_add_row<NC, false>(x, row, d, gamma, add, row_type, eps, out, stats, threadIdx.x & 63);
 }
 
+// Rows markers[i] of a (and of b, and of the statistics sa, when given) into row i of a_out
+// (b_out, sa_out): the marker rows, compacted for the head's last row-wise steps.
+__global__ __launch_bounds__(256) void gather_rows_kernel(const uint4* a, const uint4* b,
+                                                          const float2* sa, int n, int d,
+                                                          const uint32_t* markers, int k,
+                                                          uint4* a_out, uint4* b_out,
+                                                          float2* sa_out) {
+    const int i = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (i >= k) return;
+    const size_t r = min(markers[i], (uint32_t)(n - 1));  // the host checks markers < n
+    const int chunks = d / 8, groups = d / 64;
+    for (int c = lane; c < chunks; c += 64) {
+        a_out[(size_t)i * chunks + c] = a[r * chunks + c];
+        if (b) b_out[(size_t)i * chunks + c] = b[r * chunks + c];
+    }
+    if (sa && lane < groups) sa_out[(size_t)i * groups + lane] = sa[r * groups + lane];
+}
+
 template <int NC>
 __global__ __launch_bounds__(256) void score_kernel(const f16* y, int n, int d, const f16* w,
                                                     float b, const uint32_t* markers, int k,
@@ -105,11 +123,25 @@ void norm_add_launch(const jh_half* x, int n, int d, const float* gamma, const f
     check_launch("norm_add");
 }
 
+void gather_rows_launch(const jh_half* a, const jh_half* b, const float* stats, int n, int d,
+                        const uint32_t* markers, int k, jh_half* a_out, jh_half* b_out,
+                        float* stats_out, hipStream_t st) {
+    check_row("gather", n, d, a, a_out);
+    if (k <= 0) return;
+    if (!markers || (b && (!b_out || ((uintptr_t)b % 16) || ((uintptr_t)b_out % 16))) ||
+        (stats && (!stats_out || ((uintptr_t)stats % 8) || ((uintptr_t)stats_out % 8))))
+        throw std::runtime_error("gather: bad markers, rows or statistics");
+    hipLaunchKernelGGL(gather_rows_kernel, dim3((k + 3) / 4), dim3(256), 0, st, (const uint4*)a,
+                       (const uint4*)b, (const float2*)stats, n, d, markers, k, (uint4*)a_out,
+                       (uint4*)b_out, (float2*)stats_out);
+    check_launch("gather");
+}
+
 void score_launch(const jh_half* y, int n, int d, const jh_half* w, float b,
                   const uint32_t* markers, int k, float* logits, hipStream_t st) {
     check_row("score", n, d, y, w);
     if (k <= 0) return;  // no markers: nothing to score
-    if (!markers || !logits) throw std::runtime_error("score: null markers or logits");
+    if (!logits || (!markers && k > n)) throw std::runtime_error("score: null logits, or k > n rows");
     JH_ROW_DISPATCH(score_kernel, dim3((k + 3) / 4), st, (const f16*)y, n, d, (const f16*)w, b,
                     markers, k, logits);
     check_launch("score");
