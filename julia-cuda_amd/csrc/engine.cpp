@@ -395,6 +395,7 @@ Engine* load_engine(const char* dir, size_t max_length, size_t batch_rows = 0) {
     std::unique_ptr<Checkpoint> ck;
     if (Checkpoint::is_checkpoint(dir)) ck.reset(new Checkpoint(dir));
     const ModelConfig spec = ck ? ck->config() : parse_model_spec(dir);
+    if (batch_rows > (1u << 20)) throw std::runtime_error("batch_rows out of range");
     int count = 0;
     if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
         throw std::runtime_error("no HIP device is available");
@@ -415,7 +416,6 @@ Engine* load_engine(const char* dir, size_t max_length, size_t batch_rows = 0) {
     if (ml > (size_t)c.max_positions)
         throw std::runtime_error("max_length " + std::to_string(ml) + " is over the model's " +
                                  std::to_string(c.max_positions));
-    if (batch_rows > (1u << 20)) throw std::runtime_error("batch_rows out of range");
     e->max_length = (int)ml;
     e->rows = (int)std::max({ml, (size_t)c.batch_rows, batch_rows});
     HostWeights hw = ck ? prepare(c, ck->source()) : prepare_synthetic(c);

@@ -40,6 +40,9 @@ def test_load_without_a_gpu_or_model_is_an_error():
         jh.Engine("synthetic:d=100")
     with pytest.raises(jh.JuliaHipError, match="batch_rows"):
         jh.Engine("synthetic:batch_rows=-1")
+    # julia_hip_load's own batch_rows, checked before any device work
+    with pytest.raises(jh.JuliaHipError, match="batch_rows out of range"):
+        jh.Engine("synthetic", batch_rows=(1 << 20) + 1)
     if jh.device_count() == 0:
         with pytest.raises(jh.JuliaHipError, match="no HIP device"):
             jh.Engine("synthetic:layers=1")
