@@ -301,14 +301,16 @@ struct Engine {
     // scored, so unless all_rows (or the markers are not fewer than the rows) those steps run on
     // the marker rows alone, gathered into rows 0 .. nm - 1 of spare buffers: the same values
     // for those rows (up to the GEMM tiles' summation order, which depends on the row count).
+    // Without markers (and without all_rows) the head is not run at all.
     void launch_head(const jh_half* xin, int n, int qtype, const uint32_t* markers, int nm,
                      float* logits, const int32_t* seg = nullptr,
                      const int32_t* row_type = nullptr, bool all_rows = false) {
+        if (nm <= 0 && !all_rows) return;  // no marker: nothing the head computes is read
         const int d = cfg.d, F = cfg.head_ff;
         const float* add = f(layout.type_emb) + (row_type ? 0 : (size_t)qtype * d);
         norm_add_launch(xin, n, d, f(layout.final_norm), add, cfg.norm_eps, hx, stats_a, stream,
                         row_type);
-        const bool compact = !all_rows && nm > 0 && nm < n;
+        const bool compact = !all_rows && nm < n;
         // The marker rows' residual stream: x is free once norm_add has read the encoder's
         // output; their attention output goes to qkv (free once attention has read it).
         jh_half* hr = hx;
