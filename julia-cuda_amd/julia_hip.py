@@ -195,6 +195,7 @@ class Engine:
     def __init__(self, spec="synthetic", max_length=0, batch_rows=0):
         """batch_rows: room for that many concatenated rows (julia_hip_load), for run_batched."""
         e = _err()
+        self._free = lib().julia_cuda_free  # (held: module globals go at shutdown)
         if batch_rows:
             self.ptr = lib().julia_hip_load(spec.encode(), max_length, batch_rows, e, ERR_LEN)
         else:
@@ -204,7 +205,7 @@ class Engine:
 
     def close(self):
         if getattr(self, "ptr", None):
-            lib().julia_cuda_free(self.ptr)
+            self._free(self.ptr)
             self.ptr = None
 
     __del__ = close
@@ -345,13 +346,14 @@ class Scratch:
 
     def __init__(self, ws_floats=1 << 22, counters=1 << 16):
         e = _err()
+        self._free = lib().julia_hip_scratch_free  # (held: module globals go at shutdown)
         self.ptr = lib().julia_hip_scratch_new(ws_floats, counters, e, ERR_LEN)
         if not self.ptr:
             raise JuliaHipError(e.value.decode(errors="replace"))
 
     def close(self):
         if getattr(self, "ptr", None):
-            lib().julia_hip_scratch_free(self.ptr)
+            self._free(self.ptr)
             self.ptr = None
 
     __del__ = close
