@@ -273,6 +273,27 @@ def test_whole_model_on_256_tiles(torch_cuda):
     e.close()
 
 
+def test_fused_fallback_when_the_head_does_not_fit(torch_cuda):
+    """A head the 256 x 256 instance cannot take (head_ff 1152, not a multiple of 256): the
+    layer_fused pass falls back to the encoder kernel and the head's own launches, and still
+    matches the per-step kernels."""
+    c = dict(d=768, layers=2, inter=1152, vocab=1000, head_ff=1152, max_positions=4096, seed=13)
+    e = jh.Engine(spec(c), max_length=1024, batch_rows=2600)
+    rng = np.random.default_rng(37)
+    lens = [1024, 700, 513, 300]
+    reqs = [(rng.integers(0, c["vocab"], n).astype(np.uint32),
+             rng.integers(0, n, 3).astype(np.uint32), i % 3) for i, n in enumerate(lens)]
+    plan, _ = e.profile_layer(sum(lens), 0)
+    assert list(plan[:4]) == [256, 256, 256, 256], plan
+    assert not e.model_kernel(sum(lens)) and e.model_kernel(300)
+    lf, _ = e.run(reqs, layer_fused=True, batched=True)
+    ls, _ = e.run(reqs, batched=True)
+    a, b = np.concatenate(lf), np.concatenate(ls)
+    say(f"fallback: max |d| to per-step {np.abs(a - b).max():.2e}")
+    assert np.isfinite(a).all() and np.abs(a - b).max() <= 1e-2
+    e.close()
+
+
 def test_load_errors(torch_cuda):
     with pytest.raises(jh.JuliaHipError, match="max_length"):
         jh.Engine(spec(dict(SMALL, max_positions=512)), max_length=600)
