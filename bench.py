@@ -40,9 +40,10 @@ def log(*a):
 
 
 def percentile(xs, p):
-    """src/serve.rs:85: the value at index round((len - 1) p) of the sorted values."""
+    """src/serve.rs:85: the value at index round((len - 1) p) of the sorted values (Rust's
+    round: halves away from zero)."""
     s = sorted(xs)
-    return s[int(round((len(s) - 1) * p))]
+    return s[int(np.floor((len(s) - 1) * p + 0.5))]
 
 
 def request(rng, n, nm=6):
@@ -155,6 +156,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="forward timing only")
+    ap.add_argument("--path", choices=("both", "per-step", "fused"), default="both",
+                    help="with --quick: time only this path of the forward pass")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -162,26 +165,25 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    import torch
-
-    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    # No torch in this process: the library's own HIP runtime (the ROCm it was built with) runs
+    # everything, and the device buffers of the sweeps come from it too.
+    assert jh.device_count() > 0, "bench.py needs a GPU"
     rng = np.random.default_rng(293)
     eng = jh.Engine("synthetic", max_length=1024)
     info = eng.info()
     log(f"device {eng.device()}, {info.cus} CUs; weights {info.weight_bytes_f16 / 1e6:.1f} MB f16")
     req = request(rng, 293)
 
-    def timed(fused):
+    def timed(fused):  # julia_cuda_run returns after its stream has finished
         eng.run([req] * args.warmup, layer_fused=fused)
-        torch.cuda.synchronize()
         t0 = time.perf_counter()
         _, ms = eng.run([req] * args.steps, layer_fused=fused)
-        torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) * 1e3 / args.steps
         return float(np.mean(ms)), float(np.median(ms)), wall
 
-    per_step = timed(False)
-    fused = timed(True)
+    skip = (float("inf"),) * 3
+    per_step = timed(False) if args.path != "fused" else skip
+    fused = timed(True) if args.path != "per-step" else skip
     log(f"293 tokens: per-step kernels {per_step[0]:.3f} ms GPU ({per_step[2]:.3f} wall), "
         f"layer kernel {fused[0]:.3f} ms GPU ({fused[2]:.3f} wall)")
     best_fused = fused[0] < per_step[0]
@@ -212,6 +214,7 @@ def main():
                             "wall": round(fused[2], 4)},
     }
     if args.quick:
+        eng.close()
         print(json.dumps(out), flush=True)
         return
 
@@ -221,7 +224,7 @@ def main():
         mn, md = eng.time_step(step, 293)
         kern[step] = dict(us=round(md, 3), us_min=round(mn, 3), per_forward=cnt,
                           bytes=gemm_bytes(293, n, k, epi), flops=2 * 293 * n * k,
-                          config=list(jh.gemm_choose(293, n, k, info.cus)))
+                          config=list(jh.gemm_choose(293, n, k, info.cus, epi)))
     for step, window in (("attention_global", 0), ("attention", None)):
         mn, md = eng.time_step(step, 293)
         kern[step] = dict(us=round(md, 3), us_min=round(mn, 3),
@@ -276,18 +279,20 @@ def main():
     c2 = {}
     scr = jh.Scratch(1 << 24, 1 << 16)
     M2 = 512
+    r2 = np.random.default_rng(2)
+    dev = jh.DeviceBuffer.of
     for step in ("wo", "wi", "wo_mlp"):
         n, k, epi, _ = STEP_SHAPES[step]
         nout = n // 2 if epi == "lngeglu" else n
-        a = torch.randn(M2, k, device="cuda").half()
-        w = (torch.randn(n * k, device="cuda") * 0.02).half()
-        c = torch.randn(M2, nout, device="cuda").half()
-        st_in = torch.ones(M2, k // 64, 2, device="cuda")
-        cs = torch.zeros(n, device="cuda")
-        st_out = torch.zeros(M2, n // 64, 2, device="cuda")
-        kw = dict(stats_in=st_in.data_ptr(), colsum=cs.data_ptr()) if epi == "lngeglu" else \
-            dict(stats_out=st_out.data_ptr())
-        gargs = jh.gemm_args(epi, a.data_ptr(), w.data_ptr(), c.data_ptr(), M2, n, k, **kw)
+        a = dev(r2.standard_normal((M2, k)).astype(np.float16))
+        w = dev((r2.standard_normal(n * k) * 0.02).astype(np.float16))
+        c = dev(r2.standard_normal((M2, nout)).astype(np.float16))
+        st_in = dev(np.ones((M2, k // 64, 2), np.float32))
+        cs = dev(np.zeros(n, np.float32))
+        st_out = dev(np.zeros((M2, n // 64, 2), np.float32))
+        kw = dict(stats_in=st_in.ptr, colsum=cs.ptr) if epi == "lngeglu" else \
+            dict(stats_out=st_out.ptr)
+        gargs = jh.gemm_args(epi, a.ptr, w.ptr, c.ptr, M2, n, k, **kw)
         grid = {}
         for bm in (32, 64, 128):
             for sp in (1, 2, 4):
@@ -299,8 +304,10 @@ def main():
                     grid[f"{bm}/{sp}"] = None
         _, md = jh.time_gemm(gargs, scratch=scr, warmup=5, batches=5, per_batch=20)
         c2[step] = {"epilogue": epi, "us_by_bm_split": grid,
-                    "chosen": list(jh.gemm_choose(M2, n, k, info.cus)), "chosen_us": round(md, 2),
+                    "chosen": list(jh.gemm_choose(M2, n, k, info.cus, epi)), "chosen_us": round(md, 2),
                     "TFLOPs": round(2 * M2 * n * k / (md * 1e-6) / 1e12, 1)}
+        for b in (a, w, c, st_in, cs, st_out):
+            b.close()
     scr.close()
     out["config2_512"] = c2
     log("config 2:", json.dumps(c2))
@@ -308,14 +315,16 @@ def main():
     # ---- config 3: attention alone, global and +-64 window ----
     c3 = {}
     for n_att in (72, 293, 1024):
-        q = (torch.randn(n_att, 3 * D, device="cuda")).half()
-        o = torch.empty(n_att, D, dtype=torch.float16, device="cuda")
+        q = dev(r2.standard_normal((n_att, 3 * D)).astype(np.float16))
+        o = jh.DeviceBuffer(n_att * D * 2)
         for window in (0, 64):
-            _, md = jh.time_attention(q.data_ptr(), o.data_ptr(), n_att, D, window, 1,
+            _, md = jh.time_attention(q.ptr, o.ptr, n_att, D, window, 1,
                                       warmup=10, batches=5, per_batch=40)
             fl = attention_flops(n_att, window)
             c3[f"n{n_att}_{'global' if window == 0 else 'window64'}"] = {
                 "us": round(md, 2), "TFLOPs": round(fl / (md * 1e-6) / 1e12, 1)}
+        q.close()
+        o.close()
     out["config3_attention"] = c3
     log("config 3:", json.dumps(c3))
 
@@ -328,7 +337,7 @@ def main():
             fl = 2 * m * n * k
             big[f"{step}@{m}"] = dict(us=round(md, 2), TFLOPs=round(fl / (md * 1e-6) / 1e12, 1),
                                       frac_peak=round(fl / (md * 1e-6) / PEAK_F16, 4),
-                                      config=list(jh.gemm_choose(m, n, k, info.cus)))
+                                      config=list(jh.gemm_choose(m, n, k, info.cus, epi)))
     tot_fl = sum(2 * 18752 * n * k for (n, k, _, _) in STEP_SHAPES.values())
     tot_us = sum(big[f"{s}@18752"]["us"] for s in STEP_SHAPES)
     out["fused_gemm_tflops"] = round(tot_fl / (tot_us * 1e-6) / 1e12, 1)
@@ -369,6 +378,7 @@ def main():
         import oracle as O
 
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        nproc = len(os.sched_getaffinity(0))
         model = O.Model(O.cfg())
         ids, markers, q = req
         model.forward(ids, q, markers)  # warm-up
@@ -379,10 +389,12 @@ def main():
             model.forward(ids, q, markers)
             times.append((time.perf_counter() - t0) * 1e3)
         out["cpu_baseline"] = {"value": round(float(np.median(times)), 2), "unit": "ms/request",
-                               "cores": threads, "kind": "port",
+                               "cores": threads, "nproc": nproc, "kind": "port",
                                "sample": f"{len(times)} forward passes of the same 293-token "
                                          "request (22-layer encoder + head, f32, LayerNorms in "
-                                         "f64), median; weight generation excluded"}
+                                         f"f64), median, OpenMP over {threads} threads "
+                                         f"(OMP_NUM_THREADS) of {nproc} host CPUs this process "
+                                         "may run on; weight generation excluded"}
     print(json.dumps(out), flush=True)
 
 

@@ -188,9 +188,13 @@ int julia_hip_time_attention(const void *qkv, void *o, int n, int d, int window,
 int julia_hip_time_copy(size_t bytes, int warmup, int batches, int per_batch, float *min_us,
                         float *median_us, char *err, size_t err_len);
 
-/* hipMemcpy helpers for callers without a HIP binding (tests). */
+/* hipMemcpy / hipMalloc helpers for callers without a HIP binding of their own (tests and the
+ * benchmark, which then run on this library's HIP runtime alone). */
 int julia_hip_copy(void *dst, const void *src, size_t bytes, int kind, char *err, size_t err_len);
 int julia_hip_device_count(void);
+void *julia_hip_device_alloc(size_t bytes, char *err, size_t err_len);
+void julia_hip_device_free(void *p);
+int julia_hip_device_sync(char *err, size_t err_len);
 
 /* ================= Part 3: host-side logic ============================================== */
 
@@ -219,14 +223,31 @@ void julia_hip_synth(uint64_t seed, uint32_t id, uint64_t start, uint64_t count,
 /* f32 -> f16 bits, round to nearest even. */
 void julia_hip_round_f16(const float *in, uint16_t *out, size_t n);
 
-/* This library's tile and split-K chooser for a 256-CU GPU (replaces src/gemm.rs:153-163). */
-julia_hip_gemm_config julia_hip_gemm_choose(int m, int n, int k, int cus);
+/* This library's tile and split-K chooser for a 256-CU GPU (replaces src/gemm.rs:153-163);
+ * epi: the epilogue flags (the throughput tiles take LayerNorm epilogues up to k = 1024). */
+julia_hip_gemm_config julia_hip_gemm_choose(int m, int n, int k, int cus, int epi);
+/* The launcher's precondition checks alone (src/gemm.rs:262-329), on the host: 0, or -1 and the
+ * reason. The pointers are checked for null and alignment only; the scratch is described by its
+ * sizes. */
+int julia_hip_gemm_check(const julia_hip_gemm_args *g, julia_hip_gemm_config cfg,
+                         size_t ws_floats, size_t counters, char *err, size_t err_len);
 /* The reference's layer-kernel plan for a 2080 Ti, kept for provenance and tested against its
  * golden picks: src/forward.rs:759-806 (gemm_plan, phase_cost). */
 void julia_hip_gemm_plan_2080ti(int n, int cols, int k, int sms, int per_sm, int *bm,
                                 int *splits);
 /* The reference's per-step rule, src/gemm.rs:153-172 (choose, splits). */
 julia_hip_gemm_config julia_hip_gemm_choose_2080ti(int m, int n, int k, int sms);
+
+/* julia-rs `head::answer` (src/serve.rs:58), as the reference's tools/torch_baseline.py:214-226
+ * states it for results tools/score.py compares: probabilities[i] = softmax(logits)[i] (f64);
+ * value = the most probable option's index (qtype 0, choice; the first of equal ones), the
+ * expected index sum_i i p_i (1, score) or p[1] (2, noul: the "true" option; n >= 2).
+ * Returns 0, or -1 and the reason. */
+int julia_hip_answer(uint32_t qtype, const float *logits, size_t n, double *probabilities,
+                     double *value, char *err, size_t err_len);
+/* src/serve.rs:78-115 `report`'s figures over n > 0 values: out[5] = mean, then the values at
+ * index round((n - 1) p) (half away from zero) of the sorted values for p = 0.5, 0.9, 0.99, 1. */
+int julia_hip_latency_summary(const double *v, size_t n, double *out);
 
 /* Engine introspection (tests, bench). */
 typedef struct {

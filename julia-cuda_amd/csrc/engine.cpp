@@ -149,7 +149,7 @@ struct Engine {
         g.epi = epi, g.a = a, g.w = w, g.c = c, g.m = m, g.n = n, g.k = k;
         g.stats_in = stats_in, g.colsum = colsum, g.eps = eps, g.bias = bias;
         g.rope = rope, g.pos = pos, g.rope_rows = cfg.max_positions, g.stats_out = stats_out;
-        gemm_launch(g, gemm_choose(m, n, k, cus), scratch, stream);
+        gemm_launch(g, gemm_choose(m, n, k, cus, epi), scratch, stream);
     }
 
     // Layer l's five steps as five launches (src/forward.rs:105-165, 361-424): qkv (RoPE; the
@@ -459,11 +459,12 @@ Engine* load_engine(const char* dir, size_t max_length, size_t batch_rows = 0) {
 
     // Scratch for the largest split-K / key-range partials any request up to max_length needs.
     size_t ws = 0, counters = 0;
-    const int shapes[][2] = {{3 * (int)d, (int)d}, {(int)d, (int)d},  {2 * c.inter, (int)d},
-                             {(int)d, c.inter},     {c.head_ff, (int)d}, {(int)d, c.head_ff}};
+    const int shapes[][3] = {{3 * (int)d, (int)d, EPI_LN}, {(int)d, (int)d, 0},
+                             {2 * c.inter, (int)d, EPI_LN}, {(int)d, c.inter, 0},
+                             {c.head_ff, (int)d, EPI_LN},   {(int)d, c.head_ff, 0}};
     for (int m = 1; m <= (int)n; m++) {
         for (auto& s : shapes) {
-            const GemmConfig cfg = gemm_choose(m, s[0], s[1], e->cus);
+            const GemmConfig cfg = gemm_choose(m, s[0], s[1], e->cus, s[2]);
             ws = std::max(ws, gemm_ws_floats(m, s[0], cfg));
             counters = std::max(counters, gemm_counters(m, s[0], cfg));
         }
@@ -535,15 +536,17 @@ void check_request(const Engine& e, const Request& r, size_t i) {
 }
 
 // src/engine.rs:170-196 `Engine::run`: chunks of QUEUE requests, queued back to back (copy in,
-// start event, forward, end event, logits out), then one wait per chunk.
+// start event, forward, end event, logits out), then one wait per chunk. Every request is
+// checked before the first runs (src/capi.rs:150-170), so a bad one runs nothing.
 void run_requests(Engine& e, const std::vector<Request>& reqs, bool fused, float* logits_out,
                   float* gpu_ms) {
     hip_check(hipSetDevice(e.device), "hipSetDevice");
+    for (size_t i = 0; i < reqs.size(); i++) check_request(e, reqs[i], i);
     size_t out_at = 0;
     for (size_t c0 = 0; c0 < reqs.size(); c0 += QUEUE) {
         const size_t c1 = std::min(reqs.size(), c0 + QUEUE);
         size_t chunk_markers = 0;
-        for (size_t i = c0; i < c1; i++) check_request(e, reqs[i], i), chunk_markers += reqs[i].nm;
+        for (size_t i = c0; i < c1; i++) chunk_markers += reqs[i].nm;
         e.ensure_markers(chunk_markers);  // the stream is idle here
         for (size_t i = c0, m0 = 0; i < c1; m0 += reqs[i].nm, i++) {
             const Request& r = reqs[i];
@@ -806,7 +809,7 @@ int julia_hip_gemm(const julia_hip_gemm_args* g, julia_hip_gemm_config cfg,
     return guarded(err, err_len, [&] {
         const Gemm x = to_gemm(g);
         GemmConfig c{cfg.bm, cfg.splits};
-        if (c.bm == 0) c = gemm_choose(x.m, x.n, x.k, device_cus());
+        if (c.bm == 0) c = gemm_choose(x.m, x.n, x.k, device_cus(), x.epi);
         gemm_launch(x, c, scratch_of(s), (hipStream_t)stream);
     });
 }
@@ -862,7 +865,7 @@ int julia_hip_time_gemm(const julia_hip_gemm_args* g, julia_hip_gemm_config cfg,
     return guarded(err, err_len, [&] {
         const Gemm x = to_gemm(g);
         GemmConfig c{cfg.bm, cfg.splits};
-        if (c.bm == 0) c = gemm_choose(x.m, x.n, x.k, device_cus());
+        if (c.bm == 0) c = gemm_choose(x.m, x.n, x.k, device_cus(), x.epi);
         const Scratch sc = scratch_of(s);
         gemm_check(x, c, sc);
         hipStream_t st = nullptr;
@@ -940,6 +943,20 @@ int julia_hip_device_count(void) {
     return n;
 }
 
+void* julia_hip_device_alloc(size_t bytes, char* err, size_t err_len) {
+    void* p = nullptr;
+    guarded(err, err_len, [&] { p = dalloc<uint8_t>(bytes, "julia_hip_device_alloc"); });
+    return p;
+}
+
+void julia_hip_device_free(void* p) {
+    if (p) hipFree(p);
+}
+
+int julia_hip_device_sync(char* err, size_t err_len) {
+    return guarded(err, err_len, [&] { hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize"); });
+}
+
 // ---------------------------------------------------------------- Part 3: host-side logic
 void julia_hip_prep_fold_layernorm(const float* w, const float* gamma, int out, int k,
                                    uint16_t* w16, float* colsum) {
@@ -975,9 +992,21 @@ void julia_hip_round_f16(const float* in, uint16_t* out, size_t n) {
     for (size_t i = 0; i < n; i++) out[i] = f32_to_f16(in[i]);
 }
 
-julia_hip_gemm_config julia_hip_gemm_choose(int m, int n, int k, int cus) {
-    const GemmConfig c = gemm_choose(m, n, k, cus);
+julia_hip_gemm_config julia_hip_gemm_choose(int m, int n, int k, int cus, int epi) {
+    const GemmConfig c = gemm_choose(m, n, k, cus, epi);
     return julia_hip_gemm_config{c.bm, c.splits};
+}
+
+int julia_hip_gemm_check(const julia_hip_gemm_args* g, julia_hip_gemm_config cfg,
+                         size_t ws_floats, size_t counters, char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        // Stand-in scratch of the stated sizes: the check reads only the sizes and non-null.
+        static float ws_probe;
+        static uint32_t counter_probe;
+        const Scratch s{ws_floats ? &ws_probe : nullptr, ws_floats,
+                        counters ? &counter_probe : nullptr, counters};
+        gemm_check(to_gemm(g), GemmConfig{cfg.bm, cfg.splits}, s);
+    });
 }
 
 // src/forward.rs:771-806 `phase_cost`, the 2080 Ti latency model: a task costs 5 us (10 with
@@ -1123,8 +1152,8 @@ int julia_hip_time_encoder_step(const Engine* ce, int step, int m, int bm, int s
         e.launch_layer(0, m);
         hip_check(hipStreamSynchronize(e.stream), "time");
         int l = 0;
-        auto gemm_cfg = [&](int n, int k) {
-            return bm > 0 ? GemmConfig{bm, splits} : gemm_choose(m, n, k, e.cus);
+        auto gemm_cfg = [&](int n, int k, int epi) {
+            return bm > 0 ? GemmConfig{bm, splits} : gemm_choose(m, n, k, e.cus, epi);
         };
         // Rotate through the layers' weights, as the reference's --time does (src/main.rs:
         // 307-312), so the weights are not the last call's, still in L2. Layer 0 has no
@@ -1161,7 +1190,7 @@ int julia_hip_time_encoder_step(const Engine* ce, int step, int m, int bm, int s
                     return;
                 }
             }
-            gemm_launch(g, gemm_cfg(g.n, g.k), e.scratch, e.stream);
+            gemm_launch(g, gemm_cfg(g.n, g.k, g.epi), e.scratch, e.stream);
         };
         time_calls(launch, warmup, batches, per_batch, e.stream, min_us, median_us);
     });

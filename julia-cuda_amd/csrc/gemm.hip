@@ -229,7 +229,8 @@ void gemm_launch(const Gemm& g, GemmConfig cfg, const Scratch& s, hipStream_t st
 // Measured winners: 48-row latency tiles for qkv and wi at 293 tokens, 16-row for wo and
 // wo_mlp, 32-row at 2048 for wo and wo_mlp; 128 x 128 for qkv at 2048 and 8192; 256 x 256
 // for qkv at 4096 and everything at 18752.
-GemmConfig gemm_choose(int m, int n, int k, int cus) {
+GemmConfig gemm_choose(int m, int n, int k, int cus, int epi) {
+    static_assert(GEMM_BIG_LN_MAX_K == 128 * BIG_LN_SLOTS, "the LayerNorm limit of the throughput tiles");
     if (cus <= 0) cus = 256;
     GemmConfig best{32, 1};
     double best_cost = 1e30;
@@ -239,7 +240,7 @@ GemmConfig gemm_choose(int m, int n, int k, int cus) {
         const double cost = 4.0 + (double)per_cu * (bm + 64) * k * 2 / 55e3;
         if (cost < best_cost - 0.05) best_cost = cost, best = GemmConfig{bm, 1};
     }
-    if (m >= 1024 && n % 128 == 0 && k % 64 == 0) {
+    if (m >= 1024 && n % 128 == 0 && k % 64 == 0 && !((epi & EPI_LN) && k > GEMM_BIG_LN_MAX_K)) {
         const double ks = (double)k / 768.0;
         const long l128 = ((long)(n / 128) * ((m + 127) / 128) + cus - 1) / cus;
         const double c128 = 2.0 + 12.0 * ks * (1.5 * (double)(l128 / 2) + (double)(l128 % 2));

@@ -110,8 +110,10 @@ struct Gemm {
 // Throws std::runtime_error when g or cfg break what the kernels assume.
 void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s);
 void gemm_launch(const Gemm& g, GemmConfig cfg, const Scratch& s, hipStream_t stream);
-// The tile height and split-K for an m x n x k GEMM on `cus` compute units.
-GemmConfig gemm_choose(int m, int n, int k, int cus);
+// The tile height and split-K for an m x n x k GEMM with epilogue `epi` on `cus` compute units
+// (the throughput tiles only where they take the epilogue: LayerNorm up to k = GEMM_BIG_LN_MAX_K).
+GemmConfig gemm_choose(int m, int n, int k, int cus, int epi = 0);
+constexpr int GEMM_BIG_LN_MAX_K = 1024;
 size_t gemm_ws_floats(int m, int n, GemmConfig cfg);
 size_t gemm_counters(int m, int n, GemmConfig cfg);
 

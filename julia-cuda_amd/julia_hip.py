@@ -11,6 +11,7 @@ The library must be built (`make -C julia-cuda_amd`); there is no fallback.
 
 import ctypes
 import os
+import sys
 
 import numpy as np
 
@@ -82,20 +83,23 @@ EXPORTS = [
     "julia_hip_attention_seg",
     "julia_hip_embed", "julia_hip_norm_add", "julia_hip_score", "julia_hip_time_gemm",
     "julia_hip_time_attention", "julia_hip_time_copy", "julia_hip_copy", "julia_hip_device_count",
+    "julia_hip_device_alloc", "julia_hip_device_free", "julia_hip_device_sync",
     "julia_hip_prep_fold_layernorm", "julia_hip_prep_fold_layernorm_bias",
     "julia_hip_prep_geglu_rows", "julia_hip_prep_pack_frag", "julia_hip_prep_unpack_frag",
     "julia_hip_prep_rope_table", "julia_hip_synth",
-    "julia_hip_round_f16", "julia_hip_gemm_choose", "julia_hip_gemm_plan_2080ti",
+    "julia_hip_round_f16", "julia_hip_gemm_choose", "julia_hip_gemm_check", "julia_hip_gemm_plan_2080ti",
     "julia_hip_gemm_choose_2080ti", "julia_hip_engine_info_get", "julia_hip_engine_tensor",
     "julia_hip_time_encoder_step", "julia_hip_profile_layer", "julia_hip_run_trace",
     "julia_hip_encode_batch",
-    "julia_hip_encode_batch_phases", "julia_hip_checkpoint_config",
+    "julia_hip_encode_batch_phases", "julia_hip_checkpoint_config", "julia_hip_answer",
+    "julia_hip_latency_summary",
 ]
 
 _VP, _SZ, _I, _F, _CP = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float, ctypes.c_char_p
 _F32P = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _U16P = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
 _I32P = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_F64P = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
 
 
 def lib():
@@ -130,6 +134,9 @@ def lib():
                                      _CP, _SZ]),
         "julia_hip_copy": (_I, [_VP, _VP, _SZ, _I, _CP, _SZ]),
         "julia_hip_device_count": (_I, []),
+        "julia_hip_device_alloc": (_VP, [_SZ, _CP, _SZ]),
+        "julia_hip_device_free": (None, [_VP]),
+        "julia_hip_device_sync": (_I, [_CP, _SZ]),
         "julia_hip_prep_fold_layernorm": (None, [_F32P, _F32P, _I, _I, _U16P, _F32P]),
         "julia_hip_prep_fold_layernorm_bias": (None, [_F32P, _F32P, _F32P, _F32P, _I, _I, _U16P,
                                                       _F32P, _F32P]),
@@ -140,7 +147,11 @@ def lib():
         "julia_hip_synth": (None, [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint64,
                                    ctypes.c_uint64, ctypes.c_double, ctypes.c_double, _F32P]),
         "julia_hip_round_f16": (None, [_F32P, _U16P, _SZ]),
-        "julia_hip_gemm_choose": (GemmConfig, [_I, _I, _I, _I]),
+        "julia_hip_answer": (_I, [ctypes.c_uint32, _F32P, _SZ, _F64P, ctypes.POINTER(ctypes.c_double),
+                                  _CP, _SZ]),
+        "julia_hip_latency_summary": (_I, [_F64P, _SZ, _F64P]),
+        "julia_hip_gemm_choose": (GemmConfig, [_I, _I, _I, _I, _I]),
+        "julia_hip_gemm_check": (_I, [ctypes.POINTER(GemmArgs), GemmConfig, _SZ, _SZ, _CP, _SZ]),
         "julia_hip_gemm_plan_2080ti": (None, [_I, _I, _I, _I, _I, ctypes.POINTER(_I),
                                               ctypes.POINTER(_I)]),
         "julia_hip_gemm_choose_2080ti": (GemmConfig, [_I, _I, _I, _I]),
@@ -180,6 +191,16 @@ def _np_ptr(a):
     return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
 
 
+def _finalize(obj):
+    """Garbage-collected objects free their device memory, except at interpreter shutdown: then
+    the HIP runtime may already be torn down, so no device call is made (the process's memory
+    goes with it). Callers close() what they own before exiting."""
+    if sys.is_finalizing():
+        obj.ptr = None
+    else:
+        obj.close()
+
+
 def tier():
     return lib().julia_cuda_tier().decode()
 
@@ -208,7 +229,8 @@ class Engine:
             self._free(self.ptr)
             self.ptr = None
 
-    __del__ = close
+    def __del__(self):
+        _finalize(self)
 
     def __enter__(self):
         return self
@@ -340,6 +362,44 @@ def copy(dst, src, nbytes, kind=4):
     _call(lib().julia_hip_copy, dst, src, nbytes, kind)
 
 
+def sync():
+    _call(lib().julia_hip_device_sync)
+
+
+class DeviceBuffer:
+    """Device memory from this library's own HIP runtime (julia_hip_device_alloc): for callers
+    that do not bring a HIP binding (bench.py). `ptr` is the device address."""
+
+    def __init__(self, nbytes):
+        e = _err()
+        self._free = lib().julia_hip_device_free  # (held: module globals go at shutdown)
+        self.nbytes = int(nbytes)
+        self.ptr = lib().julia_hip_device_alloc(self.nbytes, e, ERR_LEN)
+        if not self.ptr:
+            raise JuliaHipError(e.value.decode(errors="replace"))
+
+    @classmethod
+    def of(cls, a):
+        """A buffer holding a copy of the numpy array a."""
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        copy(b.ptr, _np_ptr(a).value, a.nbytes, kind=1)
+        return b
+
+    def to_host(self, dtype, shape):
+        out = np.empty(shape, dtype)
+        copy(_np_ptr(out).value, self.ptr, out.nbytes, kind=2)
+        return out
+
+    def close(self):
+        if getattr(self, "ptr", None):
+            self._free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        _finalize(self)
+
+
 # ---------------------------------------------------------------- Part 2: per-op surface
 class Scratch:
     """Split-K / key-range partials and arrival counters (src/gemm.rs `Scratch`)."""
@@ -356,7 +416,8 @@ class Scratch:
             self._free(self.ptr)
             self.ptr = None
 
-    __del__ = close
+    def __del__(self):
+        _finalize(self)
 
 
 def gemm_args(epi, a, w, c, m, n, k, stats_in=0, colsum=0, eps=1e-5, bias=0, rope=0, positions=0,
@@ -485,9 +546,17 @@ def round_f16(x):
     return out
 
 
-def gemm_choose(m, n, k, cus=256):
-    c = lib().julia_hip_gemm_choose(m, n, k, cus)
+def gemm_choose(m, n, k, cus=256, epi=0):
+    if isinstance(epi, str):
+        epi = EPI[epi]
+    c = lib().julia_hip_gemm_choose(m, n, k, cus, epi)
     return c.bm, c.splits
+
+
+def gemm_check(args, bm, splits=1, ws_floats=0, counters=0):
+    """The launcher's precondition checks on the host (no device): raises JuliaHipError."""
+    _call(lib().julia_hip_gemm_check, ctypes.byref(args), GemmConfig(bm, splits), ws_floats,
+          counters)
 
 
 def gemm_plan_2080ti(n, cols, k, sms=68, per_sm=2):
@@ -499,3 +568,28 @@ def gemm_plan_2080ti(n, cols, k, sms=68, per_sm=2):
 def gemm_choose_2080ti(m, n, k, sms=68):
     c = lib().julia_hip_gemm_choose_2080ti(m, n, k, sms)
     return c.bm, c.splits
+
+
+QTYPES = ("choice", "score", "noul")
+SERVE_PATH = os.path.join(_HERE, "lib", "julia-serve")
+
+
+def answer(qtype, logits):
+    """julia-rs head::answer (julia_hip_answer): (value, probabilities); value is the chosen
+    index (choice), the expected index (score) or p[1] (noul)."""
+    if isinstance(qtype, str):
+        qtype = QTYPES.index(qtype)
+    lg = np.ascontiguousarray(logits, np.float32)
+    p = np.zeros(max(len(lg), 1), np.float64)
+    v = ctypes.c_double()
+    _call(lib().julia_hip_answer, qtype, lg, len(lg), p, ctypes.byref(v))
+    return (int(v.value) if qtype == 0 else v.value), p[: len(lg)]
+
+
+def latency_summary(values):
+    """src/serve.rs:78-115 report's (mean, p50, p90, p99, max)."""
+    v = np.ascontiguousarray(values, np.float64)
+    out = np.zeros(5, np.float64)
+    if lib().julia_hip_latency_summary(v, len(v), out):
+        raise JuliaHipError("latency_summary: no values")
+    return tuple(float(x) for x in out)

@@ -56,15 +56,20 @@ def tensors(c, seed, enc=""):
     return out
 
 
-def write(path, c, seed, dtype=np.float32, enc="", config_extra=None, drop=(), reshape=None):
-    """Writes the synthetic model (seed) of config c as a checkpoint directory at path."""
+def write(path, c, seed, dtype=np.float32, enc="", config_extra=None, drop=(), reshape=None,
+          gen=None):
+    """Writes the synthetic model (seed) of config c as a checkpoint directory at path.
+    gen(tid, shape, mean, std) -> f32 array: the tensors from another generator instead."""
     os.makedirs(os.path.join(path, "encoder"), exist_ok=True)
     arrays = {}
     for name, (tid, shape) in tensors(c, seed, enc).items():
         if name in drop:
             continue
         mean, std = O.dist(tid)
-        v = jh.synth(seed, tid, int(np.prod(shape)), mean, std).reshape(shape)
+        if gen is None:
+            v = jh.synth(seed, tid, int(np.prod(shape)), mean, std).reshape(shape)
+        else:
+            v = np.asarray(gen(tid, shape, mean, std), np.float32).reshape(shape)
         if reshape and name in reshape:
             v = v.reshape(reshape[name])
         if dtype == "bf16":  # round to nearest even into the top 16 bits

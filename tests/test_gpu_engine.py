@@ -192,6 +192,33 @@ def test_run_errors(small):
     assert np.isfinite(out[0]).all()
 
 
+@pytest.mark.parametrize("batched", [False, True])
+def test_bad_request_past_the_first_queue_runs_nothing(small, batched):
+    """src/capi.rs:150-170 checks every sequence before Engine::run: a bad request at index 16
+    (past the first queue of 16) fails the call before any request has run, so the logits and
+    times of the good requests before it are left as they were."""
+    import ctypes
+    e, _ = small
+    rng = np.random.default_rng(16)
+    reqs = [(rng.integers(0, SMALL["vocab"], 20).astype(np.uint32), np.array([1, 5], np.uint32), 0)
+            for _ in range(20)]
+    reqs[16] = (reqs[16][0], np.array([25], np.uint32), 0)  # marker past the sequence
+    ids = np.concatenate([r[0] for r in reqs])
+    lens = np.array([len(r[0]) for r in reqs], np.uintp)
+    markers = np.concatenate([r[1] for r in reqs])
+    nm = np.array([len(r[1]) for r in reqs], np.uintp)
+    qt = np.zeros(len(reqs), np.uint32)
+    logits = np.full(len(markers), -7.0, np.float32)
+    ms = np.full(len(reqs), -7.0, np.float32)
+    err = ctypes.create_string_buffer(256)
+    fn = jh.lib().julia_hip_run_batched if batched else jh.lib().julia_cuda_run
+    p = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    rc = fn(e.ptr, len(reqs), p(ids), p(lens), p(markers), p(nm), p(qt), 0, p(logits), p(ms),
+            err, 256)
+    assert rc == -1 and b"marker is past" in err.value, err.value
+    assert np.all(logits == -7.0) and np.all(ms == -7.0)
+
+
 def test_batched_encoder_matches_each_request(torch_cuda):
     """Config 5's batched variant: requests concatenated into one set of rows,
     positions restarting in every request and attention kept within each, give every request its

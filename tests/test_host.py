@@ -214,6 +214,56 @@ def test_chooser_picks_valid_configs(m, n, k):
         assert 1 <= sp <= 4 and (k // 32) // (4 * sp) >= 2
 
 
+# The encoder's and head's GEMM shapes at width d (inter 1152, head_ff 1536) with their epilogues.
+def _model_gemms(d, inter=1152, ff=1536):
+    return [(3 * d, d, "lnrope"), (d, d, "resstats"), (2 * inter, d, "lngeglu"),
+            (d, inter, "resstats"), (3 * d, d, "lnbias"), (ff, d, "lnbiasrelu"),
+            (d, ff, "biasresstats"), (d, d, "lnbiasgelu")]
+
+
+@pytest.mark.parametrize("d", [384, 768, 1280, 2048])
+def test_every_pick_passes_the_launch_checks(d):
+    """gemm_choose's pick for every model GEMM (with its epilogue) at every row count passes the
+    launcher's own precondition checks (src/gemm.rs:262-329): in particular the throughput tiles'
+    LayerNorm limit (k <= 1024), which widths past 1024 reach."""
+    base = 1 << 20  # 16-byte aligned stand-in addresses (the check does not dereference them)
+    for m in list(range(1, 4097, 37)) + [8192, 18752, 20000]:
+        for n, k, epi in _model_gemms(d):
+            flags = jh.EPI[epi]
+            kw = {}
+            if flags & jh.EPI_LN:
+                kw.update(stats_in=base + 64, colsum=base + 128)
+            if flags & jh.EPI_ROPE:
+                kw.update(rope=base + 192, rope_rows=m)
+            if flags & jh.EPI_STATS:
+                kw.update(stats_out=base + 256)
+            if flags & jh.EPI_BIAS:
+                kw.update(bias=base + 320)
+            args = jh.gemm_args(flags, base, base + 4096, base + 8192, m, n, k, **kw)
+            bm, sp = jh.gemm_choose(m, n, k, 256, flags)
+            jh.gemm_check(args, bm, sp, ws_floats=1 << 30, counters=1 << 20)
+            if flags & jh.EPI_LN and k > 1024:
+                assert bm < 128, (m, n, k, epi, bm)
+
+
+def test_gemm_check_rejects_what_the_kernels_do_not_take():
+    base = 1 << 20
+    ln = dict(stats_in=base + 64, colsum=base + 128)
+    ok = jh.gemm_args("lngeglu", base, base + 4096, base + 8192, 4096, 2560, 1280, **ln)
+    jh.gemm_check(ok, 64)
+    with pytest.raises(jh.JuliaHipError, match="LayerNorm epilogues up to k = 1024"):
+        jh.gemm_check(ok, 256)
+    with pytest.raises(jh.JuliaHipError, match="not a multiple of 64"):
+        jh.gemm_check(jh.gemm_args("resstats", base, base, base + 64, 8, 100, 64,
+                                   stats_out=base + 256), 16)
+    with pytest.raises(jh.JuliaHipError, match="16-byte aligned"):
+        jh.gemm_check(jh.gemm_args("resstats", base + 2, base, base + 8192, 8, 64, 64,
+                                   stats_out=base + 256), 16)
+    with pytest.raises(jh.JuliaHipError, match="scratch is too small"):
+        jh.gemm_check(jh.gemm_args("resstats", base, base + 4096, base + 8192, 64, 768, 768,
+                                   stats_out=base + 256), 32, 2)
+
+
 def test_chooser_matches_the_measured_winners():
     """The picks at the shapes measured on MI355X (per-step GEMM times, the fastest config within
     a few percent): qkv/wi 48-row latency tiles at 293 tokens, wo and wo_mlp 16 rows."""
