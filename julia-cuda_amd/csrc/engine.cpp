@@ -411,6 +411,7 @@ Engine* load_engine(const char* dir, size_t max_length, size_t batch_rows = 0) {
         throw std::runtime_error(std::string("this library has gfx950 kernels, but ") + prop.name +
                                  " is " + arch);
     e->name = prop.name;
+    if (e->name.empty()) e->name = "AMD GPU (" + arch + ")";  // a runtime without the name table
     e->cus = prop.multiProcessorCount;
     e->cfg = spec;
     const ModelConfig& c = e->cfg;

@@ -139,6 +139,12 @@ public:
 private:
     int cus_ = 0, per_cu_ = 0, per_cu_big_ = 0, per_cu_big256_ = 0, lds_max_ = 0;
     uint32_t* bar_ = nullptr;  // BAR_WORDS words
+    // Launch through hipLaunchCooperativeKernel (true), or as a plain launch of the same
+    // resident grid: after the runtime refuses a cooperative launch because another process
+    // holds the GPU's cooperative-launch resource (hipErrorIllegalState), or when the
+    // environment sets JULIA_HIP_COOPERATIVE=0. The grid barrier is the kernel's own (atomics
+    // with a bounded wait), so the plain launch runs the same code.
+    bool coop_ = true;
 };
 
 }  // namespace jh

@@ -18,6 +18,9 @@
 // Activations written once per launch (x after each residual step, each layer's qkv and o, each
 // in its own buffer: LayerArgs) are read through the caches; mid and the statistics are read
 // device-coherent. Every output is stored device-coherent (written through to memory).
+#include <stdlib.h>
+#include <string.h>
+
 #include <algorithm>
 #include <stdexcept>
 #include <string>
@@ -428,6 +431,8 @@ static int big_lds_bytes(int bm) {
 
 void LayerKernel::init(int cus, int lds_max) {
     cus_ = cus > 0 ? cus : 256;
+    const char* coop = getenv("JULIA_HIP_COOPERATIVE");
+    coop_ = !(coop && strcmp(coop, "0") == 0);
     lds_max_ = lds_max - 16;  // the split-K flag after the main area
     per_cu_ = per_cu_big_ = per_cu_big256_ = 0;
     auto occupancy = [](const void* k, int threads, int lds) {
@@ -733,9 +738,22 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
     const void* kernel = mode == MODE_BIG256   ? reinterpret_cast<const void*>(encoder_kernel<MODE_BIG256>)
                          : mode == MODE_BIG128 ? reinterpret_cast<const void*>(encoder_kernel<MODE_BIG128>)
                                                : reinterpret_cast<const void*>(encoder_kernel<MODE_LAT>);
-    const hipError_t e = hipLaunchCooperativeKernel(kernel, dim3(grid_blocks),
-                                                    dim3(mode == MODE_BIG256 ? 512 : 256), args,
-                                                    lds + 16, stream);
+    const dim3 threads(mode == MODE_BIG256 ? 512 : 256);
+    hipError_t e = hipErrorIllegalState;
+    if (coop_) {
+        e = hipLaunchCooperativeKernel(kernel, dim3(grid_blocks), threads, args, lds + 16, stream);
+        if (e == hipErrorIllegalState) {
+            // Another process holds the cooperative-launch resource: from now on, plain launches
+            // of the same grid (at most the blocks resident at once, as the occupancy query
+            // sized it; a block that never gets a CU ends the barrier's bounded wait, which the
+            // host reports as an error, instead of hanging).
+            (void)hipGetLastError();
+            coop_ = false;
+        }
+    }
+    if (!coop_) {
+        e = hipLaunchKernel(kernel, dim3(grid_blocks), threads, args, lds + 16, stream);
+    }
     if (e != hipSuccess) fail(std::string(hipGetErrorString(e)) + " (" + plan.str() + ", grid " +
                               std::to_string(grid_blocks) + ")");
 }
