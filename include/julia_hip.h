@@ -145,6 +145,16 @@ void julia_hip_scratch_free(julia_hip_scratch *s);
 int julia_hip_gemm(const julia_hip_gemm_args *g, julia_hip_gemm_config cfg,
                    const julia_hip_scratch *s, void *stream, char *err, size_t err_len);
 
+/* No counterpart in the reference: julia_hip_gemm for callers that cannot allocate (code under
+ * HIP graph capture, serving loops that forbid hipMalloc). It takes no scratch: split-K
+ * partials and arrival counters live in a static device array of the library (32 MiB of
+ * partials and 16384 counters, held on every GPU it runs on until the process ends), and it
+ * calls no allocating routine. A tiling that needs more is rejected with -1 and the sizes.
+ * Calls on one GPU share the array: calls that overlap on one GPU (several streams at once)
+ * race. The counters a call uses are cleared by a fill kernel on its stream first. */
+int julia_hip_gemm_static(const julia_hip_gemm_args *g, julia_hip_gemm_config cfg, void *stream,
+                          char *err, size_t err_len);
+
 /* src/attn.rs:20-56 `attn::launch` (+ the layer kernel's key ranges): o [n][d] from qkv
  * [n][3d], heads of 64; window 0 = global; chunks = key ranges per tile (0: the chooser's). */
 int julia_hip_attention(const void *qkv, void *o, int n, int d, int window, int chunks,

@@ -815,6 +815,16 @@ int julia_hip_gemm(const julia_hip_gemm_args* g, julia_hip_gemm_config cfg,
     });
 }
 
+int julia_hip_gemm_static(const julia_hip_gemm_args* g, julia_hip_gemm_config cfg, void* stream,
+                          char* err, size_t err_len) {
+    return guarded(err, err_len, [&] {
+        const Gemm x = to_gemm(g);
+        GemmConfig c{cfg.bm, cfg.splits};
+        if (c.bm == 0) c = gemm_choose(x.m, x.n, x.k, device_cus(), x.epi);
+        gemm_launch_static(x, c, (hipStream_t)stream);
+    });
+}
+
 int julia_hip_attention(const void* qkv, void* o, int n, int d, int window, int chunks,
                         const julia_hip_scratch* s, void* stream, char* err, size_t err_len) {
     return guarded(err, err_len, [&] {

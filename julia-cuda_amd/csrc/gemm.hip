@@ -17,6 +17,7 @@
 // Both apply the epilogues of device.h (LayerNorm folding, bias, ReLU/GELU, RoPE, GeGLU,
 // residual, output statistics) in the same order.
 #include <algorithm>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 
@@ -213,6 +214,77 @@ void gemm_launch(const Gemm& g, GemmConfig cfg, const Scratch& s, hipStream_t st
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         throw std::runtime_error(std::string("gemm (") + cfg_str(cfg) + "): " + hipGetErrorString(e));
+}
+
+// ---------------------------------------------------------------------------------------------
+// The allocation-free entry (julia_hip_gemm_static): the split-K partials and arrival counters
+// live in this file-scope device array instead of a caller's julia_hip_scratch, so a caller that
+// cannot allocate (code under HIP graph capture, serving loops that forbid hipMalloc) can still
+// launch split-K tilings. Every GPU the library runs on holds its own copy (32.06 MiB) until
+// the process ends; every call on one GPU shares it, so calls that overlap on one GPU (two
+// streams at once) race. The counters must start at zero: each split-K call clears the ones it
+// uses with a fill kernel on its own stream before the GEMM (no hipMemsetAsync: the call may be
+// under graph capture).
+constexpr size_t STATIC_WS_FLOATS = size_t(8) << 20;  // f32 split-K partials (32 MiB)
+constexpr size_t STATIC_COUNTERS = 16384;              // split-K tiles
+static __device__ __align__(256) float scratch[STATIC_WS_FLOATS + STATIC_COUNTERS];
+
+__global__ __launch_bounds__(256) void zero_words(uint32_t* p, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+namespace {
+
+// The array's device address on each GPU: host code never uses the name `scratch` itself (it is
+// a host-side stand-in), only these addresses, looked up once per device with it current.
+std::mutex static_mu;
+float* static_addr[64] = {};
+
+float* static_scratch() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        throw std::runtime_error("gemm_static: no current device (or more than 64)");
+    std::lock_guard<std::mutex> lock(static_mu);
+    if (!static_addr[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            throw std::runtime_error(std::string("gemm_static: hipGetSymbolAddress: ") +
+                                     hipGetErrorString(e));
+        static_addr[dev] = (float*)ptr;
+    }
+    return static_addr[dev];
+}
+
+}  // namespace
+
+size_t gemm_static_ws_floats() { return STATIC_WS_FLOATS; }
+size_t gemm_static_counters() { return STATIC_COUNTERS; }
+
+void gemm_launch_static(const Gemm& g, GemmConfig cfg, hipStream_t st) {
+    if (cfg.splits > 1) {
+        const size_t need = gemm_ws_floats(g.m, g.n, cfg), tiles = gemm_counters(g.m, g.n, cfg);
+        if (need > STATIC_WS_FLOATS || tiles > STATIC_COUNTERS)
+            throw std::runtime_error(
+                "gemm_static: " + cfg_str(cfg) + " at m = " + std::to_string(g.m) + ", n = " +
+                std::to_string(g.n) + " needs " + std::to_string(need) + " floats of split-K "
+                "partials and " + std::to_string(tiles) + " counters; the static scratch holds " +
+                std::to_string(STATIC_WS_FLOATS) + " and " + std::to_string(STATIC_COUNTERS));
+    }
+    float* base = static_scratch();
+    uint32_t* counters = reinterpret_cast<uint32_t*>(base + STATIC_WS_FLOATS);
+    const Scratch s{base, STATIC_WS_FLOATS, counters, STATIC_COUNTERS};
+    gemm_check(g, cfg, s);
+    if (cfg.splits > 1) {
+        const int n = (int)gemm_counters(g.m, g.n, cfg);
+        hipLaunchKernelGGL(zero_words, dim3((n + 255) / 256), dim3(256), 0, st, counters, n);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess)
+            throw std::runtime_error(std::string("gemm_static: clearing the counters: ") +
+                                     hipGetErrorString(e));
+    }
+    gemm_launch(g, cfg, s, st);
 }
 
 // The tiling for a GEMM on a 256-CU GPU: the cheapest of the latency tiles and the two

@@ -116,6 +116,11 @@ GemmConfig gemm_choose(int m, int n, int k, int cus, int epi = 0);
 constexpr int GEMM_BIG_LN_MAX_K = 1024;
 size_t gemm_ws_floats(int m, int n, GemmConfig cfg);
 size_t gemm_counters(int m, int n, GemmConfig cfg);
+// gemm_launch with the split-K partials and counters in the library's static device scratch
+// (no allocation); throws when the tiling needs more than it holds.
+void gemm_launch_static(const Gemm& g, GemmConfig cfg, hipStream_t stream);
+size_t gemm_static_ws_floats();
+size_t gemm_static_counters();
 
 void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, int chunks,
                       const Scratch& s, hipStream_t stream, const int32_t* seg = nullptr);

@@ -79,7 +79,8 @@ class EngineInfo(ctypes.Structure):
 EXPORTS = [
     "julia_cuda_tier", "julia_cuda_load", "julia_cuda_free", "julia_cuda_device", "julia_cuda_run",
     "julia_hip_load", "julia_hip_run_batched", "julia_hip_model_kernel",
-    "julia_hip_scratch_new", "julia_hip_scratch_free", "julia_hip_gemm", "julia_hip_attention",
+    "julia_hip_scratch_new", "julia_hip_scratch_free", "julia_hip_gemm", "julia_hip_gemm_static",
+    "julia_hip_attention",
     "julia_hip_attention_seg",
     "julia_hip_embed", "julia_hip_norm_add", "julia_hip_score", "julia_hip_time_gemm",
     "julia_hip_time_attention", "julia_hip_time_copy", "julia_hip_copy", "julia_hip_device_count",
@@ -121,6 +122,7 @@ def lib():
         "julia_hip_scratch_new": (_VP, [_SZ, _SZ, _CP, _SZ]),
         "julia_hip_scratch_free": (None, [_VP]),
         "julia_hip_gemm": (_I, [ctypes.POINTER(GemmArgs), GemmConfig, _VP, _VP, _CP, _SZ]),
+        "julia_hip_gemm_static": (_I, [ctypes.POINTER(GemmArgs), GemmConfig, _VP, _CP, _SZ]),
         "julia_hip_attention": (_I, [_VP, _VP, _I, _I, _I, _I, _VP, _VP, _CP, _SZ]),
         "julia_hip_attention_seg": (_I, [_VP, _VP, _I, _I, _I, _VP, _VP, _VP, _CP, _SZ]),
         "julia_hip_embed": (_I, [_VP, _I, _VP, _I, _I, _VP, _F, _VP, _VP, _CP, _SZ]),
@@ -431,6 +433,11 @@ def gemm_args(epi, a, w, c, m, n, k, stats_in=0, colsum=0, eps=1e-5, bias=0, rop
 def gemm(args, bm=0, splits=1, scratch=None, stream=0):
     _call(lib().julia_hip_gemm, ctypes.byref(args), GemmConfig(bm, splits),
           scratch.ptr if scratch else None, stream or None)
+
+
+def gemm_static(args, bm=0, splits=1, stream=0):
+    """julia_hip_gemm without a scratch argument: the library's static device scratch."""
+    _call(lib().julia_hip_gemm_static, ctypes.byref(args), GemmConfig(bm, splits), stream or None)
 
 
 def time_gemm(args, bm=0, splits=1, scratch=None, warmup=20, batches=10, per_batch=50):

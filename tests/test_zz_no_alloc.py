@@ -1,0 +1,101 @@
+"""julia_hip_gemm_static, the GEMM entry point that allocates nothing (split-K partials and
+counters in the library's static device scratch), through the C ABI: bit-identical to
+julia_hip_gemm with a caller's scratch on the same inputs, over two calls in a row per shape
+(the second smaller, so stale partials and counters of the first would show), and rejected with
+the sizes when a tiling needs more scratch than the library holds."""
+
+import numpy as np
+import pytest
+
+import julia_hip as jh
+import oracle as O
+from checks import EMU_REL, compare, f32, rand16
+from conftest import f16_bits, to_dev
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-5
+
+
+def problem(kind, m, n, k, seed):
+    rng = np.random.default_rng(seed)
+    P = dict(kind=kind, epi=jh.EPI[kind], m=m, n=n, k=k, a=rand16(rng, (m, k), mean=0.1))
+    W = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    if kind == "resstats":
+        P["w"] = O.to_f16_bits(W)
+        P["res"] = rand16(rng, (m, n))
+        P["emu"], _ = O.emu_gemm(P["a"], P["w"], P["epi"], c16=P["res"])
+    else:
+        gamma = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+        P["w"], P["colsum"] = O.fold_layernorm(W, gamma)
+        P["stats_in"] = O.row_stats(P["a"])
+        if kind == "lnrope":
+            P["rope"] = O.rope_table(160000.0, m)
+        P["emu"] = O.emu_gemm(P["a"], P["w"], P["epi"], stats_in=P["stats_in"],
+                              colsum=P["colsum"], eps=EPS, rope=P.get("rope"),
+                              rope_cols=2 * n // 3 if kind == "lnrope" else 0)
+    return P
+
+
+def run(torch, P, bm, splits, scratch):
+    """One launch: through julia_hip_gemm with `scratch`, or julia_hip_gemm_static (None)."""
+    m, n, k = P["m"], P["n"], P["k"]
+    dev = {key: to_dev(torch, P[key]) for key in ("a", "stats_in", "colsum", "rope") if key in P}
+    dev["w"] = to_dev(torch, O.pack_frag(P["w"]))
+    ncols = n // 2 if P["kind"] == "lngeglu" else n
+    c = to_dev(torch, P["res"]) if "res" in P else torch.zeros((m, ncols), dtype=torch.float16,
+                                                               device="cuda")
+    st = torch.zeros((m, n // 64, 2), dtype=torch.float32, device="cuda") if "res" in P else None
+    ptr = lambda key: dev[key].data_ptr() if key in dev else 0
+    args = jh.gemm_args(P["epi"], ptr("a"), ptr("w"), c.data_ptr(), m, n, k,
+                        stats_in=ptr("stats_in"), colsum=ptr("colsum"), eps=EPS, rope=ptr("rope"),
+                        rope_rows=m, stats_out=st.data_ptr() if st is not None else 0)
+    stream = torch.cuda.current_stream().cuda_stream
+    if scratch is None:
+        jh.gemm_static(args, bm=bm, splits=splits, stream=stream)
+    else:
+        jh.gemm(args, bm=bm, splits=splits, scratch=scratch, stream=stream)
+    torch.cuda.synchronize()
+    return f16_bits(c), (st.cpu().numpy() if st is not None else None)
+
+
+# (kind, n, k, bm, splits, first m, second m): every split count the latency tiles take, and the
+# chooser's pick (bm 0).
+CASES = [("resstats", 768, 1152, 32, 4, 512, 200), ("lngeglu", 2304, 768, 48, 2, 448, 100),
+         ("lnrope", 2304, 768, 16, 3, 293, 72), ("resstats", 768, 768, 64, 2, 1024, 333),
+         ("lnrope", 2304, 768, 0, 1, 293, 72)]
+
+
+@pytest.mark.parametrize("kind,n,k,bm,splits,m1,m2", CASES)
+def test_gemm_static_matches_gemm(torch_cuda, kind, n, k, bm, splits, m1, m2):
+    scratch = jh.Scratch(ws_floats=1 << 24, counters=1 << 16)
+    try:
+        for call, m in enumerate((m1, m2)):
+            print(f"gemm_static {kind} m={m} n={n} k={k} bm={bm} splits={splits} call {call}",
+                  flush=True)
+            P = problem(kind, m, n, k, seed=100 * call + n + k + m)
+            want, want_st = run(torch_cuda, P, bm, splits, scratch)
+            got, got_st = run(torch_cuda, P, bm, splits, None)
+            assert np.array_equal(got, want), f"{kind} m={m}: output differs from julia_hip_gemm"
+            if want_st is not None:
+                assert np.array_equal(got_st.view(np.uint32), want_st.view(np.uint32))
+            compare(f32(got), f32(P["emu"]), EMU_REL, what=f"{kind} m={m} vs emulation")
+    finally:
+        scratch.close()
+
+
+def test_gemm_static_rejects_tilings_past_its_scratch(torch_cuda):
+    torch = torch_cuda
+    m, n, k = 8192, 2304, 768  # 16-row tiles, split 4: 18432 tiles > 16384 counters
+    a = torch.zeros((m, k), dtype=torch.float16, device="cuda")
+    w = torch.zeros((n * k,), dtype=torch.float16, device="cuda")
+    c = torch.zeros((m, n), dtype=torch.float16, device="cuda")
+    st = torch.zeros((m, n // 64, 2), dtype=torch.float32, device="cuda")
+    args = jh.gemm_args("resstats", a.data_ptr(), w.data_ptr(), c.data_ptr(), m, n, k,
+                        stats_out=st.data_ptr())
+    with pytest.raises(jh.JuliaHipError, match="static scratch holds"):
+        jh.gemm_static(args, bm=16, splits=4)
+    # the same shape without a split takes no scratch and runs
+    jh.gemm_static(args, bm=64, splits=1, stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert float(c.float().abs().max()) == 0.0
