@@ -79,6 +79,29 @@ STEP_SHAPES = {  # step: (n, k, epilogue, count per forward)
 }
 
 
+def row_bytes(step, m):
+    """Algorithmic HBM bytes of the row kernels on m rows: embed (ids, the m table rows, the
+    output, gamma), norm_add (x, the output, its row statistics, gamma and the type embedding),
+    score over every row (the rows, w, the logits)."""
+    if step == "embed":
+        return 4 * m + 2 * D * m + 2 * D * m + 4 * D
+    if step == "norm_add":
+        return 2 * D * m + 2 * D * m + 8 * m * (D // 64) + 8 * D
+    return 2 * D * m + 2 * D + 4 * m
+
+
+def bandwidth_kernels(eng, m):
+    """embed, norm_add and score (every row) on m rows: median us over back-to-back launches,
+    GB/s of algorithmic bytes and the fraction of the HBM peak."""
+    res = {}
+    for step in ("embed", "norm_add", "score"):
+        _, md = eng.time_step(step, m, warmup=10, batches=5, per_batch=40)
+        b = row_bytes(step, m)
+        res[step] = {"us": round(md, 3), "bytes": b, "GBps": round(b / (md * 1e-6) / 1e9, 1),
+                     "frac_hbm": round(b / (md * 1e-6) / PEAK_HBM, 4)}
+    return res
+
+
 def attention_flops(n, window):
     pairs = n * n if window == 0 else sum(min(n, i + window + 1) - max(0, i - window) for i in range(n))
     return 4 * 64 * H * pairs
@@ -240,6 +263,7 @@ def main():
         if v.get("flops"):
             v["TFLOPs"] = round(v["flops"] / (v["us"] * 1e-6) / 1e12, 2)
     out["kernels_293"] = kern
+    out["bandwidth_kernels"] = {"293_rows": bandwidth_kernels(eng, 293)}
     # The roofline kernel: config 1's fused qkv GEMM (with wi the largest share of the forward).
     dom = "qkv"
     dk = kern[dom]
@@ -251,26 +275,29 @@ def main():
     # HBM bytes per dispatch from the committed rocprofv3 counter passes (FETCH_SIZE and
     # WRITE_SIZE, scaled by the library's copy kernel: profiles/traffic_<step>_293.*), when they
     # are of this kernel.
-    traffic = None
+    traffic = rocprof_us = None
     tfile = os.path.join(ROOT, "profiles", f"traffic_{dom}_293.json")
     if os.path.exists(tfile):
         with open(tfile) as fh:
             t = json.load(fh)
         if t.get("kernel") == kname:
             traffic = t["traffic_bytes"]
+            rocprof_us = t.get("rocprof_avg_us")
     t_hbm, t_mfma = dk["bytes"] / PEAK_HBM, dk["flops"] / PEAK_F16
     if t_hbm >= t_mfma:
         ach = dk["bytes"] / (dk["us"] * 1e-6) / 1e9
         out["roofline"] = {"kernel": f"{kname}: {dom} gemm_{epi} M=293 N={n} K={k}", "bound": "hbm",
                            "achieved": round(ach, 1), "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                            "frac": round(ach / (PEAK_HBM / 1e9), 4), "traffic": traffic,
-                           "algorithmic_bytes": dk["bytes"], "us": dk["us"]}
+                           "algorithmic_bytes": dk["bytes"], "us": dk["us"],
+                           "rocprof_us": rocprof_us}
     else:
         ach = dk["flops"] / (dk["us"] * 1e-6) / 1e12
         out["roofline"] = {"kernel": f"{kname}: {dom} gemm_{epi} M=293 N={n} K={k}", "bound": "mfma",
                            "achieved": round(ach, 2), "peak": PEAK_F16 / 1e12, "unit": "TFLOP/s",
                            "frac": round(ach / (PEAK_F16 / 1e12), 4), "traffic": traffic,
-                           "algorithmic_flops": dk["flops"], "us": dk["us"]}
+                           "algorithmic_flops": dk["flops"], "us": dk["us"],
+                           "rocprof_us": rocprof_us}
     log("kernels at 293 tokens:", json.dumps(kern))
 
     # ---- config 2: the per-layer GEMM set at M=512 over tile heights x split-K ----
@@ -330,7 +357,8 @@ def main():
 
     # ---- the fused GEMMs at M >= 4096 (the metric's TFLOP/s and % of f16 MFMA peak) ----
     big = {}
-    eng_big = jh.Engine("synthetic:layers=4,vocab=1000,max_positions=20480", max_length=18752)
+    # (the full vocabulary: the embed rows of 18379 ids are mostly distinct table rows)
+    eng_big = jh.Engine("synthetic:layers=4,max_positions=20480", max_length=18752)
     for m in (4096, 18752):
         for step, (n, k, epi, _) in STEP_SHAPES.items():
             mn, md = eng_big.time_step(step, m, warmup=5, batches=5, per_batch=8)
@@ -338,6 +366,8 @@ def main():
             big[f"{step}@{m}"] = dict(us=round(md, 2), TFLOPs=round(fl / (md * 1e-6) / 1e12, 1),
                                       frac_peak=round(fl / (md * 1e-6) / PEAK_F16, 4),
                                       config=list(jh.gemm_choose(m, n, k, info.cus, epi)))
+    out["bandwidth_kernels"]["18379_rows"] = bandwidth_kernels(eng_big, 18379)
+    log("bandwidth kernels:", json.dumps(out["bandwidth_kernels"]))
     tot_fl = sum(2 * 18752 * n * k for (n, k, _, _) in STEP_SHAPES.values())
     tot_us = sum(big[f"{s}@18752"]["us"] for s in STEP_SHAPES)
     out["fused_gemm_tflops"] = round(tot_fl / (tot_us * 1e-6) / 1e12, 1)

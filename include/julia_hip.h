@@ -281,8 +281,9 @@ const void *julia_hip_engine_tensor(const Engine *e, const char *name, int index
 /* src/timing.rs / the reference's --time (src/main.rs:234-453): one encoder step of the engine
  * on m rows, timed as julia_hip_time_gemm does, rotating through the layers' weights from call
  * to call so they are not L2-resident (src/main.rs:307-312). step: 0 qkv, 1 attention (the
- * layers' own global/window mix), 2 wo, 3 wi, 4 wo_mlp, 5 global attention. bm = 0: the
- * chooser's tiling. */
+ * layers' own global/window mix), 2 wo, 3 wi, 4 wo_mlp, 5 global attention; the row kernels:
+ * 6 embed (m ids), 7 norm_add (m rows), 8 score (every one of m rows). bm = 0: the chooser's
+ * tiling. */
 int julia_hip_time_encoder_step(const Engine *e, int step, int m, int bm, int splits, int warmup,
                                 int batches, int per_batch, float *min_us, float *median_us,
                                 char *err, size_t err_len);

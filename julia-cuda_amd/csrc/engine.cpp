@@ -1152,7 +1152,7 @@ int julia_hip_time_encoder_step(const Engine* ce, int step, int m, int bm, int s
         Engine& e = *const_cast<Engine*>(ce);
         hip_check(hipSetDevice(e.device), "hipSetDevice");
         if (m <= 0 || m > e.max_length) throw std::runtime_error("time: m out of range");
-        if (step < 0 || step > 5) throw std::runtime_error("time: no step " + std::to_string(step));
+        if (step < 0 || step > 8) throw std::runtime_error("time: no step " + std::to_string(step));
         const int d = e.cfg.d, I = e.cfg.inter, L = e.cfg.layers;
         // A real residual stream and statistics to run on: embed ids 0..m-1 and one layer.
         std::vector<uint32_t> ids(m);
@@ -1174,6 +1174,23 @@ int julia_hip_time_encoder_step(const Engine* ce, int step, int m, int bm, int s
             l = lo + (l + 1 - lo) % (L - lo);
             const EncoderLayer& Ly = e.layout.layers[l];
             const float* rope = e.f(Ly.global ? e.layout.rope_global : e.layout.rope_local);
+            // The row kernels: embed of the m ids, the final norm + type embedding of the
+            // residual stream, the score of every row (identity markers).
+            if (step == 6) {
+                embed_launch(e.ids_d, m, e.h(e.layout.tok_embeddings), e.cfg.vocab, d,
+                             e.f(e.layout.emb_norm), e.cfg.norm_eps, e.hx, e.stream);
+                return;
+            }
+            if (step == 7) {
+                norm_add_launch(e.x, m, d, e.f(e.layout.final_norm), e.f(e.layout.type_emb),
+                                e.cfg.norm_eps, e.hx, e.stats_a, e.stream);
+                return;
+            }
+            if (step == 8) {
+                score_launch(e.x, m, d, e.h(e.layout.scorer.lin2), e.layout.scorer.lin2_b, nullptr,
+                             m, e.logits_d, e.stream);
+                return;
+            }
             Gemm g{};
             g.m = m, g.rope_rows = e.cfg.max_positions, g.eps = e.cfg.norm_eps;
             switch (step) {

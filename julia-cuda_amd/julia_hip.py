@@ -290,7 +290,8 @@ class Engine:
               qtype, int(bool(layer_fused)), _np_ptr(logits), _np_ptr(xt), _np_ptr(hx))
         return logits[: len(markers)], xt, hx
 
-    STEPS = {"qkv": 0, "attention": 1, "wo": 2, "wi": 3, "wo_mlp": 4, "attention_global": 5}
+    STEPS = {"qkv": 0, "attention": 1, "wo": 2, "wi": 3, "wo_mlp": 4, "attention_global": 5,
+             "embed": 6, "norm_add": 7, "score": 8}
 
     def time_step(self, step, m, bm=0, splits=1, warmup=20, batches=10, per_batch=44):
         """One encoder step on m rows, rotating through the layers' weights; (min, median) us."""

@@ -3,6 +3,8 @@
 plain device-to-device copy of a known size to calibrate byte counters against.
 
     python julia-cuda_amd/kernel_bench.py --step wi --tokens 293 --iters 200 --copy-mb 64
+    python julia-cuda_amd/kernel_bench.py --step embed,norm_add,score --tokens 18379 \
+        --spec synthetic:layers=2,max_positions=20480
     python julia-cuda_amd/kernel_bench.py --batch 64 --iters 3 --copy-mb 0
     python julia-cuda_amd/kernel_bench.py --requests 64 --iters 3
 
@@ -23,7 +25,8 @@ import julia_hip as jh  # noqa: E402
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--step", default="qkv", choices=list(jh.Engine.STEPS))
+    ap.add_argument("--step", default="qkv",
+                    help="one of " + ", ".join(jh.Engine.STEPS) + ", or several, comma-separated")
     ap.add_argument("--tokens", type=int, default=293)
     ap.add_argument("--iters", type=int, default=200)
     ap.add_argument("--bm", type=int, default=0)
@@ -60,10 +63,15 @@ def main():
                   f"{sorted(ms)[len(ms) // 2]:.3f} ms", flush=True)
         e.close()
         return
+    steps = args.step.split(",")
+    for st in steps:
+        if st not in jh.Engine.STEPS:
+            ap.error(f"no step {st!r}")
     e = jh.Engine(args.spec, max_length=max(1024, args.tokens))
-    mn, md = e.time_step(args.step, args.tokens, args.bm, args.splits, warmup=10, batches=1,
-                         per_batch=args.iters)
-    print(f"{args.step} at {args.tokens} tokens: {md:.2f} us per call", flush=True)
+    for st in steps:
+        mn, md = e.time_step(st, args.tokens, args.bm, args.splits, warmup=10, batches=1,
+                             per_batch=args.iters)
+        print(f"{st} at {args.tokens} tokens: {md:.2f} us per call", flush=True)
     if args.copy_mb:
         nbytes = args.copy_mb << 20
         mn, md = jh.time_copy(nbytes, warmup=2, batches=1, per_batch=5)
