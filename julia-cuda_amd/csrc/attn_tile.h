@@ -468,14 +468,22 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
 // MFMAs; a 64-key block is two of the slice tile's 32-key steps. Each key is read once per 64
 // queries, and with three blocks a CU (48 KB of LDS each) the waves hide each other's step
 // latencies.
+//
+// KS = 2 (one long sequence, a grid of about a block a CU): the block has two groups of NW
+// waves, each running the online softmax of the same NW x 16 queries over every other key
+// block (group g takes blocks g, g + 2, ...) through its own stage ring, in lockstep (one
+// block barrier a step for both); group 1's running max, sum and output then go through LDS
+// and group 0 merges them (in group order: deterministic). Two waves a SIMD instead of one
+// hide each other's step latencies where the grid leaves the CUs a block each.
 constexpr int ATT_STREAM_STAGES = 3;
 constexpr int ATT_STREAM_LDS = ATT_STREAM_STAGES * 16384;
 
 // Task `task` of (n + 16 NW - 1) / (16 NW) query blocks x heads (XCD-mapped); `lds`:
-// ATT_STREAM_LDS bytes. XS: o is stored device-coherent (the persistent kernel). Ends with a
-// block barrier.
-template <bool XS = false, int NW = 4>
+// KS x ATT_STREAM_LDS bytes; 64 NW KS threads. XS: o is stored device-coherent (the persistent
+// kernel). Ends with a block barrier.
+template <bool XS = false, int NW = 4, int KS = 1>
 __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int task, char* lds) {
+    static_assert(KS == 1 || KS == 2, "key groups");
     constexpr int NS = ATT_STREAM_STAGES, QB = 16 * NW;
     constexpr int LOADS = 16 / NW;  // 1 KB copies a wave per stage
     static_assert(NW == 4 || NW == 8, "waves");
@@ -484,7 +492,9 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
     const int L = xcd_task(task, tiles * heads);
     const int h = L / tiles, q0 = (L % tiles) * QB;
     const int tid = threadIdx.x, l = tid & 63, r16 = l & 15, g = l >> 4;
-    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int wk = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int w = wk % NW, kg = wk / NW;  // the wave's queries, its key group
+    char* const ring = lds + kg * ATT_STREAM_LDS;
     const int j = r16 >> 2, q = r16 & 3;
 
     // The tile's keys: from its first row's sequence start to its last row's sequence end, cut
@@ -524,7 +534,7 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
     // then of V), LOADS a wave; lane l fills LDS chunk 64 I + l = row c / 8, logical chunk
     // (c % 8) ^ (row % 8). Rows past n are clamped (their keys are masked).
     auto stage = [&](int b, int st) {
-        char* dst = lds + st * 16384;
+        char* dst = ring + st * 16384;
         const int kb = k0 + 64 * b;
 #pragma unroll
         for (int qq = 0; qq < LOADS; qq++) {
@@ -553,21 +563,25 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
     for (int dt = 0; dt < 4; dt++)
         voff[dt] = 8192 + att_swz(4 * g + j, 2 * dt + (q >> 1)) + (q & 1) * 8;
 
-    // Block b, in stage ST = b % NS (a constant).
+    // The group's step b: its block kg + KS b (if there is one), in stage ST = b % NS (a
+    // constant). Both groups take every step: the barrier is the block's.
+    const int nsteps = (nblk + KS - 1) / KS;
+    auto has = [&](int b) { return kg + KS * b < nblk; };
     auto step = [&](int b, auto st_) {
         constexpr int ST = decltype(st_)::value;
-        // Block b's copies done (block b + 1's may stay in flight; the query loads came first),
-        // then every wave's: and every wave is done with block b - 1, whose stage block b + 2
+        // Step b's copies done (step b + 1's may stay in flight; the query loads came first),
+        // then every wave's: and every wave is done with step b - 1, whose stage step b + 2
         // takes.
-        if (b + 1 < nblk)
+        if (has(b + 1))
             wait_vmcnt<LOADS>();
         else
             wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
-        if (b + 2 < nblk) stage(b + 2, (ST + 2) % NS);
-        const int kb = k0 + 64 * b;
+        if (has(b + 2)) stage(kg + KS * (b + 2), (ST + 2) % NS);
+        if (!has(b)) return;
+        const int kb = k0 + 64 * (kg + KS * b);
         if (kb + 64 <= wlo || kb >= whi) return;
-        const char* st = lds + ST * 16384;
+        const char* st = ring + ST * 16384;
         // The 64 keys in one step: S^T for keys kb + 16 t + 4 g + e (t < 4), one max and one
         // rescale; P . V in two K-32 halves.
         half8 kf[4][2];
@@ -652,12 +666,38 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
     };
 
     static_assert(NS == 3, "the loop below is unrolled by the stages");
-    if (nblk > 0) stage(0, 0);
-    if (nblk > 1) stage(1, 1);
-    for (int b = 0; b < nblk; b += NS) {
+    if (has(0)) stage(kg, 0);
+    if (has(1)) stage(kg + KS, 1);
+    for (int b = 0; b < nsteps; b += NS) {
         step(b, std::integral_constant<int, 0>{});
-        if (b + 1 < nblk) step(b + 1, std::integral_constant<int, 1>{});
-        if (b + 2 < nblk) step(b + 2, std::integral_constant<int, 2>{});
+        if (b + 1 < nsteps) step(b + 1, std::integral_constant<int, 1>{});
+        if (b + 2 < nsteps) step(b + 2, std::integral_constant<int, 2>{});
+    }
+
+    if (KS == 2) {
+        // Group 1's running max, sum and unnormalised output into the first ring (every wave is
+        // done with the stages: the barrier), group 0 merges them with its own.
+        float* mg = (float*)lds + (size_t)w * 18 * 64;
+        __syncthreads();
+        if (kg == 1) {
+            mg[16 * 64 + l] = mx;
+            mg[17 * 64 + l] = lsum;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) mg[(4 * dt + e) * 64 + l] = oacc[dt][e];
+        }
+        __syncthreads();
+        if (kg == 1) return;  // (its threads take no further barrier)
+        const float m1 = mg[16 * 64 + l], l1 = mg[17 * 64 + l];
+        const float m = fmaxf(mx, m1);
+        const float base = m == -INFINITY ? 0.0f : m;
+        const float a0 = fast_exp2(mx - base), a1 = fast_exp2(m1 - base);
+        lsum = lsum * a0 + l1 * a1;
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) oacc[dt][e] = oacc[dt][e] * a0 + mg[(4 * dt + e) * 64 + l] * a1;
     }
 
     const float tot = sum_xor32(sum_xor16(lsum));
@@ -672,7 +712,7 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
             store8<XS>(op + 16 * dt, ov);
         }
     }
-    __syncthreads();  // LDS is free again
+    if (KS == 1) __syncthreads();  // LDS is free again (KS = 2: the caller's kernel ends here)
 }
 
 }  // namespace jh
