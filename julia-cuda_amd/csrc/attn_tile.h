@@ -532,18 +532,27 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
 
     // Block b (keys k0 + 64 b ..) into stage st = b % NS: 16 wave loads of 1 KB (8 rows of K,
     // then of V), LOADS a wave; lane l fills LDS chunk 64 I + l = row c / 8, logical chunk
-    // (c % 8) ^ (row % 8). Rows past n are clamped (their keys are masked).
+    // (c % 8) ^ (row % 8). The copies go through a buffer descriptor over the block's rows: the
+    // lane's offsets within a block are fixed (computed once), and rows past n read as zeros
+    // (their keys are masked).
+    uint32_t doff[LOADS];
+#pragma unroll
+    for (int qq = 0; qq < LOADS; qq++) {
+        const bool kk = qq < LOADS / 2;  // the first half of a wave's copies are K's
+        const int I = (w + NW * qq) & 7;
+        const int c = I * 64 + l, row = c >> 3, ch = (c & 7) ^ (row & 7);
+        doff[qq] = (uint32_t)((row * ld + (kk ? d : 2 * d) + h * 64 + ch * 8) * 2);
+    }
     auto stage = [&](int b, int st) {
         char* dst = ring + st * 16384;
         const int kb = k0 + 64 * b;
+        const auto rs = buffer_rsrc((const f16*)p.qkv + (size_t)kb * ld,
+                                    (uint32_t)(min(n - kb, 64) * ld * 2));
 #pragma unroll
         for (int qq = 0; qq < LOADS; qq++) {
-            const bool kk = qq < LOADS / 2;  // the first half of a wave's copies are K's
+            const bool kk = qq < LOADS / 2;
             const int I = (w + NW * qq) & 7;
-            const int c = I * 64 + l, row = c >> 3, ch = (c & 7) ^ (row & 7);
-            const int col = (kk ? d : 2 * d) + h * 64;
-            const f16* src = (const f16*)p.qkv + (size_t)min(kb + row, n - 1) * ld + col + ch * 8;
-            lds_dma16<false>(src, dst + (kk ? 0 : 8192) + I * 1024);
+            lds_bdma16<false>(rs, doff[qq], dst + (kk ? 0 : 8192) + I * 1024);
         }
     };
 

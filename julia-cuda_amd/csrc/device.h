@@ -264,6 +264,15 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* base) {
                                      XG ? 16 : 0);
 }
 
+// The same through a buffer descriptor: the lane's 16 bytes at byte `voff` of `r` (zeros past its
+// size, with no memory access). The address is the descriptor (scalar) plus a 32-bit lane
+// offset: no 64-bit address arithmetic per lane and copy.
+template <bool XG = false>
+__device__ __forceinline__ void lds_bdma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, void* base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)base, 16,
+                                             voff, 0, 0, XG ? 16 : 0);
+}
+
 // gfx950's transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group, lane i receives
 // element i % 4 of the 8 bytes lanes 4 j + i / 4 address, as its element j (j < 4). Loading a
 // row-major [key][d] tile this way hands a lane 4 consecutive keys of one d column.
