@@ -475,7 +475,7 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
 // block barrier a step for both); group 1's running max, sum and output then go through LDS
 // and group 0 merges them (in group order: deterministic). Two waves a SIMD instead of one
 // hide each other's step latencies where the grid leaves the CUs a block each.
-constexpr int ATT_STREAM_STAGES = 3;
+constexpr int ATT_STREAM_STAGES = 2;
 constexpr int ATT_STREAM_LDS = ATT_STREAM_STAGES * 16384;
 
 // Task `task` of (n + 16 NW - 1) / (16 NW) query blocks x heads (XCD-mapped); `lds`:
@@ -573,40 +573,43 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
         voff[dt] = 8192 + att_swz(4 * g + j, 2 * dt + (q >> 1)) + (q & 1) * 8;
 
     // The group's step b: its block kg + KS b (if there is one), in stage ST = b % NS (a
-    // constant). Both groups take every step: the barrier is the block's.
+    // constant). Both groups take every step: the barrier is the block's. A step waits for its
+    // block's copies (the only ones in flight), issues every LDS read of the block, then copies
+    // the next block into the other stage and computes while that copy flies: the compiler
+    // makes any LDS read wait for every direct-to-LDS copy in flight (it cannot tell the stages
+    // apart), so a copy issued before a read would be waited for there.
     const int nsteps = (nblk + KS - 1) / KS;
     auto has = [&](int b) { return kg + KS * b < nblk; };
     auto step = [&](int b, auto st_) {
         constexpr int ST = decltype(st_)::value;
-        // Step b's copies done (step b + 1's may stay in flight; the query loads came first),
-        // then every wave's: and every wave is done with step b - 1, whose stage step b + 2
-        // takes.
-        if (has(b + 1))
-            wait_vmcnt<LOADS>();
-        else
-            wait_vmcnt<0>();
+        // This wave's copies of the block done, then every wave's: and every wave is done with
+        // step b - 1, whose stage step b + 1 takes.
+        wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
-        if (has(b + 2)) stage(kg + KS * (b + 2), (ST + 2) % NS);
-        if (!has(b)) return;
         const int kb = k0 + 64 * (kg + KS * b);
-        if (kb + 64 <= wlo || kb >= whi) return;
+        const bool act = has(b) && !(kb + 64 <= wlo || kb >= whi);
         const char* st = ring + ST * 16384;
         // The 64 keys in one step: S^T for keys kb + 16 t + 4 g + e (t < 4), one max and one
         // rescale; P . V in two K-32 halves.
         half8 kf[4][2];
         half4 vlo[2][4], vhi[2][4];
+        if (act) {
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+            for (int t = 0; t < 4; t++)
 #pragma unroll
-            for (int k2 = 0; k2 < 2; k2++) kf[t][k2] = *(const half8*)(st + koff[k2] + 2048 * t);
+                for (int k2 = 0; k2 < 2; k2++) kf[t][k2] = *(const half8*)(st + koff[k2] + 2048 * t);
 #pragma unroll
-        for (int hf = 0; hf < 2; hf++)
+            for (int hf = 0; hf < 2; hf++)
 #pragma unroll
-            for (int dt = 0; dt < 4; dt++) {
-                vlo[hf][dt] = lds_read_tr16(st + voff[dt] + 4096 * hf);
-                vhi[hf][dt] = lds_read_tr16(st + voff[dt] + 4096 * hf + 2048);
-            }
+                for (int dt = 0; dt < 4; dt++) {
+                    vlo[hf][dt] = lds_read_tr16(st + voff[dt] + 4096 * hf);
+                    vhi[hf][dt] = lds_read_tr16(st + voff[dt] + 4096 * hf + 2048);
+                }
+        }
         __builtin_amdgcn_sched_barrier(0);
+        if (has(b + 1)) stage(kg + KS * (b + 1), (ST + 1) % NS);
+        __builtin_amdgcn_sched_barrier(0);
+        if (!act) return;
         floatx4 sc[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
@@ -674,13 +677,11 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
         }
     };
 
-    static_assert(NS == 3, "the loop below is unrolled by the stages");
+    static_assert(NS == 2, "the loop below is unrolled by the stages");
     if (has(0)) stage(kg, 0);
-    if (has(1)) stage(kg + KS, 1);
     for (int b = 0; b < nsteps; b += NS) {
         step(b, std::integral_constant<int, 0>{});
         if (b + 1 < nsteps) step(b + 1, std::integral_constant<int, 1>{});
-        if (b + 2 < nsteps) step(b + 2, std::integral_constant<int, 2>{});
     }
 
     if (KS == 2) {
