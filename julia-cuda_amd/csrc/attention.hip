@@ -33,11 +33,12 @@ __global__ __launch_bounds__(256) void attention_stream_kernel(AttnParams p) {
     attention_stream_tile(p, blockIdx.x, lds);
 }
 
-// The streaming tile with two key groups of four waves (one long sequence on a grid of about a
+// The streaming tile with two key groups of NW waves (one long sequence on a grid of about a
 // block a CU). Dynamic LDS: 2 ATT_STREAM_LDS.
-__global__ __launch_bounds__(512) void attention_stream2_kernel(AttnParams p) {
+template <int NW>
+__global__ __launch_bounds__(128 * NW) void attention_stream2_kernel(AttnParams p) {
     extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
-    attention_stream_tile<false, 4, 2>(p, blockIdx.x, lds_dyn);
+    attention_stream_tile<false, NW, 2>(p, blockIdx.x, lds_dyn);
 }
 
 __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
@@ -67,7 +68,9 @@ bool attention_prepare() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, att_lds_bytes(512, 4)) == hipSuccess &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(attention_lds_kernel<8>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, att_lds_bytes(512, 8)) == hipSuccess &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(attention_stream2_kernel),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(attention_stream2_kernel<2>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 2 * ATT_STREAM_LDS) == hipSuccess &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(attention_stream2_kernel<4>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, 2 * ATT_STREAM_LDS) == hipSuccess;
     return ok;
 }
@@ -136,7 +139,20 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
     if (seg && chunks != 1) fail("concatenated sequences take one key range");
     if (seg && ((uintptr_t)seg % 8)) fail("seg must be 8-byte aligned");
     AttnParams p{qkv, o, n, d, window, chunks, s.ws, s.counters, seg};
-    if (chunks == 1 && !att_use_stream(n, window)) {
+    // One key range: the tile by measured crossovers (MI355X, one sequence, us; slice tile
+    // with 4 / 8 waves, streaming tile with waves x key groups 2 x 2 / 4 x 2 / 4 x 1):
+    //   global   293 rows  5.5 / 5.1 | 5.0 / 5.9 / 6.0      1024 rows 28.3 / 21.2 | 10.7 / 10.8 / 12.7
+    //            2048 rows 98 / 68   | 30.1 / 27.5 / 28.8   4096 rows (4 x 2 / 4 x 1) 85.4 / 82.5
+    //   +-64     700 rows  4.9 / 6.6 | 5.0 / 5.1 / 5.0      1024 rows 5.3 / 7.1 | 5.3 / 5.3 / 5.0
+    //            1536 rows 7.9 / 10.4 | 7.9 / 6.8 / 6.1
+    // so the slice tile below 293 rows (global) or 768 (window), else the streaming tile: two
+    // key groups of two waves while that grid fits the CUs, of four while the four-wave grid is
+    // at most two blocks a CU (global), one group of four otherwise (config 5's batch: 4 x 1
+    // 48 us a global layer against 59 for 4 x 2).
+    const int cus = device_cus();
+    const long grid64 = (long)(n + 63) / 64 * (d / 64), grid32 = (long)(n + 31) / 32 * (d / 64);
+    const bool slice = chunks == 1 && (window == 0 ? n < 293 : n <= 768);
+    if (slice) {
         if (!attention_prepare()) fail("the LDS-resident kernel cannot have its LDS");
         const int gkeys = attention_gkeys(n, window);
         const dim3 grid((n + 15) / 16 * (d / 64));
@@ -145,17 +161,13 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
         else
             hipLaunchKernelGGL(attention_lds_kernel<4>, grid, dim3(256), att_lds_bytes(gkeys, 4), st, p, gkeys);
     } else if (chunks == 1) {
-        // Two key groups a block where the grid leaves the CUs a block each (measured on
-        // MI355X, one sequence, global: 448 rows 7.8 -> 7.3 us, 1024 rows 15.0 -> 12.6 us), one
-        // where blocks share CUs (2048 rows 34.8 against 40.7 us, config 5's batch 1.06 against
-        // 1.90 ms for the 22 layers).
-        const dim3 grid((n + 63) / 64 * (d / 64));
-        if ((int)grid.x <= device_cus()) {
-            if (!attention_prepare()) fail("the two-group streaming kernel cannot have its LDS");
-            hipLaunchKernelGGL(attention_stream2_kernel, grid, dim3(512), 2 * ATT_STREAM_LDS, st, p);
-        } else {
-            hipLaunchKernelGGL(attention_stream_kernel, grid, dim3(256), 0, st, p);
-        }
+        if (!attention_prepare()) fail("the two-group streaming kernels cannot have their LDS");
+        if (window == 0 && grid32 <= cus)
+            hipLaunchKernelGGL(attention_stream2_kernel<2>, dim3(grid32), dim3(256), 2 * ATT_STREAM_LDS, st, p);
+        else if (window == 0 && grid64 <= 2 * cus)
+            hipLaunchKernelGGL(attention_stream2_kernel<4>, dim3(grid64), dim3(512), 2 * ATT_STREAM_LDS, st, p);
+        else
+            hipLaunchKernelGGL(attention_stream_kernel, dim3(grid64), dim3(256), 0, st, p);
     } else {
         hipLaunchKernelGGL(attention_kernel, dim3((n + 63) / 64, d / 64, chunks), dim3(256), 0, st, p);
     }

@@ -486,7 +486,7 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
     static_assert(KS == 1 || KS == 2, "key groups");
     constexpr int NS = ATT_STREAM_STAGES, QB = 16 * NW;
     constexpr int LOADS = 16 / NW;  // 1 KB copies a wave per stage
-    static_assert(NW == 4 || NW == 8, "waves");
+    static_assert(NW == 2 || NW == 4 || NW == 8, "waves");
     const int n = p.n, d = p.d, ld = 3 * d, heads = d >> 6;
     const int tiles = (n + QB - 1) / QB;
     const int L = xcd_task(task, tiles * heads);
