@@ -129,7 +129,8 @@ typedef struct {
     float *stats_out;
 } julia_hip_gemm_args;
 
-/* src/gemm.rs:126-137 `Config`: tile height (16, 32, 64, 128, 256) and K splits (1-8). */
+/* src/gemm.rs:126-137 `Config`: tile height (16, 32, 48, 64: the latency tiles, 64 columns
+ * wide; 128, 192, 256: the throughput tiles, 128, 256 and 256 wide) and K splits (1-8). */
 typedef struct {
     int bm;
     int splits;

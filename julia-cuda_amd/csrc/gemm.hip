@@ -56,11 +56,11 @@ __global__ __launch_bounds__(512, 1) void gemm_lat1(GemmParams p) {
 // without a block dispatch in between. (The grid is a multiple of 8, so a block's tasks stay on
 // its XCD's range of xcd_task.)
 template <int BM, int EPI>
-__global__ __launch_bounds__((Big<BM, BM>::THREADS)) void gemm_big(GemmParams p) {
+__global__ __launch_bounds__((Big<BM, big_bn(BM)>::THREADS)) void gemm_big(GemmParams p) {
     extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
     const int T = p.tiles_n * p.tiles_m;
     for (int task = blockIdx.x; task < T; task += gridDim.x)
-        gemm_big_tile<BM, BM, EPI, false, false>(p, task, lds_dyn);  // ends with a block barrier
+        gemm_big_tile<BM, big_bn(BM), EPI, false, false>(p, task, lds_dyn);  // ends with a block barrier
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -69,7 +69,7 @@ __global__ __launch_bounds__((Big<BM, BM>::THREADS)) void gemm_big(GemmParams p)
 namespace {
 
 std::string cfg_str(GemmConfig c) {
-    return std::to_string(c.bm) + "x" + std::to_string(c.bm >= 128 ? c.bm : 64) + " split " +
+    return std::to_string(c.bm) + "x" + std::to_string(c.bm >= 128 ? big_bn(c.bm) : 64) + " split " +
            std::to_string(c.splits);
 }
 
@@ -109,9 +109,11 @@ void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
     if (g.m <= 0) fail("no rows");
     if (g.n <= 0 || g.n % 64) fail("n = " + std::to_string(g.n) + " is not a multiple of 64");
     const bool tput = cfg.bm >= 128;
-    if (!(cfg.bm == 16 || cfg.bm == 32 || cfg.bm == 48 || cfg.bm == 64 || cfg.bm == 128 || cfg.bm == 256))
+    if (!(cfg.bm == 16 || cfg.bm == 32 || cfg.bm == 48 || cfg.bm == 64 || cfg.bm == 128 ||
+          cfg.bm == 192 || cfg.bm == 256))
         fail("no tile height " + std::to_string(cfg.bm));
-    if (tput && g.n % cfg.bm) fail("the " + cfg_str(cfg) + " tiles need n % " + std::to_string(cfg.bm) + " == 0");
+    if (tput && g.n % big_bn(cfg.bm))
+        fail("the " + cfg_str(cfg) + " tiles need n % " + std::to_string(big_bn(cfg.bm)) + " == 0");
     if (tput && cfg.splits != 1) fail("the " + cfg_str(cfg) + " tiles take no K split");
     if (tput && (g.epi & EPI_LN) && g.k > 128 * BIG_LN_SLOTS)
         fail("the " + cfg_str(cfg) + " tiles take LayerNorm epilogues up to k = " +
@@ -156,12 +158,13 @@ static void launch_one(const GemmParams& p, hipStream_t st) {
     const int blocks = p.tiles_n * p.tiles_m * p.splits;
     if (BM >= 128) {
         constexpr int B = BM >= 128 ? BM : 128;
+        using C = Big<B, big_bn(B)>;
         static const bool lds_ok =  // once per instantiation, before its first launch
             hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_big<B, EPI>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, Big<B, B>::LDS_BYTES) == hipSuccess;
+                                hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES) == hipSuccess;
         if (!lds_ok) throw std::runtime_error("gemm: the throughput kernel cannot have its LDS");
-        const int grid = std::min(blocks, (B == 256 ? 1 : 2) * device_cus());
-        hipLaunchKernelGGL((gemm_big<B, EPI>), dim3(grid), dim3(Big<B, B>::THREADS), (Big<B, B>::LDS_BYTES), st, p);
+        const int grid = std::min(blocks, (B == 128 ? 2 : 1) * device_cus());
+        hipLaunchKernelGGL((gemm_big<B, EPI>), dim3(grid), dim3(C::THREADS), (C::LDS_BYTES), st, p);
     } else if (p.splits == 1 && blocks <= device_cus()) {
         constexpr int B = BM < 128 ? BM : 64;
         constexpr int LDS = lat_lds_floats<B, 8>() * 4;
@@ -183,6 +186,7 @@ static void launch_epi(const GemmParams& p, int bm, hipStream_t st) {
         case 48: launch_one<48, EPI>(p, st); break;
         case 64: launch_one<64, EPI>(p, st); break;
         case 128: launch_one<128, EPI>(p, st); break;
+        case 192: launch_one<192, EPI>(p, st); break;
         default: launch_one<256, EPI>(p, st); break;
     }
 }
@@ -197,7 +201,7 @@ void gemm_launch(const Gemm& g, GemmConfig cfg, const Scratch& s, hipStream_t st
     p.rope_cols = (g.epi & EPI_ROPE) ? 2 * (g.n / 3) : 0;
     p.rope_rows = g.rope_rows;
     p.splits = cfg.splits;
-    p.tiles_n = g.n / (cfg.bm >= 128 ? cfg.bm : 64);
+    p.tiles_n = g.n / (cfg.bm >= 128 ? big_bn(cfg.bm) : 64);
     p.tiles_m = (g.m + cfg.bm - 1) / cfg.bm;
     switch (g.epi) {
         case EPI_K_ROPE: launch_epi<EPI_K_ROPE>(p, cfg.bm, st); break;
@@ -287,20 +291,24 @@ void gemm_launch_static(const Gemm& g, GemmConfig cfg, hipStream_t st) {
     gemm_launch(g, cfg, s, st);
 }
 
-// The tiling for a GEMM on a 256-CU GPU: the cheapest of the latency tiles and the two
+// The tiling for a GEMM on a 256-CU GPU: the cheapest of the latency tiles and the three
 // throughput tiles under a cost model fitted to MI355X sweeps (M = 72 .. 18752, the encoder's
-// four shapes; microseconds).
+// four shapes; microseconds, random operands, weights rotating through the layers).
 //  - Latency tiles (BM = 16/32/48/64 x 64): bound by how fast a CU takes in its tiles'
 //    operands: a fixed ~4 us (launch, first round trip, reduction, epilogue) plus the busiest
 //    CU's operand bytes, ceil(tiles / CUs) x (BM + 64) x K x 2, at about 55 GB/s into one CU.
 //    Ties go to the shorter tile.
-//  - 256 x 256 tiles (one a CU): ~2 us plus ~27.5 us per round of tiles at K = 768.
-//  - 128 x 128 tiles (two a CU): ~2 us plus ~12 us at K = 768 for a CU's first tile; a CU's
-//    second tile runs beside it and adds half that, so l tiles on the busiest CU take
-//    1.5 floor(l / 2) + (l odd) of those.
-// Measured winners: 48-row latency tiles for qkv and wi at 293 tokens, 16-row for wo and
-// wo_mlp, 32-row at 2048 for wo and wo_mlp; 128 x 128 for qkv at 2048 and 8192; 256 x 256
-// for qkv at 4096 and everything at 18752.
+//  - 128 x 128 tiles (two a CU): ~2 us plus ~8.5 us (K = 768) per tile on the busiest CU,
+//    ceil(tiles / CUs) of them (measured 10.1-11.8 us at one a CU, 17.5-19.9 at two, 27.6 at
+//    three, 35.7-43.9 at four and five).
+//  - 256 x 256 tiles (one a CU): ~2 us plus ~26.5 us per round of tiles (measured 21.6-29 us
+//    for one round, 48.7-55 for two, 82 for three).
+//  - 192 x 256 tiles (one a CU): ~2 us plus ~21.7 us per round (0.82 of the 256-row round:
+//    23.3-24.4, 42.5-45.9, 66.1, 89.5 us for one to four rounds).
+// Measured winners it reproduces: 48-row tiles for qkv and wi at 293 tokens, 16-row for wo and
+// wo_mlp; 128 x 128 for qkv at 1024-3072 and 8192 rows and for wo and wo_mlp from 2048 to 8192;
+// 192 x 256 for qkv and wi at 4096; 256 x 256 at 6144 and 12288 (qkv, wi) and everything at
+// 18752.
 GemmConfig gemm_choose(int m, int n, int k, int cus, int epi) {
     static_assert(GEMM_BIG_LN_MAX_K == 128 * BIG_LN_SLOTS, "the LayerNorm limit of the throughput tiles");
     if (cus <= 0) cus = 256;
@@ -315,12 +323,15 @@ GemmConfig gemm_choose(int m, int n, int k, int cus, int epi) {
     if (m >= 1024 && n % 128 == 0 && k % 64 == 0 && !((epi & EPI_LN) && k > GEMM_BIG_LN_MAX_K)) {
         const double ks = (double)k / 768.0;
         const long l128 = ((long)(n / 128) * ((m + 127) / 128) + cus - 1) / cus;
-        const double c128 = 2.0 + 12.0 * ks * (1.5 * (double)(l128 / 2) + (double)(l128 % 2));
+        const double c128 = 2.0 + 8.5 * ks * (double)l128;
         if (c128 < best_cost) best_cost = c128, best = GemmConfig{128, 1};
         if (n % 256 == 0) {
             const long l256 = ((long)(n / 256) * ((m + 255) / 256) + cus - 1) / cus;
-            const double c256 = 2.0 + 27.5 * ks * (double)l256;
+            const double c256 = 2.0 + 26.5 * ks * (double)l256;
             if (c256 < best_cost) best_cost = c256, best = GemmConfig{256, 1};
+            const long l192 = ((long)(n / 256) * ((m + 191) / 192) + cus - 1) / cus;
+            const double c192 = 2.0 + 21.7 * ks * (double)l192;
+            if (c192 < best_cost) best_cost = c192, best = GemmConfig{192, 1};
         }
     }
     return best;

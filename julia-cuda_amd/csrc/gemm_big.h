@@ -36,16 +36,22 @@ namespace jh {
 
 template <int BM, int BN>
 struct Big {
-    static_assert((BM == 256 && BN == 256) || (BM == 128 && BN == 128), "tile shape");
+    static_assert((BM == 256 && BN == 256) || (BM == 192 && BN == 256) || (BM == 128 && BN == 128),
+                  "tile shape");
     static constexpr int TM = BM, TN = BN, BK = 32, NSTAGE = 4;
-    static constexpr int WAVES_M = 2, WAVES_N = BN / 64;  // 2 x 4 waves (256) or 2 x 2 (128)
+    static constexpr int WAVES_M = 2, WAVES_N = BN / 64;  // 2 x 4 waves (BN 256) or 2 x 2 (128)
     static constexpr int NWAVES = WAVES_M * WAVES_N, THREADS = 64 * NWAVES;
     static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;  // a wave's block
     static constexpr int MR = WM / 32, NC = WN / 32;  // its 32 x 32 fragments
     static constexpr int NG = WN / 64;                // its 64-column groups
     static constexpr int A_BYTES = BM * BK * 2, W_BYTES = BN * BK * 2;
     static constexpr int STAGE = A_BYTES + W_BYTES;   // bytes per stage
-    static constexpr int LOADS = STAGE / 1024 / NWAVES;  // 1 KB copies per wave per stage
+    static constexpr int NCOPY = STAGE / 1024, A_COPIES = A_BYTES / 1024;  // 1 KB copies a stage
+    // Copies per wave and stage: LOADS for waves below FULL, LOADS - 1 for the rest (192 x 256:
+    // 28 copies over eight waves; the square tiles: LOADS for every wave).
+    static constexpr int LOADS = (NCOPY + NWAVES - 1) / NWAVES;
+    static constexpr int FULL = NCOPY - (LOADS - 1) * NWAVES;
+    static constexpr bool EVEN = FULL == NWAVES && A_BYTES == W_BYTES;
     static constexpr int COLS = NSTAGE * STAGE;       // per wave: colsum, bias of its columns
     static constexpr int ROWS = COLS + NWAVES * 2 * WN * 4;  // per row: LayerNorm mean, rstd
     static constexpr int POSR = ROWS + BM * 8;                // per row: RoPE position
@@ -53,9 +59,12 @@ struct Big {
     // RoPE epilogues, after the K loop: the tile's table rows (BM x 256 bytes) in the stages'
     // space, then the f16 staging of the output rows.
     static constexpr int TABLE_BYTES = BM * 256;
-    static_assert(NG == 1 && LOADS >= 1, "wave blocks of 64 columns");
-    static_assert(THREADS == 2 * BM, "two threads a row for the row statistics");
+    static_assert(NG == 1 && LOADS >= 2, "wave blocks of 64 columns");
+    static_assert(THREADS >= 2 * BM, "two threads a row for the row statistics");
 };
+
+// The column width of the throughput tile BM rows high.
+__host__ __device__ constexpr int big_bn(int bm) { return bm == 192 ? 256 : bm; }
 
 // LayerNorm statistics slots one thread reads (two threads split a row's K / 64 slots): the big
 // tiles take LayerNorm epilogues for K <= 64 * 2 * BIG_LN_SLOTS.
@@ -109,7 +118,7 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     const int slots = p.k >> 6;
     float2 sl[BIG_LN_SLOTS];
     if (EPI & EPI_LN) {
-        const int r = min(by * BM + (tid >> 1), p.m - 1);
+        const int r = min(by * BM + min(tid >> 1, BM - 1), p.m - 1);
         const float* st = p.stats_in + (size_t)r * slots * 2;
 #pragma unroll
         for (int u = 0; u < BIG_LN_SLOTS; u++) sl[u] = load8f<XG>(st + 2 * min(2 * u + (tid & 1), slots - 1));
@@ -118,7 +127,7 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     // are no positions), into LDS with the row statistics.
     int rpos = 0;
     if (EPI & EPI_ROPE) {
-        const int r = min(by * BM + (tid >> 1), p.m - 1);
+        const int r = min(by * BM + min(tid >> 1, BM - 1), p.m - 1);
         const int v = *(const int*)(p.pos ? (const void*)(p.pos + r) : (const void*)p.rope);
         rpos = min(max(p.pos ? v : r, 0), p.rope_rows - 1);
     }
@@ -127,11 +136,15 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     // Stage copies: copy q of the wave's LOADS is load I = w + NWAVES q of the stage's A_BYTES / 1024
     // a loads then W_BYTES / 1024 w loads.
     // (Copies q < LOADS / 2 are a's, the rest w's: the test is on the unrolled q, no branch.)
-    static_assert(C::A_BYTES == C::W_BYTES && C::LOADS % 2 == 0, "half the copies a's");
+    // (The square tiles: copies q < LOADS / 2 are a's, the rest w's, a test on the unrolled q;
+    // 192 x 256: copy I is a's while I < A_COPIES, a wave-uniform test, and copies past NCOPY
+    // are none.)
+    static_assert(!C::EVEN || C::LOADS % 2 == 0, "half the copies a's");
     auto issue_one = [&](int kt, int buf, int q) {
         char* st = lds + buf * C::STAGE;
         const int I = w + C::NWAVES * q;
-        if (q < C::LOADS / 2) {
+        if (!C::EVEN && I >= C::NCOPY) return;
+        if (C::EVEN ? q < C::LOADS / 2 : I < C::A_COPIES) {
             const int r = 16 * I + (l >> 2), ch = (l & 3) ^ ((r >> 2) & 3);
             const int row = min(by * BM + r, p.m - 1);
             const f16* src = (const f16*)p.a + (size_t)row * p.k + kt * 32 + ch * 8;
@@ -156,10 +169,13 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
         return *(const float4*)(wcols + a * C::WN + 64 * j + 32 * h + 8 * q + 4 * hi);
     };
 
-    if (nkt > 2)
-        wait_vmcnt<2 * C::LOADS>();
-    else
-        wait_vmcnt<C::LOADS>();
+    // This wave's copies a stage: LOADS, or LOADS - 1 (a wave-uniform branch between the waits).
+    const bool full_wave = C::EVEN || w < C::FULL;
+    if (nkt > 2) {
+        if (full_wave) wait_vmcnt<2 * C::LOADS>(); else wait_vmcnt<2 * C::LOADS - 2>();
+    } else {
+        if (full_wave) wait_vmcnt<C::LOADS>(); else wait_vmcnt<C::LOADS - 1>();
+    }
     mark(1);  // (not in the loop: the clock read is a scalar-memory operation, and with one of
               // those outstanding the compiler waits for every LDS read at once)
     auto col_out = [&](int a) {
@@ -184,10 +200,10 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
         Q = group_sum<2>(Q);
         const float mean = S / (float)p.k;
         const float var = fmaxf(Q / (float)p.k - mean * mean, 0.0f);
-        if ((tid & 1) == 0) rows_ms[tid >> 1] = make_float2(mean, 1.0f / sqrtf(var + p.eps));
+        if ((tid & 1) == 0 && tid < 2 * BM) rows_ms[tid >> 1] = make_float2(mean, 1.0f / sqrtf(var + p.eps));
     }
     int* rows_pos = (int*)(lds + C::POSR);
-    if ((EPI & EPI_ROPE) && (tid & 1) == 0) rows_pos[tid >> 1] = rpos;
+    if ((EPI & EPI_ROPE) && (tid & 1) == 0 && tid < 2 * BM) rows_pos[tid >> 1] = rpos;
 
     floatx16 acc[MR][NC];
 #pragma unroll
@@ -248,8 +264,10 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
         if (NEXT) {
             if (NEXT_LAST)
                 wait_vmcnt<0>();
-            else
+            else if (full_wave)
                 wait_vmcnt<C::LOADS>();
+            else
+                wait_vmcnt<C::LOADS - 1>();
             __builtin_amdgcn_s_barrier();
         }
 #pragma unroll

@@ -184,7 +184,7 @@ BIG_EPIS = [("lnrope", 2304, 768), ("rope", 2304, 768), ("lngeglu", 2304, 768),
 
 
 @pytest.mark.parametrize("kind,n,k", BIG_EPIS, ids=[f"{a}-{b}-{c}" for a, b, c in BIG_EPIS])
-@pytest.mark.parametrize("bm", [128, 256])
+@pytest.mark.parametrize("bm", [128, 192, 256])
 def test_big_tiles_every_epilogue(torch_cuda, scratch, kind, n, k, bm):
     say(f"big tiles {kind} M=2100 N={n} K={k} bm={bm}")
     P = gemm_problem(kind, 2100, n, k, seed=51 + n + k)
