@@ -327,7 +327,7 @@ def main():
                     _, md = jh.time_gemm(gargs, bm=bm, splits=sp, scratch=scr, warmup=5, batches=5,
                                          per_batch=20)
                     grid[f"{bm}/{sp}"] = round(md, 2)
-                except jh.JuliaHipError:  # a combination the kernels do not take (128: no split)
+                except jh.JuliaHipError:  # a combination the kernels do not take
                     grid[f"{bm}/{sp}"] = None
         _, md = jh.time_gemm(gargs, scratch=scr, warmup=5, batches=5, per_batch=20)
         c2[step] = {"epilogue": epi, "us_by_bm_split": grid,

@@ -130,7 +130,8 @@ typedef struct {
 } julia_hip_gemm_args;
 
 /* src/gemm.rs:126-137 `Config`: tile height (16, 32, 48, 64: the latency tiles, 64 columns
- * wide; 128, 192, 256: the throughput tiles, 128, 256 and 256 wide) and K splits (1-8). */
+ * wide; 128, 192, 256: the throughput tiles, 128, 256 and 256 wide) and K splits (1-8; at least
+ * four K steps of 32 a split on the latency tiles, two on the throughput tiles). */
 typedef struct {
     int bm;
     int splits;

@@ -9,10 +9,12 @@
 //    reduce their partial tiles through LDS, so a tile's serial K loop is a quarter as long and
 //    there are more tiles to spread over 256 CUs. Grid split-K on top is deterministic: the
 //    last block of a tile to arrive sums every split's partial in split order.
-//  - gemm_big (128 x 128 or 256 x 256 tiles): the MFMA-bound regime (M >= 2048): a and w
-//    tiles copied into four LDS stages by direct global -> LDS loads (gemm_big.h), four or eight
-//    waves each owning a 64 x 64 (or 128 x 64) output block on 32 x 32 x 16 MFMA, the epilogue's
-//    column-wise part applied on the accumulators.
+//  - gemm_big (128 x 128, 192 x 256 or 256 x 256 tiles): the MFMA-bound regime (M >= 2048): a
+//    and w tiles copied into four LDS stages by direct global -> LDS loads (gemm_big.h), four or
+//    eight waves each owning a 64 x 64 (96 x 64, 128 x 64) output block on 32 x 32 x 16 MFMA, the
+//    epilogue's column-wise part applied on the accumulators. A K split, the same deterministic
+//    last-arriver sum, is there for completeness (config sweeps): at these sizes the chooser
+//    never picks one.
 //
 // Both apply the epilogues of device.h (LayerNorm folding, bias, ReLU/GELU, RoPE, GeGLU,
 // residual, output statistics) in the same order.
@@ -55,12 +57,13 @@ __global__ __launch_bounds__(512, 1) void gemm_lat1(GemmParams p) {
 // b takes tasks b, b + grid, ...: a CU goes from one tile's epilogue to the next tile's copies
 // without a block dispatch in between. (The grid is a multiple of 8, so a block's tasks stay on
 // its XCD's range of xcd_task.)
-template <int BM, int EPI>
+// SPLIT: K split p.splits ways, the tile's last arriving split running the epilogue.
+template <int BM, int EPI, bool SPLIT>
 __global__ __launch_bounds__((Big<BM, big_bn(BM)>::THREADS)) void gemm_big(GemmParams p) {
     extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
-    const int T = p.tiles_n * p.tiles_m;
-    for (int task = blockIdx.x; task < T; task += gridDim.x)
-        gemm_big_tile<BM, big_bn(BM), EPI, false, false>(p, task, lds_dyn);  // ends with a block barrier
+    const int T = p.tiles_n * p.tiles_m * (SPLIT ? p.splits : 1);
+    for (int task = blockIdx.x; task < T; task += gridDim.x)  // each task ends with a block barrier
+        gemm_big_tile<BM, big_bn(BM), EPI, false, false, SPLIT>(p, task, lds_dyn);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -90,17 +93,20 @@ int device_cus() {
 
 }  // namespace
 
-// Split-K scratch (latency tiles only: the throughput tiles take no split).
+// Split-K scratch: a tile's f32 partial per split (the latency tiles store at least 32 rows), and
+// an arrival counter per tile.
 size_t gemm_ws_floats(int m, int n, GemmConfig cfg) {
-    if (cfg.splits <= 1 || cfg.bm >= 128) return 0;
-    const size_t tiles = (size_t)(n / 64) * ((m + cfg.bm - 1) / cfg.bm);
+    if (cfg.splits <= 1) return 0;
+    const int bn = cfg.bm >= 128 ? big_bn(cfg.bm) : 64;
+    const size_t tiles = (size_t)(n / bn) * ((m + cfg.bm - 1) / cfg.bm);
     const size_t rows = cfg.bm < 32 ? 32 : cfg.bm;
-    return tiles * cfg.splits * rows * 64;
+    return tiles * cfg.splits * rows * bn;
 }
 
 size_t gemm_counters(int m, int n, GemmConfig cfg) {
-    if (cfg.splits <= 1 || cfg.bm >= 128) return 0;
-    return (size_t)(n / 64) * ((m + cfg.bm - 1) / cfg.bm);
+    if (cfg.splits <= 1) return 0;
+    const int bn = cfg.bm >= 128 ? big_bn(cfg.bm) : 64;
+    return (size_t)(n / bn) * ((m + cfg.bm - 1) / cfg.bm);
 }
 
 void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
@@ -114,7 +120,6 @@ void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
         fail("no tile height " + std::to_string(cfg.bm));
     if (tput && g.n % big_bn(cfg.bm))
         fail("the " + cfg_str(cfg) + " tiles need n % " + std::to_string(big_bn(cfg.bm)) + " == 0");
-    if (tput && cfg.splits != 1) fail("the " + cfg_str(cfg) + " tiles take no K split");
     if (tput && (g.epi & EPI_LN) && g.k > 128 * BIG_LN_SLOTS)
         fail("the " + cfg_str(cfg) + " tiles take LayerNorm epilogues up to k = " +
              std::to_string(128 * BIG_LN_SLOTS));
@@ -151,6 +156,21 @@ void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
         fail("the throughput tiles take outputs up to 4 GB");
     if (!tput && ksteps / cfg.splits < 4)  // each of the four waves takes a K step of every split
         fail(std::to_string(cfg.splits) + " splits leave a wave no K step of " + std::to_string(ksteps));
+    if (tput && ksteps / cfg.splits < 2)  // the stage pipeline's first wait covers two stages
+        fail(std::to_string(cfg.splits) + " splits leave a throughput tile fewer than two K steps of " +
+             std::to_string(ksteps));
+}
+
+template <int B, int EPI, bool SPLIT>
+static void launch_big(const GemmParams& p, hipStream_t st) {
+    using C = Big<B, big_bn(B)>;
+    static const bool lds_ok =  // once per instantiation, before its first launch
+        hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_big<B, EPI, SPLIT>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES) == hipSuccess;
+    if (!lds_ok) throw std::runtime_error("gemm: the throughput kernel cannot have its LDS");
+    const int blocks = p.tiles_n * p.tiles_m * p.splits;
+    const int grid = std::min(blocks, (B == 128 ? 2 : 1) * device_cus());
+    hipLaunchKernelGGL((gemm_big<B, EPI, SPLIT>), dim3(grid), dim3(C::THREADS), (C::LDS_BYTES), st, p);
 }
 
 template <int BM, int EPI>
@@ -158,13 +178,8 @@ static void launch_one(const GemmParams& p, hipStream_t st) {
     const int blocks = p.tiles_n * p.tiles_m * p.splits;
     if (BM >= 128) {
         constexpr int B = BM >= 128 ? BM : 128;
-        using C = Big<B, big_bn(B)>;
-        static const bool lds_ok =  // once per instantiation, before its first launch
-            hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_big<B, EPI>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS_BYTES) == hipSuccess;
-        if (!lds_ok) throw std::runtime_error("gemm: the throughput kernel cannot have its LDS");
-        const int grid = std::min(blocks, (B == 128 ? 2 : 1) * device_cus());
-        hipLaunchKernelGGL((gemm_big<B, EPI>), dim3(grid), dim3(C::THREADS), (C::LDS_BYTES), st, p);
+        if (p.splits > 1) launch_big<B, EPI, true>(p, st);
+        else launch_big<B, EPI, false>(p, st);
     } else if (p.splits == 1 && blocks <= device_cus()) {
         constexpr int B = BM < 128 ? BM : 64;
         constexpr int LDS = lat_lds_floats<B, 8>() * 4;

@@ -70,10 +70,12 @@ __host__ __device__ constexpr int big_bn(int bm) { return bm == 192 ? 256 : bm; 
 // tiles take LayerNorm epilogues for K <= 64 * 2 * BIG_LN_SLOTS.
 constexpr int BIG_LN_SLOTS = 8;
 
-// Task `task` of tiles_n * tiles_m (XCD-mapped: an XCD takes a contiguous range of tasks, in the
-// grouped order below). AX: a is read device-coherent; XG: the outputs are stored and the
-// statistics read device-coherent. The residual is read through the caches.
-template <int BM, int BN, int EPI, bool AX, bool XG>
+// Task `task` of tiles_n * tiles_m (x splits with SPLIT; XCD-mapped: an XCD takes a contiguous
+// range of tasks, in the grouped order below). AX: a is read device-coherent; XG: the outputs are
+// stored and the statistics read device-coherent. The residual is read through the caches.
+// SPLIT: p.splits K splits a tile (the instances without it keep the whole K loop's code as it
+// is).
+template <int BM, int BN, int EPI, bool AX, bool XG, bool SPLIT = false>
 __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, char* lds,
                                               uint64_t* sub = nullptr) {
     auto mark = [&](int i) {  // profiling: thread 0's view of the task's stages
@@ -82,8 +84,10 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     mark(0);
     using C = Big<BM, BN>;
     constexpr int MR = C::MR, NC = C::NC, NG = C::NG;
-    const int T = p.tiles_n * p.tiles_m;
-    const int t2 = xcd_task(task, T);
+    // A task is (tile, K split z): the splits of a tile are consecutive tasks, on one XCD.
+    const int S = SPLIT ? p.splits : 1;
+    const int L = xcd_task(task, p.tiles_n * p.tiles_m * S);
+    const int z = L % S, t2 = L / S;
     // Groups of G row bands (about 2 MB of a): within a group the column block changes slowest,
     // so an XCD's concurrent tiles share a few w column blocks and the group's a bands, which
     // together fit its 4 MB L2 (a walk along whole row bands would cycle all of w through the
@@ -95,7 +99,8 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     const int tid = threadIdx.x, l = tid & 63, l32 = l & 31, hi = l >> 5;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar branches
     const int wm = w / C::WAVES_N, wn = w % C::WAVES_N;
-    const int U = p.k >> 5, nkt = U;               // K units of 32 = stages
+    const int U = p.k >> 5;                        // K units of 32
+    const int ub = z * U / S, nkt = (z + 1) * U / S - ub;  // this split's units = stages
     const int g0 = (bx * BN + wn * C::WN) >> 6;    // the wave's first 64-column group
 
     // ---- epilogue inputs that go with the first stage -----------------------------------------
@@ -140,9 +145,9 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     // 192 x 256: copy I is a's while I < A_COPIES, a wave-uniform test, and copies past NCOPY
     // are none.)
     static_assert(!C::EVEN || C::LOADS % 2 == 0, "half the copies a's");
-    auto issue_one = [&](int kt, int buf, int q) {
+    auto issue_one = [&](int ks, int buf, int q) {
         char* st = lds + buf * C::STAGE;
-        const int I = w + C::NWAVES * q;
+        const int I = w + C::NWAVES * q, kt = ub + ks;
         if (!C::EVEN && I >= C::NCOPY) return;
         if (C::EVEN ? q < C::LOADS / 2 : I < C::A_COPIES) {
             const int r = 16 * I + (l >> 2), ch = (l & 3) ^ ((r >> 2) & 3);
@@ -318,6 +323,60 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     float* sg = (float*)stage_base + w * 32 * PAD;
     f16* sgh = (f16*)stage_base + w * 32 * PADH;
     __syncthreads();  // every wave is done reading the stages
+
+    // Split-K (kernels/src/gemm.rs:355-433), as the latency tile's (finish in gemm_tile.h): every
+    // split stores its accumulators to the scratch ([tile][split][float4 v][thread], coherent
+    // stores), waits for them, then counts its arrival; the tile's last arriver (which resets the
+    // counter) sums every split's partial in split order, so the result does not depend on
+    // arrival order, and runs the epilogue. The others are done with the task.
+    if (SPLIT && S > 1) {
+        constexpr int NV = MR * NC * 4;  // float4s a lane
+        float* part = p.ws + (size_t)t2 * S * NV * C::THREADS * 4;
+        float* mine = part + (size_t)z * NV * C::THREADS * 4;
+#pragma unroll
+        for (int i = 0; i < MR; i++)
+#pragma unroll
+            for (int c = 0; c < NC; c++)
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    xstore16(mine + (((i * NC + c) * 4 + q) * C::THREADS + tid) * 4,
+                             make_float4(acc[i][c][4 * q], acc[i][c][4 * q + 1], acc[i][c][4 * q + 2],
+                                         acc[i][c][4 * q + 3]));
+        release_wait();
+        __syncthreads();
+        uint32_t* s_last = (uint32_t*)lds;  // the stages' space is free here
+        if (tid == 0) {
+            const uint32_t old = atomic_add_agent(p.counters + t2, 1u);
+            const uint32_t last = old == (uint32_t)(S - 1);
+            if (last) atomic_store_agent(p.counters + t2, 0u);
+            *s_last = last;
+        }
+        __syncthreads();
+        const uint32_t last = *s_last;
+        __syncthreads();  // every thread has read s_last before the epilogue writes the space
+        if (last == 0) return;
+#pragma unroll
+        for (int i = 0; i < MR; i++)
+#pragma unroll
+            for (int c = 0; c < NC; c++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[i][c][e] = 0.0f;
+        for (int zz = 0; zz < S; zz++) {
+            const float* src = part + (size_t)zz * NV * C::THREADS * 4;
+#pragma unroll
+            for (int i = 0; i < MR; i++)
+#pragma unroll
+                for (int c = 0; c < NC; c++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float4 v4 = xload16f(src + (((i * NC + c) * 4 + q) * C::THREADS + tid) * 4);
+                        acc[i][c][4 * q] += v4.x;
+                        acc[i][c][4 * q + 1] += v4.y;
+                        acc[i][c][4 * q + 2] += v4.z;
+                        acc[i][c][4 * q + 3] += v4.w;
+                    }
+        }
+    }
 
     // RoPE: the tile's table rows into LDS as whole lines (copy I takes rows 4 I .. 4 I + 3, 16
     // lanes a row; the 16-byte chunk c of row r is stored at chunk c ^ (r % 16), so that the 16

@@ -262,6 +262,15 @@ def test_gemm_check_rejects_what_the_kernels_do_not_take():
     with pytest.raises(jh.JuliaHipError, match="scratch is too small"):
         jh.gemm_check(jh.gemm_args("resstats", base, base + 4096, base + 8192, 64, 768, 768,
                                    stats_out=base + 256), 32, 2)
+    # the throughput tiles split K too (a 128 x 128 tile's partial is 16384 floats a split),
+    # down to two K steps a split
+    wo = jh.gemm_args("resstats", base, base + 4096, base + 8192, 512, 768, 768, stats_out=base + 256)
+    jh.gemm_check(wo, 128, 4, ws_floats=24 * 4 * 128 * 128, counters=24)
+    with pytest.raises(jh.JuliaHipError, match="scratch is too small"):
+        jh.gemm_check(wo, 128, 4, ws_floats=24 * 4 * 128 * 128 - 1, counters=24)
+    with pytest.raises(jh.JuliaHipError, match="fewer than two K steps"):
+        jh.gemm_check(jh.gemm_args("resstats", base, base + 4096, base + 8192, 512, 768, 128,
+                                   stats_out=base + 256), 256, 3, ws_floats=1 << 24, counters=64)
 
 
 def test_chooser_matches_the_measured_winners():
