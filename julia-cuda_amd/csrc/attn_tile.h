@@ -463,11 +463,11 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
 // ---- the streaming tile: long concatenated inputs ---------------------------------------------
 // A task is (16 NW queries, head): each of the NW waves runs the online softmax over every key of
 // the tile's range for its own 16 queries (no merge between waves). The key range (cut to the
-// rows' sequences and the window) goes through NS LDS stages of 64 keys, K and V row-major and
-// swizzled as in the slice tile, filled by direct global -> LDS loads two blocks ahead of the
+// rows' sequences and the window) goes through two LDS stages of 64 keys, K and V row-major and
+// swizzled as in the slice tile, filled by direct global -> LDS loads one block ahead of the
 // MFMAs; a 64-key block is two of the slice tile's 32-key steps. Each key is read once per 64
-// queries, and with three blocks a CU (48 KB of LDS each) the waves hide each other's step
-// latencies.
+// queries, and with four blocks a CU (32 KB of LDS and 108 registers a lane each) the waves
+// hide each other's step latencies.
 //
 // KS = 2 (one long sequence, a grid of about a block a CU): the block has two groups of NW
 // waves, each running the online softmax of the same NW x 16 queries over every other key
@@ -497,10 +497,24 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
     char* const ring = lds + kg * ATT_STREAM_LDS;
     const int j = r16 >> 2, q = r16 & 3;
 
+    // The sequence bounds the tile needs, all loaded in one round trip (the first stage's copy
+    // waits for them, and each round trip costs about a microsecond under load): the tile's first
+    // row's sequence start and last row's sequence end, the wave's first and last rows'
+    // sequences (uniform: scalar loads), this lane's query's sequence.
+    const int qlast = min(q0 + QB - 1, n - 1);
+    const int wq0 = min(q0 + 16 * w, n - 1), wql = min(q0 + 16 * w + 15, n - 1);
+    const int qi = q0 + 16 * w + r16;
+    const int qc = min(qi, n - 1);
+    int k0 = 0, k1 = n, ulo = 0, uhi = n, slo = 0, shi = n;
+    bool one_seq = true;
+    if (p.seg) {
+        const int t0 = p.seg[2 * q0], t1 = p.seg[2 * qlast + 1];
+        const int w0 = p.seg[2 * wq0], wls = p.seg[2 * wql], wle = p.seg[2 * wql + 1];
+        const int2 sq = *(const int2*)(p.seg + 2 * qc);
+        k0 = t0, k1 = t1, ulo = w0, uhi = wle, one_seq = w0 == wls, slo = sq.x, shi = sq.y;
+    }
     // The tile's keys: from its first row's sequence start to its last row's sequence end, cut
     // to the window; 64-aligned blocks.
-    const int qlast = min(q0 + QB - 1, n - 1);
-    int k0 = p.seg ? p.seg[2 * q0] : 0, k1 = p.seg ? p.seg[2 * qlast + 1] : n;
     if (p.window > 0) {
         k0 = max(k0, q0 - p.window);
         k1 = min(k1, q0 + QB + p.window);
@@ -508,21 +522,14 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
     k0 &= ~63;
     const int nblk = k1 > k0 ? (k1 - k0 + 63) >> 6 : 0;
 
-    // This lane's query and its sequence; the wave's 16 queries' common bounds (uniform).
-    const int qi = q0 + 16 * w + r16;
-    const int qc = min(qi, n - 1);
-    int slo = 0, shi = n;
-    if (p.seg) slo = p.seg[2 * qc], shi = p.seg[2 * qc + 1];
-    const int wq0 = min(q0 + 16 * w, n - 1), wql = min(q0 + 16 * w + 15, n - 1);
-    const bool one_seq = !p.seg || p.seg[2 * wq0] == p.seg[2 * wql];
-    const int ulo = p.seg ? p.seg[2 * wq0] : 0, uhi = p.seg ? p.seg[2 * wql + 1] : n;
-    const int wl = p.window > 0 ? p.window : (1 << 30);  // the lane's valid keys: [klo, khi)
+    // This lane's valid keys: its sequence cut to the window, [klo, khi).
+    const int wl = p.window > 0 ? p.window : (1 << 30);
     const int klo = max(slo, qi - wl), khi = min(shi, qi + wl + 1);
     const uint32_t kspan = khi > klo ? (uint32_t)(khi - klo) : 0u;
     // Keys any of the wave's 16 queries may see, [wlo, whi): the wave skips the MFMAs and the
     // softmax of a block wholly outside (every score masked: the step would change nothing).
     const int wlo = __builtin_amdgcn_readfirstlane(max(ulo, wq0 - wl));
-    const int whi = __builtin_amdgcn_readfirstlane(min(p.seg ? p.seg[2 * wql + 1] : n, wql + wl + 1));
+    const int whi = __builtin_amdgcn_readfirstlane(min(uhi, wql + wl + 1));
     half8 qf[2];
     {
         const f16* qp = (const f16*)p.qkv + (size_t)qc * ld + h * 64 + 8 * g;
