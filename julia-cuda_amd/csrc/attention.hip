@@ -33,12 +33,12 @@ __global__ __launch_bounds__(256) void attention_stream_kernel(AttnParams p) {
     attention_stream_tile(p, blockIdx.x, lds);
 }
 
-// The streaming tile with two key groups of NW waves (one long sequence on a grid of about a
-// block a CU). Dynamic LDS: 2 ATT_STREAM_LDS.
-template <int NW>
-__global__ __launch_bounds__(128 * NW) void attention_stream2_kernel(AttnParams p) {
+// The streaming tile with KS key groups of NW waves (one long sequence on a grid of about a
+// block a CU). Dynamic LDS: KS ATT_STREAM_LDS.
+template <int NW, int KS>
+__global__ __launch_bounds__(64 * NW * KS) void attention_streamk_kernel(AttnParams p) {
     extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
-    attention_stream_tile<false, NW, 2>(p, blockIdx.x, lds_dyn);
+    attention_stream_tile<false, NW, KS>(p, blockIdx.x, lds_dyn);
 }
 
 __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
@@ -68,10 +68,12 @@ bool attention_prepare() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, att_lds_bytes(512, 4)) == hipSuccess &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(attention_lds_kernel<8>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, att_lds_bytes(512, 8)) == hipSuccess &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(attention_stream2_kernel<2>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(attention_streamk_kernel<2, 2>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, 2 * ATT_STREAM_LDS) == hipSuccess &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(attention_stream2_kernel<4>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 2 * ATT_STREAM_LDS) == hipSuccess;
+        hipFuncSetAttribute(reinterpret_cast<const void*>(attention_streamk_kernel<4, 2>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 2 * ATT_STREAM_LDS) == hipSuccess &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(attention_streamk_kernel<4, 4>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 4 * ATT_STREAM_LDS) == hipSuccess;
     return ok;
 }
 
@@ -145,10 +147,14 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
     //            2048 rows 98 / 68   | 30.1 / 27.5 / 28.8   4096 rows (4 x 2 / 4 x 1) 85.4 / 82.5
     //   +-64     700 rows  4.9 / 6.6 | 5.0 / 5.1 / 5.0      1024 rows 5.3 / 7.1 | 5.3 / 5.3 / 5.0
     //            1536 rows 7.9 / 10.4 | 7.9 / 6.8 / 6.1
+    // and four key groups of four waves (one 1024-thread block a CU) against 2 x 2 / 4 x 2:
+    //   global   448 rows 6.9 against 5.6 / 6.7     768 rows 8.8 against 8.9 / 9.0
+    //            1024 rows 10.5 against 11.1 / 11.0  1536 rows 25.4 against 24.1 / 22.4
     // so the slice tile below 293 rows (global) or 768 (window), else the streaming tile: two
-    // key groups of two waves while that grid fits the CUs, of four while the four-wave grid is
-    // at most two blocks a CU (global), one group of four otherwise (config 5's batch: 4 x 1
-    // 48 us a global layer against 59 for 4 x 2).
+    // key groups of two waves while that grid fits the CUs, then four groups of four while
+    // their grid does, two of four while the four-wave grid is at most two blocks a CU
+    // (global), one group of four otherwise (config 5's batch: 4 x 1 48 us a global layer
+    // against 59 for 4 x 2).
     const int cus = device_cus();
     const long grid64 = (long)(n + 63) / 64 * (d / 64), grid32 = (long)(n + 31) / 32 * (d / 64);
     const bool slice = chunks == 1 && (window == 0 ? n < 293 : n <= 768);
@@ -161,11 +167,13 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
         else
             hipLaunchKernelGGL(attention_lds_kernel<4>, grid, dim3(256), att_lds_bytes(gkeys, 4), st, p, gkeys);
     } else if (chunks == 1) {
-        if (!attention_prepare()) fail("the two-group streaming kernels cannot have their LDS");
+        if (!attention_prepare()) fail("the multi-group streaming kernels cannot have their LDS");
         if (window == 0 && grid32 <= cus)
-            hipLaunchKernelGGL(attention_stream2_kernel<2>, dim3(grid32), dim3(256), 2 * ATT_STREAM_LDS, st, p);
+            hipLaunchKernelGGL((attention_streamk_kernel<2, 2>), dim3(grid32), dim3(256), 2 * ATT_STREAM_LDS, st, p);
+        else if (window == 0 && grid64 <= cus)
+            hipLaunchKernelGGL((attention_streamk_kernel<4, 4>), dim3(grid64), dim3(1024), 4 * ATT_STREAM_LDS, st, p);
         else if (window == 0 && grid64 <= 2 * cus)
-            hipLaunchKernelGGL(attention_stream2_kernel<4>, dim3(grid64), dim3(512), 2 * ATT_STREAM_LDS, st, p);
+            hipLaunchKernelGGL((attention_streamk_kernel<4, 2>), dim3(grid64), dim3(512), 2 * ATT_STREAM_LDS, st, p);
         else
             hipLaunchKernelGGL(attention_stream_kernel, dim3(grid64), dim3(256), 0, st, p);
     } else {

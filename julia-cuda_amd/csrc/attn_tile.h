@@ -469,12 +469,13 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
 // queries, and with four blocks a CU (32 KB of LDS and 108 registers a lane each) the waves
 // hide each other's step latencies.
 //
-// KS = 2 (one long sequence, a grid of about a block a CU): the block has two groups of NW
-// waves, each running the online softmax of the same NW x 16 queries over every other key
-// block (group g takes blocks g, g + 2, ...) through its own stage ring, in lockstep (one
-// block barrier a step for both); group 1's running max, sum and output then go through LDS
-// and group 0 merges them (in group order: deterministic). Two waves a SIMD instead of one
-// hide each other's step latencies where the grid leaves the CUs a block each.
+// KS = 2 or 4 (one long sequence, a grid of about a block a CU): the block has KS groups of NW
+// waves, each running the online softmax of the same NW x 16 queries over every KS-th key
+// block (group g takes blocks g, g + KS, ...) through its own stage ring, in lockstep (one
+// block barrier a step for all); groups 1 .. KS - 1 then pass their running max, sum and
+// output through LDS and group 0 merges them (in group order: deterministic). Two or four
+// waves a SIMD instead of one hide each other's step latencies where the grid leaves the CUs
+// a block each, and the chain of steps is KS times shorter.
 constexpr int ATT_STREAM_STAGES = 2;
 constexpr int ATT_STREAM_LDS = ATT_STREAM_STAGES * 16384;
 
@@ -483,7 +484,7 @@ constexpr int ATT_STREAM_LDS = ATT_STREAM_STAGES * 16384;
 // kernel). Ends with a block barrier.
 template <bool XS = false, int NW = 4, int KS = 1>
 __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int task, char* lds) {
-    static_assert(KS == 1 || KS == 2, "key groups");
+    static_assert(KS == 1 || KS == 2 || KS == 4, "key groups");
     constexpr int NS = ATT_STREAM_STAGES, QB = 16 * NW;
     constexpr int LOADS = 16 / NW;  // 1 KB copies a wave per stage
     static_assert(NW == 2 || NW == 4 || NW == 8, "waves");
@@ -691,12 +692,14 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
         if (b + 1 < nsteps) step(b + 1, std::integral_constant<int, 1>{});
     }
 
-    if (KS == 2) {
-        // Group 1's running max, sum and unnormalised output into the first ring (every wave is
-        // done with the stages: the barrier), group 0 merges them with its own.
-        float* mg = (float*)lds + (size_t)w * 18 * 64;
+    if (KS > 1) {
+        // Groups 1 .. KS - 1: running max, sum and unnormalised output into the first rings
+        // (every wave is done with the stages: the barrier); group 0 merges them with its own,
+        // in group order (deterministic).
+        auto slot = [&](int k) { return (float*)lds + (size_t)((k - 1) * NW + w) * 18 * 64; };
         __syncthreads();
-        if (kg == 1) {
+        if (kg > 0) {
+            float* mg = slot(kg);
             mg[16 * 64 + l] = mx;
             mg[17 * 64 + l] = lsum;
 #pragma unroll
@@ -705,16 +708,29 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
                 for (int e = 0; e < 4; e++) mg[(4 * dt + e) * 64 + l] = oacc[dt][e];
         }
         __syncthreads();
-        if (kg == 1) return;  // (its threads take no further barrier)
-        const float m1 = mg[16 * 64 + l], l1 = mg[17 * 64 + l];
-        const float m = fmaxf(mx, m1);
+        if (kg > 0) return;  // (their threads take no further barrier)
+        float mk[KS];
+        mk[0] = mx;
+#pragma unroll
+        for (int k = 1; k < KS; k++) mk[k] = slot(k)[16 * 64 + l];
+        float m = mx;
+#pragma unroll
+        for (int k = 1; k < KS; k++) m = fmaxf(m, mk[k]);
         const float base = m == -INFINITY ? 0.0f : m;
-        const float a0 = fast_exp2(mx - base), a1 = fast_exp2(m1 - base);
-        lsum = lsum * a0 + l1 * a1;
+        const float a0 = fast_exp2(mx - base);
+        lsum = lsum * a0;
 #pragma unroll
-        for (int dt = 0; dt < 4; dt++)
+        for (int dt = 0; dt < 4; dt++) oacc[dt] = oacc[dt] * a0;
 #pragma unroll
-            for (int e = 0; e < 4; e++) oacc[dt][e] = oacc[dt][e] * a0 + mg[(4 * dt + e) * 64 + l] * a1;
+        for (int k = 1; k < KS; k++) {
+            const float* mg = slot(k);
+            const float ak = fast_exp2(mk[k] - base);
+            lsum += mg[17 * 64 + l] * ak;
+#pragma unroll
+            for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) oacc[dt][e] += mg[(4 * dt + e) * 64 + l] * ak;
+        }
     }
 
     const float tot = sum_xor32(sum_xor16(lsum));
@@ -729,7 +745,7 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
             store8<XS>(op + 16 * dt, ov);
         }
     }
-    if (KS == 1) __syncthreads();  // LDS is free again (KS = 2: the caller's kernel ends here)
+    if (KS == 1) __syncthreads();  // LDS is free again (KS > 1: the caller's kernel ends here)
 }
 
 }  // namespace jh
