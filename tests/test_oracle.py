@@ -274,3 +274,60 @@ def test_checks_reject_a_two_ulp_embed_error():
     bad = x.copy()
     bad[5, 100] += 2
     assert O.ulps(x, x).max() == 0 and O.ulps(bad, x).max() == 2
+
+
+def _np_layernorm64(x, gamma, eps):
+    """LayerNorm of each row in float64 with numpy alone (no oracle code), weight gamma, no bias."""
+    x = np.asarray(x, np.float64)
+    mu = x.mean(axis=1, keepdims=True)
+    var = ((x - mu) ** 2).mean(axis=1, keepdims=True)
+    return (x - mu) / np.sqrt(var + eps) * np.asarray(gamma, np.float64)
+
+
+def _f16_bits(x):
+    return np.asarray(x, np.float64).astype(np.float16).view(np.uint16)
+
+
+def test_emu_embed_is_the_layernorm_of_the_table_rows():
+    """The f16 emulation of embed (oracle_emu_embed) against numpy's float64 LayerNorm of the
+    gathered table rows, rounded once to f16: at most one f16 step apart (the emulation computes
+    in f32), and a dropped gamma or a wrong row is caught."""
+    rng = np.random.default_rng(21)
+    d, vocab = 384, 200
+    table16 = rand16(rng, (vocab, d), std=2.0, mean=0.3)
+    gamma = (1 + 0.2 * rng.standard_normal(d)).astype(np.float32)
+    ids = rng.integers(0, vocab, 64).astype(np.uint32)
+    eps = 1e-5
+    emu = O.emu_embed(table16, gamma, ids, eps)
+    ref = _f16_bits(_np_layernorm64(f32(table16)[ids], gamma, eps))
+    assert O.ulps(emu, ref).max() <= 1
+    no_gamma = _f16_bits(_np_layernorm64(f32(table16)[ids], np.ones(d), eps))
+    assert O.ulps(emu, no_gamma).max() > 1
+    shifted = _f16_bits(_np_layernorm64(f32(table16)[(ids + 1) % vocab], gamma, eps))
+    assert O.ulps(emu, shifted).max() > 1
+
+
+def test_emu_norm_add_is_layernorm_plus_the_added_vector_with_stored_value_stats():
+    """The f16 emulation of norm_add against numpy: float64 LayerNorm times gamma plus the added
+    vector, rounded once to f16 (within one f16 step and 2^-10 relative), and its per-(row, 64-column) sums
+    and sums of squares taken over the stored f16 values; a dropped add is caught."""
+    rng = np.random.default_rng(22)
+    n, d = 48, 768
+    x16 = rand16(rng, (n, d), std=3.0, mean=0.5)
+    gamma = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    add = (0.5 * rng.standard_normal(d)).astype(np.float32)
+    eps = 1e-5
+    out, st = O.emu_norm_add(x16, gamma, add, eps)
+    ref64 = _np_layernorm64(f32(x16), gamma, eps) + add.astype(np.float64)
+    ref = _f16_bits(ref64)
+    # LN(x) . gamma + add cancels to small values in places, where the emulation's f32 rounding
+    # moves a value by more than one of its tiny f16 steps: bound the value error instead there
+    u = O.ulps(out, ref)
+    assert (u > 1).mean() < 2e-3
+    err = np.abs(out.view(np.float16).astype(np.float64) - ref64)
+    assert np.all(err <= np.maximum(np.abs(ref64) * 2.0 ** -10, 1e-5))
+    stored = out.view(np.float16).astype(np.float64).reshape(n, d // 64, 64)
+    np.testing.assert_allclose(st[..., 0], stored.sum(axis=2), rtol=1e-5, atol=1e-4)
+    np.testing.assert_allclose(st[..., 1], (stored ** 2).sum(axis=2), rtol=1e-5, atol=1e-4)
+    no_add = _f16_bits(_np_layernorm64(f32(x16), gamma, eps))
+    assert O.ulps(out, no_add).max() > 1
