@@ -59,10 +59,11 @@ def run(torch, P, bm, splits, scratch):
     return f16_bits(c), (st.cpu().numpy() if st is not None else None)
 
 
-# (kind, n, k, bm, splits, first m, second m): every split count the latency tiles take, and the
-# chooser's pick (bm 0).
+# (kind, n, k, bm, splits, first m, second m): every split count the latency tiles take, the
+# throughput tiles' K split (128 x 128 and 192 x 256), and the chooser's pick (bm 0).
 CASES = [("resstats", 768, 1152, 32, 4, 512, 200), ("lngeglu", 2304, 768, 48, 2, 448, 100),
          ("lnrope", 2304, 768, 16, 3, 293, 72), ("resstats", 768, 768, 64, 2, 1024, 333),
+         ("resstats", 768, 1152, 128, 2, 1100, 600), ("lngeglu", 2304, 768, 192, 2, 1000, 400),
          ("lnrope", 2304, 768, 0, 1, 293, 72)]
 
 
