@@ -325,9 +325,18 @@ __device__ __forceinline__ int xcd_task(int b, int T) {
 // of a row with k <= 1024; epi_apply loads the rest of a wider row itself.
 constexpr int EPI_PRE_SLOTS = 2;
 
-struct EpiCol {  // per column: colsum (LN) and bias, lo and hi halves
+struct EpiCol {  // per column: colsum (LN), bias and the score's weights, lo and hi halves
     float4 cs[2], bs[2];
+    half4 sw[2];
 };
+
+// The source row of output row r (r < m): rows[r] with a gather (clamped to the source's rows).
+// (A compile-time choice: a load under a run-time branch would make the compiler wait for every
+// load issued before it.)
+template <int EPI>
+__device__ __forceinline__ int src_row(const GemmParams& p, int r) {
+    return (EPI & EPI_GATHER) ? (int)min(p.rows[r], (uint32_t)(p.src_m - 1)) : r;
+}
 struct EpiRow {  // per row: statistics slots, position, RoPE (cos, sin) pairs, residual lo, hi
     float2 st[EPI_PRE_SLOTS];
     int pos;
@@ -346,16 +355,20 @@ __device__ __forceinline__ void epi_load_col(const GemmParams& p, int grp, int c
         e.bs[0] = *(const float4*)(p.bias + gcol + c0);
         e.bs[1] = *(const float4*)(p.bias + gcol + 32 + c0);
     }
+    if (EPI & EPI_SCORE) {
+        e.sw[0] = *(const half4*)((const f16*)p.score_w + gcol + c0);
+        e.sw[1] = *(const half4*)((const f16*)p.score_w + gcol + 32 + c0);
+    }
 }
 
 // XS: the statistics are read device-coherent; XR: the residual rows are.
 template <int EPI, bool XS, bool XR = XS>
 __device__ __forceinline__ void epi_load_row(const GemmParams& p, int row, int grp, int c0,
                                              EpiRow& e) {
-    const int r = min(row, p.m - 1);
+    const int r = min(row, p.m - 1), rs = src_row<EPI>(p, r);
     if (EPI & EPI_LN) {
         const int slots = p.k >> 6, j = c0 >> 2;
-        const float* st = p.stats_in + (size_t)r * slots * 2;
+        const float* st = p.stats_in + (size_t)rs * slots * 2;
 #pragma unroll
         for (int i = 0; i < EPI_PRE_SLOTS; i++) e.st[i] = load8f<XS>(st + 2 * min(j + 8 * i, slots - 1));
     }
@@ -367,7 +380,7 @@ __device__ __forceinline__ void epi_load_row(const GemmParams& p, int row, int g
         e.pos = p.pos ? v : r;
     }
     if ((EPI & EPI_RES) && !(EPI & EPI_GEGLU)) {
-        const f16* x = (const f16*)(p.res ? p.res : p.c) + (size_t)r * p.n + grp * 64 + c0;
+        const f16* x = (const f16*)(p.res ? p.res : p.c) + (size_t)(p.res ? rs : r) * p.n + grp * 64 + c0;
         e.rl = load8h<XR>(x);
         e.rh = load8h<XR>(x + 32);
     }
@@ -395,7 +408,7 @@ __device__ __forceinline__ void epi_apply(const GemmParams& p, int row, int grp,
 #pragma unroll
         for (int i = 0; i < EPI_PRE_SLOTS; i++)
             if (j + 8 * i < slots) S += er.st[i].x, Q += er.st[i].y;
-        const float* st = p.stats_in + (size_t)min(row, p.m - 1) * slots * 2;
+        const float* st = p.stats_in + (size_t)src_row<EPI>(p, min(row, p.m - 1)) * slots * 2;
         for (int s = j + 8 * EPI_PRE_SLOTS; s < slots; s += 8) {  // rows wider than 1024
             const float2 sq = load8f<XG>(st + 2 * s);
             S += sq.x, Q += sq.y;
@@ -460,7 +473,14 @@ __device__ __forceinline__ void epi_apply(const GemmParams& p, int row, int grp,
             lo[e] = (f16)v[e];
             hi[e] = (f16)v[4 + e];
         }
-        if (valid) {
+        if (EPI & EPI_SCORE) {  // the row's partial dot product over the tile's 64 columns
+            float s = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                s += (float)lo[e] * (float)ec.sw[0][e] + (float)hi[e] * (float)ec.sw[1][e];
+            s = group_sum<8>(s);
+            if (valid && (threadIdx.x & 7) == 0) xstore32(p.ws + (size_t)row * p.tiles_n + grp, s);
+        } else if (valid) {
             store8<XG>(out, lo);
             store8<XG>(out + 32, hi);
         }

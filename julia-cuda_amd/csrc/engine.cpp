@@ -311,12 +311,22 @@ struct Engine {
         norm_add_launch(xin, n, d, f(layout.final_norm), add, cfg.norm_eps, hx, stats_a, stream,
                         row_type);
         const bool compact = !all_rows && nm < n;
+        const size_t L = layout.head.size();
+        const Scorer& S = layout.scorer;
+        // With fewer markers than rows the head's last steps run on the marker rows alone. The
+        // GEMM that first reads them gathers them itself (EPI_GATHER: out_proj of the last head
+        // layer, or the scorer's lin1 without head layers), and the score rides on lin1's
+        // epilogue (EPI_SCORE), where the chooser gives those GEMMs latency tiles (lin1 without
+        // a K split); otherwise a gather kernel and a score kernel run.
+        auto lat = [&](GemmConfig c) { return c.bm < 128; };
+        const GemmConfig cs = compact ? gemm_choose(nm, d, d, cus, EPI_K_LNBIASGELU) : GemmConfig{};
+        const bool fold = compact && lat(cs) && cs.splits == 1 &&
+                          (L == 0 || lat(gemm_choose(nm, d, d, cus, EPI_K_BIASRESSTATS)));
         // The marker rows' residual stream: x is free once norm_add has read the encoder's
         // output; their attention output goes to qkv (free once attention has read it).
         jh_half* hr = hx;
         int m = n;
-        const size_t L = layout.head.size();
-        if (compact && L == 0) {  // straight into the scorer: its LN statistics go along
+        if (compact && L == 0 && !fold) {  // straight into the scorer: its LN statistics go along
             gather_rows_launch(hx, nullptr, stats_a, n, d, markers, nm, x, nullptr, stats_b, stream);
             hr = x, m = nm;
         }
@@ -326,19 +336,37 @@ struct Engine {
                  cfg.head_eps, f(H.in_proj_b), nullptr, nullptr);
             attention_launch(qkv, o, n, d, 0, attention_chunks(n, d, 0, cus), scratch, stream,
                              seg);
-            const jh_half* ao = o;
-            if (compact && i + 1 == L) {
-                gather_rows_launch(o, hx, nullptr, n, d, markers, nm, qkv, x, nullptr, stream);
-                ao = qkv, hr = x, m = nm;
+            if (compact && i + 1 == L && fold) {  // out_proj on the marker rows of o and hx
+                Gemm g{};
+                g.epi = EPI_K_BIASRESSTATS | EPI_GATHER, g.a = o, g.w = h(H.out_proj), g.c = x;
+                g.m = nm, g.n = d, g.k = d, g.bias = f(H.out_proj_b), g.stats_out = stats_b;
+                g.res = hx, g.rows = markers, g.src_m = n;
+                gemm_launch(g, gemm_choose(nm, d, d, cus, g.epi), scratch, stream);
+                hr = x, m = nm;
+            } else {
+                const jh_half* ao = o;
+                if (compact && i + 1 == L) {
+                    gather_rows_launch(o, hx, nullptr, n, d, markers, nm, qkv, x, nullptr, stream);
+                    ao = qkv, hr = x, m = nm;
+                }
+                gemm(EPI_K_BIASRESSTATS, ao, h(H.out_proj), hr, m, d, d, nullptr, nullptr, 0.0f,
+                     f(H.out_proj_b), nullptr, stats_b);
             }
-            gemm(EPI_K_BIASRESSTATS, ao, h(H.out_proj), hr, m, d, d, nullptr, nullptr, 0.0f,
-                 f(H.out_proj_b), nullptr, stats_b);
             gemm(EPI_K_LNBIASRELU, hr, h(H.linear1), mid, m, F, d, stats_b, f(H.linear1_colsum),
                  cfg.head_eps, f(H.linear1_b), nullptr, nullptr);
             gemm(EPI_K_BIASRESSTATS, mid, h(H.linear2), hr, m, d, F, nullptr, nullptr, 0.0f,
                  f(H.linear2_b), nullptr, stats_a);
         }
-        const Scorer& S = layout.scorer;
+        if (fold) {  // lin1 and the score in one launch (without head layers: from hx's rows)
+            Gemm g{};
+            g.epi = EPI_K_LNBIASGELU_SCORE | (L == 0 ? EPI_GATHER : 0), g.a = L == 0 ? hx : hr;
+            g.w = h(S.lin1), g.c = o, g.m = nm, g.n = d, g.k = d, g.stats_in = stats_a;
+            g.colsum = f(S.lin1_colsum), g.eps = cfg.head_eps, g.bias = f(S.lin1_b);
+            g.score_w = h(S.lin2), g.score_b = S.lin2_b, g.logits = logits;
+            if (L == 0) g.rows = markers, g.src_m = n;
+            gemm_launch(g, cs, scratch, stream);
+            return;
+        }
         const float* st = compact && L == 0 ? stats_b : stats_a;
         gemm(EPI_K_LNBIASGELU, hr, h(S.lin1), o, m, d, d, st, f(S.lin1_colsum), cfg.head_eps,
              f(S.lin1_b), nullptr, nullptr);
@@ -510,6 +538,8 @@ Engine* load_engine(const char* dir, size_t max_length, size_t batch_rows = 0) {
     if (!attention_prepare()) throw std::runtime_error("attention: cannot set the kernel's LDS size");
     ws = std::max(ws, e->layer_kernel.ws_floats((int)n, (int)d, c.inter, c.head_ff));
     counters = std::max(counters, e->layer_kernel.counters((int)n, (int)d, c.inter, c.head_ff));
+    ws = std::max(ws, n * (d / 64));  // the score's partials: up to a marker a row
+    counters = std::max<size_t>(counters, 1);
     e->scratch.ws = dalloc<float>(ws, "scratch");
     e->scratch.ws_floats = ws;
     counters = (counters + 31) / 32 * 32;  // the barrier's words start on a 128-byte line

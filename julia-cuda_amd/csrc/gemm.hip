@@ -133,6 +133,21 @@ void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
     if (!aligned(g.a, 16) || !aligned(g.w, 16) || !aligned(g.c, 16))
         fail("a, w and c must be 16-byte aligned");
     if ((const void*)g.a == (const void*)g.c) fail("c may not alias a");
+    if (g.res && (!(g.epi & EPI_RES) || !aligned(g.res, 16) || (const void*)g.res == (const void*)g.c))
+        fail("a separate residual goes with the residual epilogues, 16-byte aligned, not c");
+    const bool gather = g.epi & EPI_GATHER, score = g.epi & EPI_SCORE;
+    if (gather != (g.rows != nullptr) || (gather && (tput || g.src_m < 1)))
+        fail("gathered rows go with the gather epilogues on the latency tiles, from src_m >= 1 rows");
+    if (gather && (g.epi & EPI_RES) && !g.res) fail("gathered rows need a separate residual");
+    if (score != (g.score_w != nullptr && g.logits != nullptr))
+        fail("score weights and logits go with the score epilogue");
+    if (score && (tput || cfg.splits != 1 || (g.epi & (EPI_GEGLU | EPI_RES | EPI_STATS)) ||
+                  !aligned(g.score_w, 8)))
+        fail("the score takes latency tiles without a K split, no GeGLU, residual or statistics, "
+             "and 8-byte aligned weights");
+    if (score && ((size_t)g.m * (g.n / 64) > s.ws_floats || s.n_counters < 1 || !s.ws || !s.counters))
+        fail("the score's partials need " + std::to_string((size_t)g.m * (g.n / 64)) +
+             " floats of scratch and a counter");
     const bool ln = g.epi & EPI_LN;
     if (ln != (g.stats_in && g.colsum)) fail("LayerNorm inputs go with the ln epilogues");
     if (ln && (!aligned(g.colsum, 16) || !aligned(g.stats_in, 8)))
@@ -174,22 +189,39 @@ static void launch_big(const GemmParams& p, hipStream_t st) {
 }
 
 template <int BM, int EPI>
-static void launch_one(const GemmParams& p, hipStream_t st) {
+static void launch_lat(const GemmParams& p, hipStream_t st) {
     const int blocks = p.tiles_n * p.tiles_m * p.splits;
+    if (p.splits == 1 && blocks <= device_cus()) {
+        constexpr int LDS = lat_lds_floats<BM, 8>() * 4;
+        static const bool lds_ok =  // once per instantiation, before its first launch
+            hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_lat1<BM, EPI>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS) == hipSuccess;
+        if (!lds_ok) throw std::runtime_error("gemm: the one-block latency kernel cannot have its LDS");
+        hipLaunchKernelGGL((gemm_lat1<BM, EPI>), dim3(blocks), dim3(512), LDS, st, p);
+    } else {
+        hipLaunchKernelGGL((gemm_lat<BM, EPI>), dim3(blocks), dim3(256), 0, st, p);
+    }
+}
+
+template <int BM, int EPI>
+static void launch_one(const GemmParams& p, hipStream_t st) {
     if (BM >= 128) {
         constexpr int B = BM >= 128 ? BM : 128;
         if (p.splits > 1) launch_big<B, EPI, true>(p, st);
         else launch_big<B, EPI, false>(p, st);
-    } else if (p.splits == 1 && blocks <= device_cus()) {
-        constexpr int B = BM < 128 ? BM : 64;
-        constexpr int LDS = lat_lds_floats<B, 8>() * 4;
-        static const bool lds_ok =  // once per instantiation, before its first launch
-            hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_lat1<B, EPI>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS) == hipSuccess;
-        if (!lds_ok) throw std::runtime_error("gemm: the one-block latency kernel cannot have its LDS");
-        hipLaunchKernelGGL((gemm_lat1<B, EPI>), dim3(blocks), dim3(512), LDS, st, p);
     } else {
-        hipLaunchKernelGGL((gemm_lat<BM < 128 ? BM : 64, EPI>), dim3(blocks), dim3(256), 0, st, p);
+        launch_lat<BM < 128 ? BM : 64, EPI>(p, st);
+    }
+}
+
+// The epilogues only the latency tiles take (the score, gathered rows).
+template <int EPI>
+static void launch_epi_lat(const GemmParams& p, int bm, hipStream_t st) {
+    switch (bm) {
+        case 16: launch_lat<16, EPI>(p, st); break;
+        case 32: launch_lat<32, EPI>(p, st); break;
+        case 48: launch_lat<48, EPI>(p, st); break;
+        default: launch_lat<64, EPI>(p, st); break;
     }
 }
 
@@ -211,7 +243,9 @@ void gemm_launch(const Gemm& g, GemmConfig cfg, const Scratch& s, hipStream_t st
     GemmParams p{};
     p.a = g.a, p.w = g.w, p.c = g.c;
     p.stats_in = g.stats_in, p.colsum = g.colsum, p.bias = g.bias, p.rope = g.rope, p.pos = g.pos;
-    p.stats_out = g.stats_out, p.ws = s.ws, p.counters = s.counters;
+    p.stats_out = g.stats_out, p.ws = s.ws, p.counters = s.counters, p.res = g.res;
+    p.rows = g.rows, p.src_m = g.src_m;
+    p.score_w = g.score_w, p.score_b = g.score_b, p.logits = g.logits;
     p.m = g.m, p.n = g.n, p.k = g.k, p.eps = g.eps;
     p.rope_cols = (g.epi & EPI_ROPE) ? 2 * (g.n / 3) : 0;
     p.rope_rows = g.rope_rows;
@@ -227,6 +261,13 @@ void gemm_launch(const Gemm& g, GemmConfig cfg, const Scratch& s, hipStream_t st
         case EPI_K_LNBIASRELU: launch_epi<EPI_K_LNBIASRELU>(p, cfg.bm, st); break;
         case EPI_K_LNBIASGELU: launch_epi<EPI_K_LNBIASGELU>(p, cfg.bm, st); break;
         case EPI_K_BIASRESSTATS: launch_epi<EPI_K_BIASRESSTATS>(p, cfg.bm, st); break;
+        case EPI_K_BIASRESSTATS | EPI_GATHER:
+            launch_epi_lat<EPI_K_BIASRESSTATS | EPI_GATHER>(p, cfg.bm, st);
+            break;
+        case EPI_K_LNBIASGELU_SCORE: launch_epi_lat<EPI_K_LNBIASGELU_SCORE>(p, cfg.bm, st); break;
+        case EPI_K_LNBIASGELU_SCORE | EPI_GATHER:
+            launch_epi_lat<EPI_K_LNBIASGELU_SCORE | EPI_GATHER>(p, cfg.bm, st);
+            break;
         case 0: launch_epi<0>(p, cfg.bm, st); break;
         default: throw std::runtime_error("gemm: no kernel for epilogue " + std::to_string(g.epi));
     }

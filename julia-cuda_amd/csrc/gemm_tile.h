@@ -75,6 +75,28 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
         const int row = row0 + r;
         epi_apply<EPI, XG>(p, row, grp, c0, v[ps], r < rows_in_tile && row < p.m, ec, er[ps]);
     }
+    if (EPI & EPI_SCORE) {
+        // Every tile's partials are stored (device-coherent) before its arrival counts; the last
+        // tile to arrive (which resets the counter) sums each row's partials in column order.
+        release_wait();
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t old = atomic_add_agent(p.counters, 1u);
+            const uint32_t last = old == (uint32_t)(p.tiles_n * p.tiles_m - 1);
+            if (last) atomic_store_agent(p.counters, 0u);
+            *s_last = last;
+        }
+        __syncthreads();
+        const uint32_t last = *s_last;
+        __syncthreads();  // every thread has read s_last before anyone can write it again
+        if (last) {
+            for (int r = tid; r < p.m; r += NT) {
+                float acc = 0.0f;
+                for (int t = 0; t < p.tiles_n; t++) acc += xload32(p.ws + (size_t)r * p.tiles_n + t);
+                p.logits[r] = acc + p.score_b;
+            }
+        }
+    }
 }
 
 // Task `task` (of tiles_n * tiles_m * splits; XCD-mapped) of c = epilogue(a . w^T). The NW
@@ -109,7 +131,7 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
 #pragma unroll
     for (int i = 0; i < MI; i++) {
         const int row = min(by * BM + 16 * i + r16, p.m - 1);  // rows past m: read, never stored
-        ap[i] = (const f16*)p.a + (size_t)row * p.k + 8 * g;
+        ap[i] = (const f16*)p.a + (size_t)src_row<EPI>(p, row) * p.k + 8 * g;
     }
     // The epilogue's other inputs, in flight with the first operand loads.
     const int c0 = (tid & 7) * 4;

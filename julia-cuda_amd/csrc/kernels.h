@@ -22,6 +22,13 @@ enum {
     EPI_BIAS = 32,
     EPI_RELU = 64,
     EPI_GELU = 128,
+    // Not in the reference's set: the score folded into the scorer's lin1 (each row's logit,
+    // the dot product of its f16 outputs with one weight row, plus a bias; the outputs are not
+    // stored). Latency tiles without a K split only.
+    EPI_SCORE = 256,
+    // Not in the reference's set either: the rows of a, the residual and the input statistics
+    // gathered through an index list (GemmParams::rows). Latency tiles only.
+    EPI_GATHER = 512,
 };
 
 // The eight epilogue combinations the model uses (src/gemm.rs:56-124).
@@ -34,6 +41,7 @@ enum {
     EPI_K_LNBIASRELU = EPI_LN | EPI_BIAS | EPI_RELU,
     EPI_K_LNBIASGELU = EPI_LN | EPI_BIAS | EPI_GELU,
     EPI_K_BIASRESSTATS = EPI_BIAS | EPI_RES | EPI_STATS,
+    EPI_K_LNBIASGELU_SCORE = EPI_K_LNBIASGELU | EPI_SCORE,
 };
 
 // c = epilogue(a . w^T): a [m][k], w [n][k], c [m][n] ([m][n/2] with GeGLU), f16; f32 math.
@@ -58,6 +66,16 @@ struct GemmParams {
     int rope_rows;          // positions in the RoPE table (positions are clamped to it)
     int splits;
     int tiles_n, tiles_m;
+    // EPI_GATHER: row r of a, of the residual and of stats_in is row rows[r] of those buffers
+    // (src_m rows each, indices clamped to them); c and stats_out keep row r.
+    const uint32_t* rows;
+    int src_m;
+    // EPI_SCORE: logits[r] = (f16 row r of the output) . score_w + score_b. Each tile leaves
+    // its rows' partial dot products in ws ([m][tiles_n]); the last tile to finish (counters[0],
+    // reset by it) sums them in column order.
+    const jh_half* score_w;
+    float score_b;
+    float* logits;
 };
 
 // Attention over qkv [n][3 d] (heads of 64, rows [q | k | v]) into o [n][d].
@@ -105,6 +123,12 @@ struct Gemm {
     const int32_t* pos;
     int rope_rows;  // positions in the RoPE table
     float* stats_out;
+    const jh_half* res = nullptr;     // the residual rows (null: c, updated in place)
+    const uint32_t* rows = nullptr;   // GemmParams::rows, over src_m rows
+    int src_m = 0;
+    const jh_half* score_w = nullptr;  // EPI_SCORE (GemmParams)
+    float score_b = 0.0f;
+    float* logits = nullptr;
 };
 
 // Throws std::runtime_error when g or cfg break what the kernels assume.

@@ -134,7 +134,9 @@ def test_full_pass_of_max_length_requests(engine):
 def test_many_markers(engine):
     """A request may name a marker any number of times (src/engine.rs:78-81 only bounds the
     positions): more markers than max_length, through the graph path, the direct path and the
-    batched path; repeated markers give identical logits."""
+    batched path; repeated markers give identical logits. (With more markers than rows the head
+    runs on every row and the score kernel sums each logit; with fewer, on the marker rows with
+    the score summed in lin1's epilogue: the same values up to the order of the f32 sums.)"""
     e, _ = engine
     rng = np.random.default_rng(11)
     ids = rng.integers(0, SMALL["vocab"], 50).astype(np.uint32)
@@ -148,7 +150,7 @@ def test_many_markers(engine):
         if batched:  # the same request at another row offset: key blocks fall differently
             path_diff([out[1][:3], out[2]], [out[0], out[0]], "repeated request, batched")
         else:
-            np.testing.assert_array_equal(out[1][:3], out[0])
+            np.testing.assert_allclose(out[1][:3], out[0], rtol=0, atol=1e-6)
             np.testing.assert_array_equal(out[2], out[0])
 
 
