@@ -247,6 +247,10 @@ __device__ __forceinline__ void bstore16(__amdgpu_buffer_rsrc_t r, uint32_t byte
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4_t, v), r, byte_off, 0, XG ? 16 : 0);
 }
 
+// s_waitcnt lgkmcnt(0) alone: this wave's LDS (and scalar memory) operations are done; vector
+// memory operations (loads, stores) may still be in flight.
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 // s_waitcnt with vmcnt = n (n < 64) and no wait on the other counters (gfx9 encoding:
 // vmcnt[3:0] in bits 3:0 and vmcnt[5:4] in bits 15:14, expcnt in 6:4, lgkmcnt in 11:8).
 template <int N>

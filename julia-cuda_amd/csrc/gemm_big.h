@@ -562,8 +562,12 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
         }
     }
     // Every wave is done with the LDS before the block's next task (the persistent kernel runs
-    // several in a row) copies into it.
-    __syncthreads();
+    // several in a row) copies into it. A bare barrier after the wave's LDS operations: the
+    // tile's stores drain while the next tile's copies go out (__syncthreads would wait for
+    // them; when all CUs end a round at once, their stores queue for the HBM for microseconds).
+    // The next tile's stage waits count these stores too, which only makes them wait longer.
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
     mark(3);
 }
 
