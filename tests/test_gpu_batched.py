@@ -180,3 +180,26 @@ def test_batch_rows_bounds(torch_cuda):
     alone, _ = e.run(reqs)
     path_diff(got, alone, "batch_rows under max_length")
     e.close()
+
+
+def test_marker_rows_on_throughput_tiles(torch_cuda):
+    """A pass with thousands of marker rows (fewer than its rows): the chooser gives the head's
+    marker-row GEMMs throughput tiles, which neither gather rows nor carry the score, so a gather
+    kernel and the score kernel run; with a few hundred markers the GEMMs gather and score
+    themselves. Both against each request alone and the oracle."""
+    e = jh.Engine(spec(SMALL), max_length=1024, batch_rows=4096)
+    m = O.Model(O.cfg(**SMALL))
+    rng = np.random.default_rng(17)
+    for nm in (700, 90):  # 4 x 700 = 2800 marker rows: 128-row tiles; 4 x 90: latency tiles
+        assert jh.gemm_choose(4 * nm, SMALL["d"], SMALL["d"], 256, 164)[0] == (128 if nm == 700 else 16)
+        reqs = []
+        for i in range(4):
+            ids = rng.integers(0, SMALL["vocab"], 1000).astype(np.uint32)
+            reqs.append((ids, rng.integers(0, 1000, nm).astype(np.uint32), i % 3))
+        got, ms = e.run(reqs, batched=True)
+        assert np.all(ms == ms[0])
+        alone, _ = e.run(reqs)
+        path_diff(got, alone, f"{4 * nm} marker rows in one pass")
+        ids, markers, q = reqs[1]
+        check_logits(got[1][:8], m.forward(ids, q, markers[:8]), f"{4 * nm} marker rows, oracle")
+    e.close()
