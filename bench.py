@@ -359,7 +359,7 @@ def main():
     big = {}
     # (the full vocabulary: the embed rows of 18379 ids are mostly distinct table rows)
     eng_big = jh.Engine("synthetic:layers=4,max_positions=20480", max_length=18752)
-    for m in (4096, 18752):
+    for m in (4096, 8192, 18752):
         for step, (n, k, epi, _) in STEP_SHAPES.items():
             mn, md = eng_big.time_step(step, m, warmup=5, batches=5, per_batch=8)
             fl = 2 * m * n * k
