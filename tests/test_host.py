@@ -271,6 +271,15 @@ def test_gemm_check_rejects_what_the_kernels_do_not_take():
     with pytest.raises(jh.JuliaHipError, match="fewer than two K steps"):
         jh.gemm_check(jh.gemm_args("resstats", base, base + 4096, base + 8192, 512, 768, 128,
                                    stats_out=base + 256), 256, 3, ws_floats=1 << 24, counters=64)
+    # The engine's own epilogues (the score folded into the scorer's lin1, the head's gathered
+    # marker rows) take arguments the per-op ABI does not carry: through it they are refused.
+    lin1 = dict(stats_in=base + 64, colsum=base + 128, bias=base + 256)
+    with pytest.raises(jh.JuliaHipError, match="score weights and logits"):
+        jh.gemm_check(jh.gemm_args(jh.EPI["lnbiasgelu"] | 256, base, base + 4096, base + 8192, 6,
+                                   768, 768, **lin1), 16)
+    with pytest.raises(jh.JuliaHipError, match="gathered rows"):
+        jh.gemm_check(jh.gemm_args(jh.EPI["biasresstats"] | 512, base, base + 4096, base + 8192, 6,
+                                   768, 768, bias=base + 256, stats_out=base + 512), 16)
 
 
 def test_chooser_matches_the_measured_winners():
