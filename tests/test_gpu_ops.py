@@ -274,6 +274,27 @@ def test_attention_d384_and_tail(torch_cuda, scratch):
         compare(f32(f16_bits(o)), ref, ATTN_REL, what=f"attention d=384 n={n} w={window}")
 
 
+@pytest.mark.parametrize("window", [0, 64])
+def test_attention_at_the_routing_edges(torch_cuda, scratch, window):
+    """One sequence at d=768 on both sides of every size where attention_launch changes tile
+    (global: the slice tile below 293 rows, then the streaming tile with 2 x 2 waves up to 682
+    rows, 4 x 4 up to 1365, 4 x 2 up to 2730, 4 x 1 past it; window: the slice tile up to 768
+    rows, then the streaming tile), and at lengths around the 16-, 32- and 64-row block edges,
+    against the f64 attention."""
+    torch = torch_cuda
+    for n in (2, 17, 63, 64, 65, 129, 292, 293, 400, 682, 683, 768, 769, 1365, 1366, 2730, 2731):
+        rng = np.random.default_rng(900 + n + window)
+        qkv16 = rand16(rng, (n, 3 * 768))
+        ref = O.attention(f32(qkv16), window)
+        q = to_dev(torch, qkv16)
+        o = torch.full((n, 768), float("nan"), dtype=torch.float16, device="cuda")
+        jh.attention(q.data_ptr(), o.data_ptr(), n, 768, window, 1, scratch,
+                     stream=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        rel, mrel = compare(f32(f16_bits(o)), ref, ATTN_REL, what=f"attention n={n} window={window}")
+        say(f"  n={n} window={window}: vs f64 {rel:.2e} (max {mrel:.2e})")
+
+
 # ---- the bandwidth kernels ----------------------------------------------------------------
 @pytest.mark.parametrize("d", [384, 768])
 def test_embed(torch_cuda, d):
