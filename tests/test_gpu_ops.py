@@ -184,6 +184,18 @@ def test_big_tiles_every_epilogue(torch_cuda, scratch, kind, n, k, bm):
     check_gemm(P, out, st, f"{kind} M=2100 n={n} k={k} bm={bm}")
 
 
+@pytest.mark.parametrize("kind,n,k", [("lnrope", 2304, 768), ("resstats", 768, 1152),
+                                      ("lngeglu", 2304, 768), ("lnbiasgelu", 768, 768)])
+def test_chooser_at_row_edges(torch_cuda, scratch, kind, n, k):
+    """The chooser's own pick (bm = 0) at row counts around the tile heights (1, 16, 48, 256)
+    and the switch from the one-block-a-CU latency kernel to the two-a-CU one and to the
+    throughput tiles, against the f32 reference and the emulation."""
+    for m in (1, 15, 17, 47, 49, 255, 257, 1023, 2049):
+        P = gemm_problem(kind, m, n, k, seed=500 + m + n)
+        out, st = run_gemm(torch_cuda, P, 0, 1, scratch)
+        check_gemm(P, out, st, f"{kind} m={m} chosen {tuple(jh.gemm_choose(m, n, k, 256, P['epi']))}")
+
+
 # K split on the throughput tiles: the last arriver's sum in split order, then every kind of
 # epilogue (RoPE, GeGLU, residual + statistics, bias + residual), rows past m in the last band.
 SPLIT_EPIS = [("lnrope", 2304, 768), ("lngeglu", 2304, 768), ("resstats", 768, 1152),
