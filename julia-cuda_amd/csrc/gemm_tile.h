@@ -345,7 +345,7 @@ __device__ __forceinline__ void gemm_w_tile(const GemmParams& p, int task, char*
     };
     constexpr int MI = BM / 16;
     constexpr int NPASS = (BM + 31) / 32;
-    constexpr int UMAX = MI == 4 ? 6 : 9;  // a fragments one wave holds: 96 or 36-72 VGPRs
+    constexpr int UMAX = MI >= 3 ? 6 : 9;  // a fragments one wave holds: 72-96 or 36-72 VGPRs
     const int T = p.tiles_n * p.tiles_m * p.splits;
     const int L = xcd_task(task, T);
     const int z = L % p.splits, t2 = L / p.splits;

@@ -96,7 +96,7 @@ struct AttnParams {
 namespace jh {
 
 struct GemmConfig {
-    int bm;      // rows per tile: 16, 32, 64 (latency kernel) or 128, 256 (throughput kernel)
+    int bm;      // rows per tile: 16, 32, 48, 64 (latency kernel) or 128, 192, 256 (throughput kernel)
     int splits;  // K splits, 1-8
 };
 

@@ -138,6 +138,7 @@ public:
 
 private:
     int cus_ = 0, per_cu_ = 0, per_cu_big_ = 0, per_cu_big256_ = 0, lds_max_ = 0;
+    bool lat48_ok_ = false;  // the 48-row instance fits as many blocks a CU as the plain one
     uint32_t* bar_ = nullptr;  // BAR_WORDS words
     // Launch through hipLaunchCooperativeKernel (true), or as a plain launch of the same
     // resident grid: after the runtime refuses a cooperative launch because another process

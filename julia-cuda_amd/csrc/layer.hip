@@ -202,8 +202,17 @@ __device__ __forceinline__ int gemm_tasks(const GemmParams& g) {
 // 256 x 256 tiles (512 threads, one block a CU), with only the throughput tiles and the streaming
 // attention tile compiled in.
 constexpr int MODE_LAT = 0, MODE_BIG128 = 1, MODE_BIG256 = 2;
+// MODE_LAT48: MODE_LAT with the 48-row latency tile compiled in for qkv and wi, for the plans
+// that take it (an instance of its own: the code it adds shifts the register and spill layout
+// of the whole kernel, which the other plans measured slower with).
+constexpr int MODE_LAT48 = 3;
 
-// bm 16/32/64: the latency tile with its weights in LDS; 128 and 256: the throughput tiles
+// The 48-row latency tile is compiled for qkv and wi only, in MODE_LAT48 (the plans give it to
+// no other GEMM).
+template <int EPI, int MODE>
+constexpr bool T48 = MODE == MODE_LAT48 && (EPI == EPI_K_ROPE || EPI == EPI_K_LNROPE || EPI == EPI_K_LNGEGLU);
+
+// bm 16/32/48/64: the latency tile with its weights in LDS; 128 and 256: the throughput tiles
 // (large batches), which stage both operands themselves.
 template <int EPI, bool AX, int MODE>
 __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* lds, bool pre,
@@ -221,6 +230,8 @@ __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* ld
             gemm_w_tile<16, EPI, AX>(g, t, lds, ready, s_last, su);
         else if (bm == 32)
             gemm_w_tile<32, EPI, AX>(g, t, lds, ready, s_last, su);
+        else if (T48<EPI, MODE> && bm == 48)
+            gemm_w_tile<T48<EPI, MODE> ? 48 : 64, EPI, AX>(g, t, lds, ready, s_last, su);
         else
             gemm_w_tile<64, EPI, AX>(g, t, lds, ready, s_last, su);
     }
@@ -229,7 +240,7 @@ __device__ __forceinline__ void gemm_phase(const GemmParams& g, int bm, char* ld
 template <int MODE>
 __global__ __launch_bounds__(MODE == MODE_BIG256 ? 512 : 256, MODE == MODE_BIG128 ? 2 : 1)
 void encoder_kernel(EncParams P) {
-    constexpr bool BIG = MODE != MODE_LAT;
+    constexpr bool BIG = MODE == MODE_BIG128 || MODE == MODE_BIG256;
     extern __shared__ __attribute__((aligned(16))) char lds[];
     uint32_t* s_last = (uint32_t*)(lds + P.lds_main);
     uint32_t g0 = 0, nb = 0;
@@ -446,6 +457,8 @@ void LayerKernel::init(int cus, int lds_max) {
     };
     // with the largest LDS a plan may use: one block per CU
     per_cu_ = occupancy(reinterpret_cast<const void*>(encoder_kernel<MODE_LAT>), 256, lds_max);
+    lat48_ok_ = per_cu_ > 0 &&
+                occupancy(reinterpret_cast<const void*>(encoder_kernel<MODE_LAT48>), 256, lds_max) >= per_cu_;
     per_cu_big_ = occupancy(reinterpret_cast<const void*>(encoder_kernel<MODE_BIG128>), 256,
                             big_lds_bytes(128) + 16);
     per_cu_big256_ = occupancy(reinterpret_cast<const void*>(encoder_kernel<MODE_BIG256>), 512,
@@ -459,11 +472,13 @@ void LayerKernel::init(int cus, int lds_max) {
 // partial exchange. The weight tile must fit the LDS. Key ranges for global attention as the
 // per-step attention's, none for sliding-window layers (src/forward.rs:173-189's rule).
 // The latency tile's height and split-K for an m x cols x k GEMM (the cost model above).
-static void lat_tile(int m, int cols, int k, int cus, int lds_max, int& bm_out, int& splits_out) {
+static void lat_tile(int m, int cols, int k, int cus, int lds_max, int& bm_out, int& splits_out,
+                     bool allow48 = false) {
     const double bw = 67e3;  // bytes per us into one CU
     double best = 1e30;
     bm_out = 16, splits_out = k / 32 >= 8 ? 2 : 1;
-    for (int bm : {16, 32, 64}) {
+    for (int bm : {16, 32, 48, 64}) {
+        if (bm == 48 && !allow48) continue;
         for (int s = 1; s <= 4; s++) {
             if (k / 32 < 4 * s) continue;  // every wave needs a K unit
             if (w_tile_bytes(k, s) > lds_max) continue;
@@ -526,7 +541,7 @@ LayerPlan LayerKernel::default_plan(int m, int d, int inter) const {
             p.bm[g] = 128, p.splits[g] = 1;
             continue;
         }
-        lat_tile(m, cols[g], ks[g], cus_, lds_max_, p.bm[g], p.splits[g]);
+        lat_tile(m, cols[g], ks[g], cus_, lds_max_, p.bm[g], p.splits[g], lat48_ok_ && (g == 0 || g == 2));
     }
     p.kv[0] = attention_chunks(m, d, 0, cus_);
     p.kv[1] = 1;
@@ -595,8 +610,8 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
     if (phases == 0 || phases > 0x1f) fail("no phases selected");
     if (phases != 0x1f && a.count != 1) fail("a subset of the phases runs one layer only");
     for (int g = 0; g < 4; g++)
-        if (!(plan.bm[g] == 16 || plan.bm[g] == 32 || plan.bm[g] == 64 || plan.bm[g] == 128 ||
-              plan.bm[g] == 256) ||
+        if (!(plan.bm[g] == 16 || plan.bm[g] == 32 || (plan.bm[g] == 48 && lat48_ok_ && (g == 0 || g == 2)) ||
+              plan.bm[g] == 64 || plan.bm[g] == 128 || plan.bm[g] == 256) ||
             plan.splits[g] < 1 || plan.splits[g] > 4 || (plan.bm[g] >= 128 && plan.splits[g] != 1))
             fail("no such plan: " + plan.str());
     if (plan.kv[0] < 1 || plan.kv[0] > 8 || plan.kv[1] < 1 || plan.kv[1] > 8)
@@ -734,9 +749,11 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
     P.prof = prof;
 
     const int grid_blocks = grid(a, plan);
+    const bool uses48 = mode == MODE_LAT && (plan.bm[0] == 48 || plan.bm[2] == 48);
     void* args[] = {&P};
     const void* kernel = mode == MODE_BIG256   ? reinterpret_cast<const void*>(encoder_kernel<MODE_BIG256>)
                          : mode == MODE_BIG128 ? reinterpret_cast<const void*>(encoder_kernel<MODE_BIG128>)
+                         : uses48 ? reinterpret_cast<const void*>(encoder_kernel<MODE_LAT48>)
                                                : reinterpret_cast<const void*>(encoder_kernel<MODE_LAT>);
     const dim3 threads(mode == MODE_BIG256 ? 512 : 256);
     hipError_t e = hipErrorIllegalState;
