@@ -15,7 +15,7 @@ namespace jh {
 
 // u32 words of device memory the grid barrier needs (zero between launches; a launch leaves
 // them zero, and the host clears them after a barrier time-out).
-constexpr int BAR_WORDS = 11 * 32;
+constexpr int BAR_WORDS = 19 * 32;
 // u64 words per block and layer of the kernel's timestamps: (start, end) of phase p at 2p,
 // 2p + 1 (100 MHz clock), the block's CU id at 10; for the block's first attention task at 12 + i:
 // its key range in LDS, its key loop done, its output stored; and for the block's first task of

@@ -74,14 +74,18 @@ __device__ __forceinline__ void stamp_end(uint64_t* prof, int phase) {
     }
 }
 
-// The grid barrier's words, each on its own 128-byte line: eight group arrival counters, the
+// The grid barrier's words, each on its own 128-byte line: BAR_NG group arrival counters, the
 // count of groups complete, the generation, and the time-out flag.
 constexpr int BAR_LINE = 32;
-constexpr int BAR_GROUPS = 8 * BAR_LINE, BAR_GEN = 9 * BAR_LINE, BAR_TIMEOUT = 10 * BAR_LINE;
+constexpr int BAR_NG = 16;  // arrival groups (8 and 32 measured slower on 256 blocks)
+static_assert(BAR_WORDS == (BAR_NG + 3) * BAR_LINE, "the barrier's words");
+constexpr int BAR_GROUPS = BAR_NG * BAR_LINE, BAR_GEN = (BAR_NG + 1) * BAR_LINE,
+              BAR_TIMEOUT = (BAR_NG + 2) * BAR_LINE;
 
 // Barrier nb (1, 2, ... within the launch) across the grid (the reference's is
-// kernels/src/gemm.rs:435-489). Blocks arrive in eight groups (block b in group b % 8, the XCD
-// it is dispatched to), so no counter sees more than an eighth of the arrivals; the arrival that
+// kernels/src/gemm.rs:435-489). Blocks arrive in BAR_NG groups (block b in group b % BAR_NG),
+// so no counter sees more than a sixteenth of the arrivals (atomics on one word are served one
+// at a time: a single counter for 256 blocks made a 293-token forward pass 15% slower); the arrival that
 // completes group x's count for barrier nb counts the group, the one that completes the groups'
 // count advances the generation. The counters only grow within a launch (targets nb * size),
 // so an arrival is two dependent atomics at most and nobody resets anything on the way; block 0
@@ -102,8 +106,8 @@ __device__ __forceinline__ void grid_sync(uint32_t* bar, uint32_t g0, uint32_t n
     __syncthreads();
     if (threadIdx.x < 64) {
         if (threadIdx.x == 0) {
-            const uint32_t grid = gridDim.x, x = blockIdx.x & 7;
-            const uint32_t groups = grid < 8 ? grid : 8, in_group = (grid - x + 7) / 8;
+            const uint32_t grid = gridDim.x, x = blockIdx.x % BAR_NG;
+            const uint32_t groups = grid < BAR_NG ? grid : BAR_NG, in_group = (grid - x + BAR_NG - 1) / BAR_NG;
             if (atomic_add_agent(bar + x * BAR_LINE, 1u) == nb * in_group - 1)
                 if (atomic_add_agent(bar + BAR_GROUPS, 1u) == nb * groups - 1)
                     atomic_add_agent(bar + BAR_GEN, 1u);
@@ -117,7 +121,7 @@ __device__ __forceinline__ void grid_sync(uint32_t* bar, uint32_t g0, uint32_t n
                 }
             }
             if (last && blockIdx.x == 0) {
-                for (int i = 0; i < 9; i++) atomic_store_agent(bar + i * BAR_LINE, 0u);
+                for (int i = 0; i <= BAR_NG; i++) atomic_store_agent(bar + i * BAR_LINE, 0u);
             }
         }
     } else {
