@@ -331,17 +331,18 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     // arrival order, and runs the epilogue. The others are done with the task.
     if (SPLIT && S > 1) {
         constexpr int NV = MR * NC * 4;  // float4s a lane
-        float* part = p.ws + (size_t)t2 * S * NV * C::THREADS * 4;
-        float* mine = part + (size_t)z * NV * C::THREADS * 4;
+        // (one buffer descriptor over the tile's partials: 16-byte coherent stores and loads)
+        const auto part = buffer_rsrc(p.ws + (size_t)t2 * S * NV * C::THREADS * 4, S * NV * C::THREADS * 16);
+        const uint32_t mine = (uint32_t)z * NV * C::THREADS * 16;
 #pragma unroll
         for (int i = 0; i < MR; i++)
 #pragma unroll
             for (int c = 0; c < NC; c++)
 #pragma unroll
                 for (int q = 0; q < 4; q++)
-                    xstore16(mine + (((i * NC + c) * 4 + q) * C::THREADS + tid) * 4,
-                             make_float4(acc[i][c][4 * q], acc[i][c][4 * q + 1], acc[i][c][4 * q + 2],
-                                         acc[i][c][4 * q + 3]));
+                    bstore16f(part, mine + (((i * NC + c) * 4 + q) * C::THREADS + tid) * 16,
+                              make_float4(acc[i][c][4 * q], acc[i][c][4 * q + 1], acc[i][c][4 * q + 2],
+                                          acc[i][c][4 * q + 3]));
         release_wait();
         __syncthreads();
         uint32_t* s_last = (uint32_t*)lds;  // the stages' space is free here
@@ -362,14 +363,14 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
 #pragma unroll
                 for (int e = 0; e < 16; e++) acc[i][c][e] = 0.0f;
         for (int zz = 0; zz < S; zz++) {
-            const float* src = part + (size_t)zz * NV * C::THREADS * 4;
+            const uint32_t src = (uint32_t)zz * NV * C::THREADS * 16;
 #pragma unroll
             for (int i = 0; i < MR; i++)
 #pragma unroll
                 for (int c = 0; c < NC; c++)
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
-                        const float4 v4 = xload16f(src + (((i * NC + c) * 4 + q) * C::THREADS + tid) * 4);
+                        const float4 v4 = bload16f(part, src + (((i * NC + c) * 4 + q) * C::THREADS + tid) * 16);
                         acc[i][c][4 * q] += v4.x;
                         acc[i][c][4 * q + 1] += v4.y;
                         acc[i][c][4 * q + 2] += v4.z;

@@ -30,14 +30,16 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
     const int tid = threadIdx.x;
     if (p.splits > 1) {
         // [tile][split][pass][half][thread] float4s: coalesced stores and loads.
-        float* part = p.ws + (size_t)(tile_id * p.splits) * NPASS * 2 * NT * 4;
-        float* mine = part + (size_t)z * NPASS * 2 * NT * 4;
+        // (one buffer descriptor over the tile's partials: 16-byte coherent stores and loads)
+        const auto part = buffer_rsrc(p.ws + (size_t)(tile_id * p.splits) * NPASS * 2 * NT * 4,
+                                      p.splits * NPASS * 2 * NT * 16);
+        const uint32_t mine = (uint32_t)z * NPASS * 2 * NT * 16;
 #pragma unroll
         for (int ps = 0; ps < NPASS; ps++)
 #pragma unroll
             for (int h = 0; h < 2; h++)
-                xstore16(mine + ((ps * 2 + h) * NT + tid) * 4,
-                         make_float4(v[ps][4 * h], v[ps][4 * h + 1], v[ps][4 * h + 2], v[ps][4 * h + 3]));
+                bstore16f(part, mine + ((ps * 2 + h) * NT + tid) * 16,
+                          make_float4(v[ps][4 * h], v[ps][4 * h + 1], v[ps][4 * h + 2], v[ps][4 * h + 3]));
         release_wait();
         __syncthreads();
         if (tid == 0) {
@@ -55,12 +57,12 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
 #pragma unroll
             for (int e = 0; e < 8; e++) v[ps][e] = 0.0f;
         for (int zz = 0; zz < p.splits; zz++) {
-            const float* src = part + (size_t)zz * NPASS * 2 * NT * 4;
+            const uint32_t src = (uint32_t)zz * NPASS * 2 * NT * 16;
 #pragma unroll
             for (int ps = 0; ps < NPASS; ps++)
 #pragma unroll
                 for (int h = 0; h < 2; h++) {
-                    const float4 q = xload16f(src + ((ps * 2 + h) * NT + tid) * 4);
+                    const float4 q = bload16f(part, src + ((ps * 2 + h) * NT + tid) * 16);
                     v[ps][4 * h] += q.x;
                     v[ps][4 * h + 1] += q.y;
                     v[ps][4 * h + 2] += q.z;
