@@ -268,10 +268,12 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* base) {
 // The same through a buffer descriptor: the lane's 16 bytes at byte `voff` of `r` (zeros past its
 // size, with no memory access). The address is the descriptor (scalar) plus a 32-bit lane
 // offset: no 64-bit address arithmetic per lane and copy.
+// soff: a wave-uniform byte offset added to every lane's (a scalar operand).
 template <bool XG = false>
-__device__ __forceinline__ void lds_bdma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, void* base) {
+__device__ __forceinline__ void lds_bdma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, void* base,
+                                           uint32_t soff = 0) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)base, 16,
-                                             voff, 0, 0, XG ? 16 : 0);
+                                             voff, soff, 0, XG ? 16 : 0);
 }
 
 // gfx950's transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group, lane i receives

@@ -10,7 +10,7 @@
 //    there are more tiles to spread over 256 CUs. Grid split-K on top is deterministic: the
 //    last block of a tile to arrive sums every split's partial in split order.
 //  - gemm_big (128 x 128, 192 x 256 or 256 x 256 tiles): the MFMA-bound regime (M >= 2048): a
-//    and w tiles copied into four LDS stages by direct global -> LDS loads (gemm_big.h), four or
+//    and w tiles copied into four LDS stages by direct buffer -> LDS loads (gemm_big.h), four or
 //    eight waves each owning a 64 x 64 (96 x 64, 128 x 64) output block on 32 x 32 x 16 MFMA, the
 //    epilogue's column-wise part applied on the accumulators. A K split, the same deterministic
 //    last-arriver sum, is there for completeness (config sweeps): at these sizes the chooser
@@ -167,8 +167,9 @@ void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
     if ((g.epi & EPI_GEGLU) && (g.epi & (EPI_RES | EPI_STATS | EPI_ROPE)))
         fail("GeGLU does not combine with a residual, statistics or RoPE");
     if (stats && (g.stats_out == g.stats_in)) fail("stats_out may not alias stats_in");
-    if (tput && (size_t)g.m * g.n * 2 > 0xFFFFFFFFull)  // the epilogue's buffer offsets
-        fail("the throughput tiles take outputs up to 4 GB");
+    if (tput && ((size_t)g.m * g.n * 2 > 0xFFFFFFFFull || (size_t)g.m * g.k * 2 > 0xFFFFFFFFull ||
+                 (size_t)g.n * g.k * 2 > 0xFFFFFFFFull))  // buffer offsets: copies, epilogue
+        fail("the throughput tiles take a, w and outputs up to 4 GB");
     if (!tput && ksteps / cfg.splits < 4)  // each of the four waves takes a K step of every split
         fail(std::to_string(cfg.splits) + " splits leave a wave no K step of " + std::to_string(ksteps));
     if (tput && ksteps / cfg.splits < 2)  // the stage pipeline's first wait covers two stages

@@ -10,7 +10,7 @@
 // 8 Kflop, half what a 256 x 128 tile reads: the copy path into a CU (about 64 bytes per clock)
 // keeps up with the MFMAs.
 //
-// The K loop runs BK = 32 at a time through four LDS stages filled by direct global -> LDS loads
+// The K loop runs BK = 32 at a time through four LDS stages filled by direct buffer -> LDS loads
 // (no register staging), three stages ahead, with one block barrier per stage. A stage's copies
 // are issued between the MFMAs of the stage three back: issued in one burst they stall the
 // issuing wave on the address path while its MFMA unit idles.
@@ -145,21 +145,33 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     // 192 x 256: copy I is a's while I < A_COPIES, a wave-uniform test, and copies past NCOPY
     // are none.)
     static_assert(!C::EVEN || C::LOADS % 2 == 0, "half the copies a's");
-    auto issue_one = [&](int ks, int buf, int q) {
-        char* st = lds + buf * C::STAGE;
-        const int I = w + C::NWAVES * q, kt = ub + ks;
-        if (!C::EVEN && I >= C::NCOPY) return;
+    // The copies go through buffer descriptors over a and w (the host checks both fit 4 GB): a
+    // lane's 32-bit offset of copy q at unit 0, computed once; unit kt adds kt * 64 bytes (a) or
+    // kt * 4 KB (w) as the scalar offset. (Global copies take a 64-bit lane address, an added
+    // 64-bit operation a copy, and cost the K loop ~20% here.)
+    const auto abuf = buffer_rsrc(p.a, (uint32_t)min((size_t)p.m * p.k * 2, (size_t)0xFFFFFFFFu));
+    const auto wbuf = buffer_rsrc(p.w, (uint32_t)min((size_t)p.n * p.k * 2, (size_t)0xFFFFFFFFu));
+    uint32_t coff[C::LOADS];
+#pragma unroll
+    for (int q = 0; q < C::LOADS; q++) {
+        const int I = w + C::NWAVES * q;
         if (C::EVEN ? q < C::LOADS / 2 : I < C::A_COPIES) {
             const int r = 16 * I + (l >> 2), ch = (l & 3) ^ ((r >> 2) & 3);
             const int row = min(by * BM + r, p.m - 1);
-            const f16* src = (const f16*)p.a + (size_t)row * p.k + kt * 32 + ch * 8;
-            lds_dma16<AX>(src, st + I * 1024);
+            coff[q] = (uint32_t)(((size_t)row * p.k + ub * 32 + ch * 8) * 2);
         } else {
             const int J = I - C::A_BYTES / 1024;  // 4 KB block J / 4 = column group, part J % 4
-            const size_t blk = (size_t)(bx * (BN / 64) + (J >> 2)) * U + kt;
-            const f16* src = (const f16*)p.w + (blk * 4 + (J & 3)) * 512 + l * 8;
-            lds_dma16<false>(src, st + C::A_BYTES + J * 1024);
+            coff[q] = (uint32_t)((((bx * (BN / 64) + (J >> 2)) * U + ub) * 4 + (J & 3)) * 1024 + l * 16);
         }
+    }
+    auto issue_one = [&](int ks, int buf, int q) {
+        char* st = lds + buf * C::STAGE;
+        const int I = w + C::NWAVES * q;
+        if (!C::EVEN && I >= C::NCOPY) return;
+        if (C::EVEN ? q < C::LOADS / 2 : I < C::A_COPIES)
+            lds_bdma16<AX>(abuf, coff[q], st + I * 1024, ks * 64);
+        else
+            lds_bdma16<false>(wbuf, coff[q], st + C::A_BYTES + (I - C::A_BYTES / 1024) * 1024, ks * 4096);
     };
     auto issue = [&](int kt, int buf) {
 #pragma unroll
