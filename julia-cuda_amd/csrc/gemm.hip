@@ -167,7 +167,7 @@ void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
     if ((g.epi & EPI_GEGLU) && (g.epi & (EPI_RES | EPI_STATS | EPI_ROPE)))
         fail("GeGLU does not combine with a residual, statistics or RoPE");
     if (stats && (g.stats_out == g.stats_in)) fail("stats_out may not alias stats_in");
-    if (tput && ((size_t)g.m * g.n * 2 > 0xFFFFFFFFull || (size_t)g.m * g.k * 2 > 0xFFFFFFFFull ||
+    if (tput && ((size_t)g.m * g.n * 2 > 0xFFFFFF00ull || (size_t)g.m * g.k * 2 > 0xFFFFFFFFull ||
                  (size_t)g.n * g.k * 2 > 0xFFFFFFFFull))  // buffer offsets: copies, epilogue
         fail("the throughput tiles take a, w and outputs up to 4 GB");
     if (!tput && ksteps / cfg.splits < 4)  // each of the four waves takes a K step of every split

@@ -395,14 +395,21 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     // lanes a row; the 16-byte chunk c of row r is stored at chunk c ^ (r % 16), so that the 16
     // rows one read serves cover all 64 banks). A lane's own gathers would touch 32 lines a load
     // instruction, over again in every wave that shares the rows.
+    // Every copy's row position is read first (one LDS round trip; a copy issued between them
+    // would make the next read wait for it), then the copies go out through a descriptor over
+    // the table (256 bytes a row).
     const char* table = lds;
     if (ROPE) {
         constexpr int COPIES = C::TM / 4 / C::NWAVES;
+        const auto tbuf = buffer_rsrc(p.rope, (uint32_t)p.rope_rows * 256u);
+        uint32_t toff[COPIES];
 #pragma unroll
         for (int q = 0; q < COPIES; q++) {
             const int I = w + C::NWAVES * q, rr = 4 * I + (l >> 4), c = (l & 15) ^ (rr & 15);
-            lds_dma16<false>(p.rope + ((size_t)rows_pos[rr] * 32 + c * 2) * 2, lds + I * 1024);
+            toff[q] = (uint32_t)rows_pos[rr] * 256u + c * 16;
         }
+#pragma unroll
+        for (int q = 0; q < COPIES; q++) lds_bdma16<false>(tbuf, toff[q], lds + (w + C::NWAVES * q) * 1024);
         wait_vmcnt<0>();
         __syncthreads();
     }
@@ -410,13 +417,15 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     struct RowIn {
         half8 rr[NPASS];        // residual, transposed layout
     };
+    // The residual through a descriptor (32-bit offsets; the rows are clamped into it).
+    [[maybe_unused]] const auto rbuf = buffer_rsrc(RES ? (p.res ? p.res : p.c) : p.c,
+                                                   (uint32_t)min((size_t)p.m * ncol * 2, (size_t)0xFFFFFFFFu));
     auto load_row = [&](int i, RowIn& in) {
         if (RES) {
-            const f16* x = (const f16*)(p.res ? p.res : p.c);
 #pragma unroll
             for (int ps = 0; ps < NPASS; ps++) {
                 const int r = min(by * BM + wm * C::WM + 32 * i + ps * RPP + l / LPR, p.m - 1);
-                in.rr[ps] = *(const half8*)(x + (size_t)r * ncol + col0 + 8 * (l % LPR));
+                in.rr[ps] = bload16<false>(rbuf, ((uint32_t)r * ncol + col0 + 8 * (l % LPR)) * 2u);
             }
         }
     };
@@ -554,12 +563,10 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
             }
             const int row = by * BM + wm * C::WM + 32 * i + rl;
             const bool valid = row < p.m;
-            if (valid) {
-                if (XG)  // one coherent 16-byte store (the host checks the output fits 4 GB)
-                    bstore16<true>(cbuf, (uint32_t)(((size_t)row * ncol + col0 + cl) * 2), o);
-                else
-                    store16<false>((f16*)p.c + (size_t)row * ncol + col0 + cl, o);
-            }
+            // One 16-byte buffer store (device-coherent with XG), no branch: a row past m takes an
+            // offset past the descriptor's range (the host keeps the output under 0xFFFFFF00
+            // bytes), and the hardware drops the store.
+            bstore16<XG>(cbuf, valid ? ((uint32_t)row * ncol + col0 + cl) * 2u : 0xFFFFFF00u, o);
             if (EPI & EPI_STATS) {
                 float s = 0.0f, sq = 0.0f;
 #pragma unroll
