@@ -271,6 +271,18 @@ def test_gemm_check_rejects_what_the_kernels_do_not_take():
     with pytest.raises(jh.JuliaHipError, match="fewer than two K steps"):
         jh.gemm_check(jh.gemm_args("resstats", base, base + 4096, base + 8192, 512, 768, 128,
                                    stats_out=base + 256), 256, 3, ws_floats=1 << 24, counters=64)
+    # The throughput tiles address a, w and c through buffer descriptors (32-bit offsets); a row
+    # past m stores to offset 0xFFFFFF00, outside any output the check lets through.
+    rope = dict(rope=base + 512, rope_rows=1 << 21)
+    big = jh.gemm_args("rope", base, base + 4096, base + 8192, (0xFFFFFF00 // 2304) // 2, 2304, 768, **rope)
+    jh.gemm_check(big, 256)
+    jh.gemm_check(jh.gemm_args("rope", base, base + 4096, base + 8192, 0xFFFFFF00 // 2 // 2304 - 255,
+                               2304, 768, **rope), 128)
+    with pytest.raises(jh.JuliaHipError, match="a, w and outputs up to 4 GB"):
+        jh.gemm_check(jh.gemm_args("rope", base, base + 4096, base + 8192, 0xFFFFFF00 // 2 // 2304 + 1,
+                                   2304, 768, **rope), 256)
+    jh.gemm_check(jh.gemm_args("rope", base, base + 4096, base + 8192, 0xFFFFFF00 // 2 // 2304 + 1,
+                               2304, 768, **rope), 64)  # the latency tiles take full pointers
     # The engine's own epilogues (the score folded into the scorer's lin1, the head's gathered
     # marker rows) take arguments the per-op ABI does not carry: through it they are refused.
     lin1 = dict(stats_in=base + 64, colsum=base + 128, bias=base + 256)
