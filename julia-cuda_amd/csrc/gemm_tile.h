@@ -128,6 +128,15 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     const int U = p.k >> 5;
     const int ub = z * U / p.splits, ue = (z + 1) * U / p.splits, nu = ue - ub;
     const int u0 = ub + w * nu / NW, u1 = ub + (w + 1) * nu / NW;
+    // Eight waves, each with its K steps in one chunk (up to 40 steps a split): the waves'
+    // partials are summed in two halves. The operands reach the CU in the order the waves issued
+    // their loads, so waves 4-7 (each the second wave of its SIMD) finish ~1.5 us after waves
+    // 0-3 (293 rows, K = 768), and waves 0-3 sum their four partials in that time; after the
+    // last wave only the half sum and four partials remain. The late waves pass the first barrier
+    // right after issuing their loads. The sums run in wave order either way (the values do not
+    // depend on which half finishes first).
+    const bool two = NW == 8 && (nu + NW - 1) / NW <= 5;  // block-uniform: every wave takes kone
+    const bool late = two && w >= NW / 2;
 
     const f16* ap[MI];
 #pragma unroll
@@ -235,6 +244,8 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
 #pragma unroll
         for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, c0, er[ps]);
         __builtin_amdgcn_sched_barrier(0);
+        if (late) __builtin_amdgcn_s_barrier();  // the halves' first barrier (see `two`)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < UC; s++) {
             const uint32_t keep = u0 + s < u1 ? 0xffffffffu : 0u;
@@ -269,23 +280,51 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
 #pragma unroll
         for (int j = 0; j < 4; j++)
             *(floatx4*)&red[(w * BM + 16 * i + r16) * 68 + 16 * j + 4 * g] = acc[i][j];
-    __syncthreads();
-
-    float v[NPASS][8];
+    // The partials summed in wave order, from slot `from` on (0: all eight; two: the half sum in
+    // slot 0, then waves 4-7).
+    auto sum_slots = [&](float (&v)[NPASS][8], int from) {
 #pragma unroll
-    for (int ps = 0; ps < NPASS; ps++) {
-        const int r = ps * RPP + (tid >> 3);
+        for (int ps = 0; ps < NPASS; ps++) {
+            const int r = ps * RPP + (tid >> 3);
 #pragma unroll
-        for (int e = 0; e < 8; e++) v[ps][e] = 0.0f;
-        if (r < BM) {
+            for (int e = 0; e < 8; e++) v[ps][e] = 0.0f;
+            if (r < BM) {
 #pragma unroll
-            for (int ww = 0; ww < NW; ww++) {
-                const float4 lo = *(const float4*)&red[(ww * BM + r) * 68 + c0];
-                const float4 hi = *(const float4*)&red[(ww * BM + r) * 68 + 32 + c0];
-                v[ps][0] += lo.x, v[ps][1] += lo.y, v[ps][2] += lo.z, v[ps][3] += lo.w;
-                v[ps][4] += hi.x, v[ps][5] += hi.y, v[ps][6] += hi.z, v[ps][7] += hi.w;
+                for (int ww = 0; ww < NW; ww++) {
+                    if (ww > 0 && ww < from) continue;
+                    const float4 lo = *(const float4*)&red[(ww * BM + r) * 68 + c0];
+                    const float4 hi = *(const float4*)&red[(ww * BM + r) * 68 + 32 + c0];
+                    v[ps][0] += lo.x, v[ps][1] += lo.y, v[ps][2] += lo.z, v[ps][3] += lo.w;
+                    v[ps][4] += hi.x, v[ps][5] += hi.y, v[ps][6] += hi.z, v[ps][7] += hi.w;
+                }
             }
         }
+    };
+    float v[NPASS][8];
+    if (two) {
+        if (!late) {
+            // The early waves' partials are in (the late waves passed this barrier earlier), and
+            // their 256 threads sum them into slot 0: 0 + w0 + w1 + w2 + w3, as the full sum
+            // would run.
+            wait_lgkm0();
+            __builtin_amdgcn_s_barrier();
+            for (int x = tid; x < BM * 16; x += 64 * (NW / 2)) {
+                float* e0 = &red[(x >> 4) * 68 + 4 * (x & 15)];
+                float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+                for (int ww = 0; ww < NW / 2; ww++) {
+                    const float4 b = *(const float4*)(e0 + ww * BM * 68);
+                    a.x += b.x, a.y += b.y, a.z += b.z, a.w += b.w;
+                }
+                *(float4*)e0 = a;
+            }
+        }
+        wait_lgkm0();
+        __builtin_amdgcn_s_barrier();  // every partial and the half sum are in
+        sum_slots(v, NW / 2);
+    } else {
+        __syncthreads();
+        sum_slots(v, 0);
     }
     __syncthreads();  // red is free again
     mark(2);
