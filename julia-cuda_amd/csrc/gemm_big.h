@@ -147,8 +147,9 @@ __device__ __forceinline__ void gemm_big_tile(const GemmParams& p, int task, cha
     static_assert(!C::EVEN || C::LOADS % 2 == 0, "half the copies a's");
     // The copies go through buffer descriptors over a and w (the host checks both fit 4 GB): a
     // lane's 32-bit offset of copy q at unit 0, computed once; unit kt adds kt * 64 bytes (a) or
-    // kt * 4 KB (w) as the scalar offset. (Global copies take a 64-bit lane address, an added
-    // 64-bit operation a copy, and cost the K loop ~20% here.)
+    // kt * 4 KB (w) as the scalar offset. (Global copies take a 64-bit lane address and an added
+    // 64-bit operation a copy: the GEMMs ran 2-6% slower with them.) Copies q past a 192-row
+    // tile's NCOPY get an offset that is never used.
     const auto abuf = buffer_rsrc(p.a, (uint32_t)min((size_t)p.m * p.k * 2, (size_t)0xFFFFFFFFu));
     const auto wbuf = buffer_rsrc(p.w, (uint32_t)min((size_t)p.n * p.k * 2, (size_t)0xFFFFFFFFu));
     uint32_t coff[C::LOADS];
