@@ -357,7 +357,9 @@ __host__ __device__ constexpr int w_tile_bytes(int k, int splits) {
     return ((k / 32 + splits - 1) / splits) * 4096;
 }
 
-// Waves [w_first, 4) copy task's weight tile to `lds` (1 KB per wave load).
+// Waves [w_first, 4) copy task's weight tile to `lds` (1 KB per wave load). (Global copies: the
+// same copies through a buffer descriptor made the whole-model launch 13-19% slower, the
+// prefetch no longer overlapping what runs before the tile's wait.)
 __device__ __forceinline__ void w_tile_fetch(const GemmParams& p, WTile t, f16* lds, int w_first) {
     const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
     if (w < w_first) return;
