@@ -280,16 +280,15 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
     }
     k0 &= ~31;
 
-    // rows [r0, r0 + rows) (rows % 8 == 0) of qkv's columns col .. col + 63 into `dst`: wave
-    // load I fills LDS chunks 64 I .. 64 I + 63, lane l chunk 64 I + l, which is row 8 I + l / 8,
-    // logical chunk (l % 8) ^ (l / 8). Through a descriptor over the rows below n (rows past n
-    // read zeros; their keys are masked): the lane's offset is the same for every load, the
-    // load's rows a scalar offset.
-    const int lrow = l >> 3, lch = (l & 7) ^ lrow;
+    // rows [r0, r0 + rows) (rows % 8 == 0) of qkv's columns col .. col + 63, clamped to row
+    // n - 1, into `dst`: wave load I fills LDS chunks 64 I .. 64 I + 63, lane l chunk 64 I + l,
+    // which is row c / 8, logical chunk (c % 8) ^ (row % 8).
     auto stage = [&](char* dst, int r0, int rows, int col) {
-        const auto rs = buffer_rsrc((const f16*)p.qkv + (size_t)r0 * ld, (uint32_t)(min(n - r0, rows) * ld * 2));
-        const uint32_t voff = (uint32_t)((lrow * ld + col + lch * 8) * 2);
-        for (int I = w; I * 64 < rows * 8; I += NW) lds_bdma16<XL>(rs, voff, dst + I * 1024, (uint32_t)(I * 16 * ld));
+        for (int I = w; I * 64 < rows * 8; I += NW) {
+            const int c = I * 64 + l, row = c >> 3, ch = (c & 7) ^ (row & 7);
+            const f16* src = (const f16*)p.qkv + (size_t)min(r0 + row, n - 1) * ld + col + ch * 8;
+            lds_dma16<XL>(src, dst + I * 1024);
+        }
     };
 
     const int qi = q0 + r16;  // this lane's query (the same 16 in every wave)
