@@ -193,11 +193,13 @@ def _np_ptr(a):
     return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
 
 
-def _finalize(obj):
+def _finalize(obj, _is_finalizing=sys.is_finalizing):
     """Garbage-collected objects free their device memory, except at interpreter shutdown: then
     the HIP runtime may already be torn down, so no device call is made (the process's memory
-    goes with it). Callers close() what they own before exiting."""
-    if sys.is_finalizing():
+    goes with it). Callers close() what they own before exiting. (The finalizers hold this
+    function and sys.is_finalizing as default arguments: at shutdown the module's globals may
+    already be gone when they run.)"""
+    if _is_finalizing():
         obj.ptr = None
     else:
         obj.close()
@@ -231,8 +233,8 @@ class Engine:
             self._free(self.ptr)
             self.ptr = None
 
-    def __del__(self):
-        _finalize(self)
+    def __del__(self, _fin=_finalize):
+        _fin(self)
 
     def __enter__(self):
         return self
@@ -399,8 +401,8 @@ class DeviceBuffer:
             self._free(self.ptr)
             self.ptr = None
 
-    def __del__(self):
-        _finalize(self)
+    def __del__(self, _fin=_finalize):
+        _fin(self)
 
 
 # ---------------------------------------------------------------- Part 2: per-op surface
@@ -419,8 +421,8 @@ class Scratch:
             self._free(self.ptr)
             self.ptr = None
 
-    def __del__(self):
-        _finalize(self)
+    def __del__(self, _fin=_finalize):
+        _fin(self)
 
 
 def gemm_args(epi, a, w, c, m, n, k, stats_in=0, colsum=0, eps=1e-5, bias=0, rope=0, positions=0,
