@@ -498,46 +498,23 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
     char* const ring = lds + kg * ATT_STREAM_LDS;
     const int j = r16 >> 2, q = r16 & 3;
 
-    // The sequence bounds the tile needs, all loaded in one round trip (the first stage's copy
-    // waits for them, and each round trip costs about a microsecond under load): the tile's first
-    // row's sequence start and last row's sequence end, the wave's first and last rows'
-    // sequences (uniform: scalar loads), this lane's query's sequence.
+    // The sequence bounds the tile needs, all loaded in one round trip (each costs about a
+    // microsecond under load; outside the window layers' early copy below, the first copy waits
+    // for them): the tile's first row's sequence start and last row's sequence end, the wave's
+    // first and last rows' sequences (uniform: scalar loads), this lane's query's sequence.
     const int qlast = min(q0 + QB - 1, n - 1);
     const int wq0 = min(q0 + 16 * w, n - 1), wql = min(q0 + 16 * w + 15, n - 1);
     const int qi = q0 + 16 * w + r16;
     const int qc = min(qi, n - 1);
-    int k0 = 0, k1 = n, ulo = 0, uhi = n, slo = 0, shi = n;
-    bool one_seq = true;
-    if (p.seg) {
-        const int t0 = p.seg[2 * q0], t1 = p.seg[2 * qlast + 1];
-        const int w0 = p.seg[2 * wq0], wls = p.seg[2 * wql], wle = p.seg[2 * wql + 1];
-        const int2 sq = *(const int2*)(p.seg + 2 * qc);
-        k0 = t0, k1 = t1, ulo = w0, uhi = wle, one_seq = w0 == wls, slo = sq.x, shi = sq.y;
-    }
     // The tile's keys: from its first row's sequence start to its last row's sequence end, cut
-    // to the window; 64-aligned blocks.
-    if (p.window > 0) {
-        k0 = max(k0, q0 - p.window);
-        k1 = min(k1, q0 + QB + p.window);
-    }
-    k0 &= ~63;
-    const int nblk = k1 > k0 ? (k1 - k0 + 63) >> 6 : 0;
-
-    // This lane's valid keys: its sequence cut to the window, [klo, khi).
-    const int wl = p.window > 0 ? p.window : (1 << 30);
-    const int klo = max(slo, qi - wl), khi = min(shi, qi + wl + 1);
-    const uint32_t kspan = khi > klo ? (uint32_t)(khi - klo) : 0u;
-    // Keys any of the wave's 16 queries may see, [wlo, whi): the wave skips the MFMAs and the
-    // softmax of a block wholly outside (every score masked: the step would change nothing).
-    const int wlo = __builtin_amdgcn_readfirstlane(max(ulo, wq0 - wl));
-    const int whi = __builtin_amdgcn_readfirstlane(min(uhi, wql + wl + 1));
-    half8 qf[2];
-    {
-        const f16* qp = (const f16*)p.qkv + (size_t)qc * ld + h * 64 + 8 * g;
-        qf[0] = load16h<false>(qp);
-        qf[1] = load16h<false>(qp + 32);
-    }
-
+    // to the window; 64-aligned blocks. In window layers the range starts at q0 - window
+    // whatever the sequences (keys before the tile's sequence are masked like any others, and a
+    // wave skips blocks wholly outside its queries' reach), so that with one key group the first
+    // block's copy goes out before the bounds arrive.
+    int k0 = p.window > 0 ? max(0, q0 - p.window) & ~63 : 0, k1 = n;
+    int ulo = 0, uhi = n, slo = 0, shi = n;
+    bool one_seq = true;
+    const bool spec = KS == 1 && p.window > 0 && p.seg;  // the first copy before the bounds
     // Block b (keys k0 + 64 b ..) into stage st = b % NS: 16 wave loads of 1 KB (8 rows of K,
     // then of V), LOADS a wave; lane l fills LDS chunk 64 I + l = row c / 8, logical chunk
     // (c % 8) ^ (row % 8). The copies go through a buffer descriptor over the block's rows: the
@@ -563,6 +540,31 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
             lds_bdma16<false>(rs, doff[qq], dst + (kk ? 0 : 8192) + I * 1024);
         }
     };
+    if (spec) stage(0, 0);
+    if (p.seg) {
+        const int t0 = p.seg[2 * q0], t1 = p.seg[2 * qlast + 1];
+        const int w0 = p.seg[2 * wq0], wls = p.seg[2 * wql], wle = p.seg[2 * wql + 1];
+        const int2 sq = *(const int2*)(p.seg + 2 * qc);
+        if (p.window == 0) k0 = t0 & ~63;
+        k1 = t1, ulo = w0, uhi = wle, one_seq = w0 == wls, slo = sq.x, shi = sq.y;
+    }
+    if (p.window > 0) k1 = min(k1, q0 + QB + p.window);
+    const int nblk = k1 > k0 ? (k1 - k0 + 63) >> 6 : 0;
+
+    // This lane's valid keys: its sequence cut to the window, [klo, khi).
+    const int wl = p.window > 0 ? p.window : (1 << 30);
+    const int klo = max(slo, qi - wl), khi = min(shi, qi + wl + 1);
+    const uint32_t kspan = khi > klo ? (uint32_t)(khi - klo) : 0u;
+    // Keys any of the wave's 16 queries may see, [wlo, whi): the wave skips the MFMAs and the
+    // softmax of a block wholly outside (every score masked: the step would change nothing).
+    const int wlo = __builtin_amdgcn_readfirstlane(max(ulo, wq0 - wl));
+    const int whi = __builtin_amdgcn_readfirstlane(min(uhi, wql + wl + 1));
+    half8 qf[2];
+    {
+        const f16* qp = (const f16*)p.qkv + (size_t)qc * ld + h * 64 + 8 * g;
+        qf[0] = load16h<false>(qp);
+        qf[1] = load16h<false>(qp + 32);
+    }
 
     const float scale = 1.4426950408889634f / 8.0f;  // log2(e) / sqrt(64)
     float mx = -INFINITY, lsum = 0.0f;
@@ -686,7 +688,7 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
     };
 
     static_assert(NS == 2, "the loop below is unrolled by the stages");
-    if (has(0)) stage(kg, 0);
+    if (has(0) && !spec) stage(kg, 0);  // (with `spec`, block 0's copy is out already)
     for (int b = 0; b < nsteps; b += NS) {
         step(b, std::integral_constant<int, 0>{});
         if (b + 1 < nsteps) step(b + 1, std::integral_constant<int, 1>{});
