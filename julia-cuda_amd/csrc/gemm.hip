@@ -93,13 +93,17 @@ int device_cus() {
 
 }  // namespace
 
-// Split-K scratch: a tile's f32 partial per split (the latency tiles store at least 32 rows), and
-// an arrival counter per tile.
+// Split-K scratch: a tile's f32 partial per split, and an arrival counter per tile. A split
+// latency tile runs on four waves (gemm_lat, gemm_w_tile: 256 threads, 32 rows an epilogue pass),
+// and finish() stores whole passes: ceil(BM / 32) x 32 rows of 64 columns (16 -> 32, 48 -> 64).
+// A throughput tile stores its BM x BN accumulators.
 size_t gemm_ws_floats(int m, int n, GemmConfig cfg) {
     if (cfg.splits <= 1) return 0;
-    const int bn = cfg.bm >= 128 ? big_bn(cfg.bm) : 64;
+    const bool tput = cfg.bm >= 128;
+    const int bn = tput ? big_bn(cfg.bm) : 64;
     const size_t tiles = (size_t)(n / bn) * ((m + cfg.bm - 1) / cfg.bm);
-    const size_t rows = cfg.bm < 32 ? 32 : cfg.bm;
+    const size_t rows = tput ? (size_t)cfg.bm : (size_t)(cfg.bm + LAT_SPLIT_PASS_ROWS - 1) /
+                                                     LAT_SPLIT_PASS_ROWS * LAT_SPLIT_PASS_ROWS;
     return tiles * cfg.splits * rows * bn;
 }
 

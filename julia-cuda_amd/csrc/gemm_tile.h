@@ -14,6 +14,11 @@ namespace jh {
 template <int BM, int NW = 4>
 constexpr int lat_lds_floats() { return NW * BM * 68; }
 
+// Rows of one epilogue pass of a four-wave latency tile (256 threads, 8 a row): the unit in which
+// a K split's partial tile is stored (gemm_ws_floats sizes the scratch by it). Only four-wave
+// tiles take a K split.
+constexpr int LAT_SPLIT_PASS_ROWS = 32;
+
 // Shared tail: each thread's 8 values (K fully summed within the block) -> the split-K
 // reduction when the grid splits K -> the epilogue. Thread t of NT owns row (pass * NT / 8 +
 // t / 8) of the tile and columns c0 = 4 (t % 8), c0 + 32 of 64-column group `grp`.
@@ -117,6 +122,7 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     constexpr int MI = BM / 16;
     constexpr int RPP = 8 * NW;                     // tile rows a pass of the epilogue
     constexpr int NPASS = (BM + RPP - 1) / RPP;
+    static_assert(NW != 4 || RPP == LAT_SPLIT_PASS_ROWS, "split partials are sized by 32-row passes");
     const int T = p.tiles_n * p.tiles_m * p.splits;
     const int L = xcd_task(task, T);
     const int z = L % p.splits, t2 = L / p.splits;
@@ -387,7 +393,7 @@ __device__ __forceinline__ void gemm_w_tile(const GemmParams& p, int task, char*
         if (sub && threadIdx.x == 0) sub[i] = wall_clock64();
     };
     constexpr int MI = BM / 16;
-    constexpr int NPASS = (BM + 31) / 32;
+    constexpr int NPASS = (BM + LAT_SPLIT_PASS_ROWS - 1) / LAT_SPLIT_PASS_ROWS;
     constexpr int UMAX = MI >= 3 ? 6 : 9;  // a fragments one wave holds: 72-96 or 36-72 VGPRs
     const int T = p.tiles_n * p.tiles_m * p.splits;
     const int L = xcd_task(task, T);

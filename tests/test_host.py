@@ -294,6 +294,29 @@ def test_gemm_check_rejects_what_the_kernels_do_not_take():
                                    768, 768, bias=base + 256, stats_out=base + 512), 16)
 
 
+@pytest.mark.parametrize("bm,pass_rows", [(16, 32), (32, 32), (48, 64), (64, 64)])
+def test_split_scratch_covers_the_latency_tiles_partials(bm, pass_rows):
+    """A split latency tile runs on four waves (256 threads, 8 a row), so its epilogue passes
+    cover 32 rows and each split stores whole passes: ceil(bm / 32) passes x 2 halves x 256
+    threads x 4 floats. The check accepts exactly that much scratch and no less."""
+    base = 1 << 20
+    ln = dict(stats_in=base + 64, colsum=base + 128)
+    for m, n, k, splits in ((1536, 2304, 768, 2), (293, 2304, 768, 4), (512, 768, 1152, 3)):
+        args = jh.gemm_args("lngeglu", base, base + 4096, base + 8192, m, n, k, **ln)
+        tiles = (n // 64) * ((m + bm - 1) // bm)
+        npass = (bm + 31) // 32
+        need = tiles * splits * npass * 2 * 256 * 4
+        assert need == tiles * splits * pass_rows * 64
+        jh.gemm_check(args, bm, splits, ws_floats=need, counters=tiles)
+        with pytest.raises(jh.JuliaHipError, match="scratch is too small"):
+            jh.gemm_check(args, bm, splits, ws_floats=need - 1, counters=tiles)
+    # The shape that exposed the 48-row under-count: 1152 tiles x 2 splits x 64 x 64 floats.
+    big48 = jh.gemm_args("lngeglu", base, base + 4096, base + 8192, 1536, 2304, 768, **ln)
+    with pytest.raises(jh.JuliaHipError, match="scratch is too small"):
+        jh.gemm_check(big48, 48, 2, ws_floats=9_437_184 - 1, counters=1152)
+    jh.gemm_check(big48, 48, 2, ws_floats=9_437_184, counters=1152)
+
+
 def test_chooser_matches_the_measured_winners():
     """The picks at the shapes measured on MI355X (per-step GEMM times, the fastest config within
     a few percent): qkv/wi 48-row latency tiles at 293 tokens, wo and wo_mlp 16 rows."""

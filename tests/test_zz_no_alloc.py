@@ -100,3 +100,96 @@ def test_gemm_static_rejects_tilings_past_its_scratch(torch_cuda):
     jh.gemm_static(args, bm=64, splits=1, stream=torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert float(c.float().abs().max()) == 0.0
+
+
+def _operands(torch, m, n, k, seed):
+    """LayerNorm-GeGLU operands on the device (the output is c alone, no residual)."""
+    rng = np.random.default_rng(seed)
+    a = rand16(rng, (m, k), mean=0.1)
+    W = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    w, colsum = O.fold_layernorm(W, gamma)
+    dev = dict(a=to_dev(torch, a), w=to_dev(torch, O.pack_frag(w)), colsum=to_dev(torch, colsum),
+               stats_in=to_dev(torch, O.row_stats(a)))
+    dev["c"] = torch.zeros((m, n // 2), dtype=torch.float16, device="cuda")
+    dev["args"] = jh.gemm_args("lngeglu", dev["a"].data_ptr(), dev["w"].data_ptr(),
+                               dev["c"].data_ptr(), m, n, k, stats_in=dev["stats_in"].data_ptr(),
+                               colsum=dev["colsum"].data_ptr(), eps=EPS)
+    return dev
+
+
+# (bm, the most rows whose two-way split fits the static scratch at n = 2304): a split latency
+# tile stores whole 32-row passes (16 -> 32 rows, 48 -> 64), a throughput tile its BM x BN.
+LIMITS = [(16, 896), (32, 1792), (48, 1344), (64, 1792), (128, 1792), (192, 1728), (256, 1792)]
+
+
+@pytest.mark.parametrize("bm,m_max", LIMITS)
+def test_gemm_static_at_its_scratch_limit(torch_cuda, bm, m_max):
+    """The largest two-way split the static scratch holds runs and equals julia_hip_gemm bit for
+    bit; one row more is refused before any launch."""
+    torch = torch_cuda
+    n, k = 2304, 768
+    print(f"gemm_static limit bm={bm} m={m_max} (and {m_max + 1} refused)", flush=True)
+    dev = _operands(torch, m_max + 1, n, k, seed=bm)
+    over = jh.gemm_args("lngeglu", dev["a"].data_ptr(), dev["w"].data_ptr(), dev["c"].data_ptr(),
+                        m_max + 1, n, k, stats_in=dev["stats_in"].data_ptr(),
+                        colsum=dev["colsum"].data_ptr(), eps=EPS)
+    with pytest.raises(jh.JuliaHipError, match="static scratch holds"):
+        jh.gemm_static(over, bm=bm, splits=2)
+    fit = jh.gemm_args("lngeglu", dev["a"].data_ptr(), dev["w"].data_ptr(), dev["c"].data_ptr(),
+                       m_max, n, k, stats_in=dev["stats_in"].data_ptr(),
+                       colsum=dev["colsum"].data_ptr(), eps=EPS)
+    stream = torch.cuda.current_stream().cuda_stream
+    scratch = jh.Scratch(ws_floats=1 << 24, counters=1 << 16)
+    try:
+        jh.gemm(fit, bm=bm, splits=2, scratch=scratch, stream=stream)
+        torch.cuda.synchronize()
+        want = f16_bits(dev["c"]).copy()
+        dev["c"].zero_()
+        jh.gemm_static(fit, bm=bm, splits=2, stream=stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(f16_bits(dev["c"]), want), f"bm={bm} m={m_max}: differs from julia_hip_gemm"
+    finally:
+        scratch.close()
+
+
+@pytest.mark.parametrize("bm,splits,m", [(48, 2, 448), (16, 3, 293), (128, 2, 1100)])
+def test_gemm_static_under_graph_capture(torch_cuda, bm, splits, m):
+    """julia_hip_gemm_static captured into a HIP graph (its counter-clearing kernel and the split
+    GEMM), replayed three times with eager work and synchronisations in between: every replay
+    equals julia_hip_gemm's output bit for bit."""
+    torch = torch_cuda
+    n, k = 2304, 768
+    print(f"gemm_static graph bm={bm} splits={splits} m={m}", flush=True)
+    dev = _operands(torch, m, n, k, seed=m)
+    scratch = jh.Scratch(ws_floats=1 << 24, counters=1 << 16)
+    try:
+        stream = torch.cuda.current_stream().cuda_stream
+        jh.gemm(dev["args"], bm=bm, splits=splits, scratch=scratch, stream=stream)
+        torch.cuda.synchronize()
+        want = f16_bits(dev["c"]).copy()
+        # The first call on a device looks up the static array's address and sets kernel
+        # attributes; it runs before the capture.
+        jh.gemm_static(dev["args"], bm=bm, splits=splits, stream=stream)
+        torch.cuda.synchronize()
+        assert np.array_equal(f16_bits(dev["c"]), want)
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                jh.gemm_static(dev["args"], bm=bm, splits=splits,
+                               stream=torch.cuda.current_stream().cuda_stream)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        for replay in range(3):
+            # eager work between the replays: the same GEMM through julia_hip_gemm, then c cleared
+            jh.gemm(dev["args"], bm=bm, splits=splits, scratch=scratch, stream=stream)
+            dev["c"].zero_()
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(f16_bits(dev["c"]), want), f"replay {replay} differs"
+        graph.reset()
+    finally:
+        scratch.close()
