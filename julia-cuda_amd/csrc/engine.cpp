@@ -256,17 +256,25 @@ struct Engine {
         return a;
     }
 
-    // Returns where the residual stream is after the launch.
+    // Returns where the residual stream is after the launch. When the runtime refuses the
+    // cooperative launch (another process holds its resource), the layers run on the per-step
+    // kernels instead, in place on x.
     const jh_half* launch_encoder_fused(int first, int count, int n, const jh_half* x_in,
                                         const int32_t* pos = nullptr, const int32_t* seg = nullptr) {
         const LayerArgs a = layer_args(first, count, n, x_in, pos, seg);
-        layer_kernel.launch(a, layer_kernel.default_plan(n, cfg.d, cfg.inter), scratch, stream);
-        return LayerKernel::x_out(a);
+        if (layer_kernel.launch(a, layer_kernel.default_plan(n, cfg.d, cfg.inter), scratch, stream))
+            return LayerKernel::x_out(a);
+        if (x_in != x)
+            hip_check(hipMemcpyAsync(x, x_in, (size_t)n * cfg.d * 2, hipMemcpyDeviceToDevice, stream),
+                      "the residual stream");
+        for (int l = first; l < first + count; l++) launch_layer(l, n, pos, seg);
+        return x;
     }
 
     // The whole forward pass as one cooperative launch (embed, every layer, the head, the score)
-    // when the plan's kernel instance takes the head's GEMMs; false if not (the caller then runs
-    // the encoder kernel and the head's own launches). ids, markers: device, row indices.
+    // when the plan's kernel instance takes the head's GEMMs; false if not, or if the runtime
+    // refused the launch (the caller then runs the encoder kernel, or the per-step layers, and
+    // the head's own launches). ids, markers: device, row indices.
     bool launch_model(const uint32_t* ids, int n, int qtype, const uint32_t* markers, int nm,
                       float* logits, const int32_t* pos = nullptr, const int32_t* seg = nullptr,
                       const int32_t* row_type = nullptr) {
@@ -286,8 +294,7 @@ struct Engine {
         M.markers = markers, M.n_markers = nm, M.logits = logits;
         LayerArgs a = layer_args(0, cfg.layers, n, x, pos, seg);
         a.model = &M;
-        layer_kernel.launch(a, plan, scratch, stream);
-        return true;
+        return layer_kernel.launch(a, plan, scratch, stream);  // false: refused, nothing ran
     }
 
     // ---- the head (src/forward.rs GpuHead) -------------------------------------------------
@@ -1289,7 +1296,9 @@ int julia_hip_profile_layer(const Engine* ce, int n, int layer, const int* plan,
         uint64_t* prof = dalloc<uint64_t>(rows * PROF_WORDS, "profile");
         try {
             hip_check(hipMemset(prof, 0, rows * PROF_WORDS * 8), "hipMemset");
-            e.layer_kernel.launch(a, p, e.scratch, e.stream, 0x1f, prof);
+            if (!e.layer_kernel.launch(a, p, e.scratch, e.stream, 0x1f, prof))
+                throw std::runtime_error("profile: the runtime refused the cooperative launch "
+                                         "(another process holds its resource)");
             hip_check(hipStreamSynchronize(e.stream), "profile");
             if (e.layer_kernel.barrier_timed_out())
                 throw std::runtime_error("layer: a grid barrier timed out");

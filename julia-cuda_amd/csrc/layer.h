@@ -113,9 +113,11 @@ public:
     size_t counters(int max_m, int d, int inter, int head_ff = 0) const;
     // Phases: bits 0-4 select qkv, attention, wo, wi, wo_mlp (0x1f: whole layers; a subset only
     // with one layer). prof: null, or PROF_WORDS u64 per block of the grid and layer run.
-    // a.model: the whole forward pass (all layers and phases, from layer 0).
-    void launch(const LayerArgs& a, const LayerPlan& plan, const Scratch& s, hipStream_t stream,
-                unsigned phases = 0x1f, uint64_t* prof = nullptr);
+    // a.model: the whole forward pass (all layers and phases, from layer 0). Returns false,
+    // having launched nothing, when the runtime refuses the cooperative launch (another process
+    // holds the GPU's cooperative-launch resource): the caller runs the pass another way.
+    [[nodiscard]] bool launch(const LayerArgs& a, const LayerPlan& plan, const Scratch& s,
+                              hipStream_t stream, unsigned phases = 0x1f, uint64_t* prof = nullptr);
     int grid(const LayerArgs& a, const LayerPlan& plan) const;
     // LDS bytes a plan needs on m rows (weight tile, reduction and attention share it).
     static int lds_bytes(const LayerPlan& plan, int d, int inter, int m, int window);
@@ -141,11 +143,15 @@ private:
     bool lat48_ok_ = false;  // the 48-row instance fits as many blocks a CU as the plain one
     uint32_t* bar_ = nullptr;  // BAR_WORDS words
     // Launch through hipLaunchCooperativeKernel (true), or as a plain launch of the same
-    // resident grid: after the runtime refuses a cooperative launch because another process
-    // holds the GPU's cooperative-launch resource (hipErrorIllegalState), or when the
-    // environment sets JULIA_HIP_COOPERATIVE=0. The grid barrier is the kernel's own (atomics
-    // with a bounded wait), so the plain launch runs the same code.
+    // resident grid when the environment sets JULIA_HIP_COOPERATIVE=0. The grid barrier is the
+    // kernel's own (atomics with a bounded wait), so the plain launch runs the same code; a grid
+    // that is not co-resident ends in the bounded wait's error.
     bool coop_ = true;
+    // Tests of the barrier's time-out path only (JULIA_HIP_TEST_BARRIER_SKEW=1 when the engine
+    // is loaded): every grid barrier waits for one generation more than its arrivals make, so
+    // each block's bounded wait gives up (the non-co-resident case, forced from the host; every
+    // block still runs to its end) and the host reports the error.
+    uint32_t skew_ = 0;
 };
 
 }  // namespace jh

@@ -51,6 +51,7 @@ struct EncParams {
     int lds_main;     // dynamic LDS bytes before the block's split-K flag
     int att_gkeys[2];  // keys the attention tile stages at once: global, window layers
     uint32_t* bar;    // the barrier's words (BAR_WORDS, zero between launches)
+    uint32_t bar_skew;  // 0; 1 (tests of the time-out path): every barrier waits one too many
     uint64_t* prof;   // null, or PROF_WORDS per block and layer: see stamp()
     // The whole model (model != 0): ModelArgs, and the head GEMMs' tile heights and splits
     // (in_proj, out_proj, linear1, linear2, the scorer's lin1).
@@ -113,11 +114,13 @@ __device__ __forceinline__ void grid_sync(uint32_t* bar, uint32_t g0, uint32_t n
                     atomic_add_agent(bar + BAR_GEN, 1u);
             const uint32_t target = g0 + nb;
             const uint64_t t0 = wall_clock64();
-            while (!timed_out && (int)(atomic_load_agent(bar + BAR_GEN) - target) < 0) {
+            for (uint32_t it = 1; !timed_out && (int)(atomic_load_agent(bar + BAR_GEN) - target) < 0; it++) {
                 __builtin_amdgcn_s_sleep(1);
                 if (wall_clock64() - t0 > 20000000ull) {
                     atomic_store_agent(bar + BAR_TIMEOUT, 1u);
                     timed_out = true;  // the launch is lost: the remaining barriers do not wait
+                } else if ((it & 63) == 0 && atomic_load_agent(bar + BAR_TIMEOUT)) {
+                    timed_out = true;  // another block gave up: stop waiting at once
                 }
             }
             if (last && blockIdx.x == 0) {
@@ -249,7 +252,7 @@ void encoder_kernel(EncParams P) {
     uint32_t* s_last = (uint32_t*)(lds + P.lds_main);
     uint32_t g0 = 0, nb = 0;
     bool timed_out = false;
-    if (threadIdx.x == 0) g0 = atomic_load_agent(P.bar + BAR_GEN);
+    if (threadIdx.x == 0) g0 = atomic_load_agent(P.bar + BAR_GEN) + P.bar_skew;
     auto on = [&](int ph) { return ((P.phases >> ph) & 1u) != 0; };
     auto sync = [&](auto&& during) {
         nb++;
@@ -448,6 +451,8 @@ void LayerKernel::init(int cus, int lds_max) {
     cus_ = cus > 0 ? cus : 256;
     const char* coop = getenv("JULIA_HIP_COOPERATIVE");
     coop_ = !(coop && strcmp(coop, "0") == 0);
+    const char* skew = getenv("JULIA_HIP_TEST_BARRIER_SKEW");
+    skew_ = skew && strcmp(skew, "1") == 0 ? 1u : 0u;
     lds_max_ = lds_max - 16;  // the split-K flag after the main area
     per_cu_ = per_cu_big_ = per_cu_big256_ = 0;
     auto occupancy = [](const void* k, int threads, int lds) {
@@ -605,7 +610,7 @@ int LayerKernel::grid(const LayerArgs& a, const LayerPlan& plan) const {
     return (int)std::max<long>(grid, 1);
 }
 
-void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratch& s,
+bool LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratch& s,
                          hipStream_t stream, unsigned phases, uint64_t* prof) {
     auto fail = [&](const std::string& m) { throw std::runtime_error("layer: " + m); };
     if (per_cu_ <= 0) fail("the encoder kernel does not fit on a CU");
@@ -750,6 +755,7 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
     P.att_gkeys[0] = attention_gkeys(a.m, 0);
     P.att_gkeys[1] = attention_gkeys(a.m, window);
     P.bar = bar_;
+    P.bar_skew = skew_;
     P.prof = prof;
 
     const int grid_blocks = grid(a, plan);
@@ -760,23 +766,24 @@ void LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
                          : uses48 ? reinterpret_cast<const void*>(encoder_kernel<MODE_LAT48>)
                                                : reinterpret_cast<const void*>(encoder_kernel<MODE_LAT>);
     const dim3 threads(mode == MODE_BIG256 ? 512 : 256);
-    hipError_t e = hipErrorIllegalState;
+    hipError_t e;
     if (coop_) {
         e = hipLaunchCooperativeKernel(kernel, dim3(grid_blocks), threads, args, lds + 16, stream);
         if (e == hipErrorIllegalState) {
-            // Another process holds the cooperative-launch resource: from now on, plain launches
-            // of the same grid (at most the blocks resident at once, as the occupancy query
-            // sized it; a block that never gets a CU ends the barrier's bounded wait, which the
-            // host reports as an error, instead of hanging).
+            // Another process holds the cooperative-launch resource: nothing was launched, and
+            // the caller runs this pass on the per-step kernels. The next pass tries again.
             (void)hipGetLastError();
-            coop_ = false;
+            return false;
         }
-    }
-    if (!coop_) {
+    } else {
+        // JULIA_HIP_COOPERATIVE=0: plain launches of the same grid (at most the blocks resident
+        // at once, as the occupancy query sized it; a grid that is not co-resident ends in the
+        // barrier's bounded wait, which the host reports as an error, instead of hanging).
         e = hipLaunchKernel(kernel, dim3(grid_blocks), threads, args, lds + 16, stream);
     }
     if (e != hipSuccess) fail(std::string(hipGetErrorString(e)) + " (" + plan.str() + ", grid " +
                               std::to_string(grid_blocks) + ")");
+    return true;
 }
 
 bool LayerKernel::is_big(const LayerPlan& plan, int m) { return big_mode(plan, m) != MODE_LAT; }

@@ -209,6 +209,30 @@ def tier():
     return lib().julia_cuda_tier().decode()
 
 
+def profiler_attached(environ=None):
+    """The reason a profiler is attached to this process (rocprofv3's tool library preloaded, or
+    its ROCP_* / ROCPROF_* settings in the environment), or None. The measurement tools refuse
+    the persistent kernel's cooperative launches under one: rocprofv3 has ended such runs with a
+    segmentation fault in its own teardown, after the program's last line."""
+    env = os.environ if environ is None else environ
+    pre = env.get("LD_PRELOAD", "")
+    if "rocprof" in pre or "roctracer" in pre:
+        return "LD_PRELOAD names a profiler library (" + pre + ")"
+    names = sorted(k for k in env if k.startswith(("ROCP_", "ROCPROF_")))
+    if names:
+        return "the environment sets " + ", ".join(names)
+    return None
+
+
+def refuse_cooperative_under_profiler(what):
+    """Exits with a message when a profiler is attached and `what` makes cooperative launches."""
+    why = profiler_attached()
+    if why:
+        sys.exit(f"{what} makes cooperative launches (the persistent kernel), which are not run "
+                 f"under a profiler here: {why}. Time the persistent kernel with its in-kernel "
+                 "stamps (profile.py) and HIP events, or profile the per-step kernels only.")
+
+
 def device_count():
     return lib().julia_hip_device_count()
 

@@ -10,7 +10,8 @@ plain device-to-device copy of a known size to calibrate byte counters against.
 
 Prints the step's median time per call (HIP events) and the copy's bytes. With --batch N: config
 5's batched encoder instead (N requests of config 4's seeded lengths concatenated, per-step
-kernels then the persistent kernel, --iters times each). With --requests N: N such requests
+kernels then the persistent kernel, --iters times each; refused under a profiler, since the
+persistent kernel is a cooperative launch). With --requests N: N such requests
 (6 markers each, question types in turn) through julia_hip_run_batched as one pass, the whole
 forward pass (embed, encoder, head, scorer), --iters times.
 """
@@ -52,6 +53,7 @@ def main():
         e.close()
         return
     if args.batch:
+        jh.refuse_cooperative_under_profiler("--batch (its persistent-kernel pass)")
         import numpy as np
         rng = np.random.default_rng(4)
         lens = np.clip(np.round(rng.lognormal(np.log(260.0), 0.5, args.batch)), 72, 1024).astype(int)

@@ -71,6 +71,7 @@ def main():
     ap.add_argument("--layer", type=int, default=1, help="-1: the whole encoder, one launch")
     ap.add_argument("--spec", default="synthetic")
     args = ap.parse_args()
+    jh.refuse_cooperative_under_profiler("profile.py (the persistent kernel's stamps)")
     e = jh.Engine(args.spec, max_length=max(1024, args.tokens))
     e.profile_layer(args.tokens, args.layer)  # warm-up
     plan, stamps = e.profile_layer(args.tokens, args.layer)

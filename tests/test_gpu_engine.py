@@ -347,3 +347,27 @@ def test_full_model_293_tokens(torch_cuda):
         assert worst < CHAINED_REL
     finally:
         e.close()
+
+
+def test_barrier_time_out_is_an_error_not_wrong_logits(torch_cuda, small, monkeypatch):
+    """A persistent launch whose grid barriers never complete (forced from the host: every barrier
+    waits for one generation more than its arrivals make, the state a grid that is not
+    co-resident leaves) ends in the bounded wait's error, with every block run to its end; the
+    barrier words are reset, so the same engine's next passes are right on both paths."""
+    e_ok, m = small
+    rng = np.random.default_rng(31)
+    ids, markers = request(rng, 200, SMALL["vocab"])
+    want, _ = e_ok.run([(ids, markers, 1)], layer_fused=True)
+    monkeypatch.setenv("JULIA_HIP_TEST_BARRIER_SKEW", "1")
+    say("engine: barrier skew (time-out path)", spec(SMALL))
+    e = jh.Engine(spec(SMALL), max_length=1024)
+    monkeypatch.delenv("JULIA_HIP_TEST_BARRIER_SKEW")
+    try:
+        with pytest.raises(jh.JuliaHipError, match="grid barrier timed out"):
+            e.run([(ids, markers, 1)], layer_fused=True)
+        got, _ = e.run([(ids, markers, 1)], layer_fused=False)
+        check_logits(got[0], want[0], what="per-step after a barrier time-out")
+    finally:
+        e.close()
+    again, _ = e_ok.run([(ids, markers, 1)], layer_fused=True)
+    assert np.array_equal(again[0], want[0])

@@ -339,3 +339,34 @@ def test_chooser_matches_the_measured_winners():
     assert jh.gemm_choose(12288, 2304, 768, 256) == (256, 1)
     assert jh.gemm_choose(2048, 768, 768, 256) == (128, 1)
     assert jh.gemm_choose(8192, 768, 768, 256) == (128, 1)
+
+
+def test_profiler_detection():
+    """The measurement tools refuse cooperative launches under rocprofv3: its tool library in
+    LD_PRELOAD or its ROCP_* / ROCPROF_* settings mark a profiled process."""
+    assert jh.profiler_attached({}) is None
+    assert jh.profiler_attached({"LD_PRELOAD": "/usr/lib/libfoo.so", "ROCM_PATH": "/opt/rocm"}) is None
+    assert "LD_PRELOAD" in jh.profiler_attached(
+        {"LD_PRELOAD": "/opt/rocm/lib/rocprofiler-sdk/librocprofiler-sdk-tool.so"})
+    assert "ROCP_TOOL_LIBRARIES" in jh.profiler_attached({"ROCP_TOOL_LIBRARIES": "x"})
+    assert "ROCPROF_KERNEL_TRACE" in jh.profiler_attached({"ROCPROF_KERNEL_TRACE": "1"})
+
+
+def test_kernel_trace_pairs_bench_runs_with_dispatches():
+    """kernel_trace.py: each labelled run is the next stretch of its kernel at least warm-up +
+    timed long (a set-up launch of the same kernel just before it merges into the stretch; only
+    the last `timed` count), other kernels in between are skipped."""
+    import kernel_trace as kt
+    ds = [("void jh::gemm_big<256, 9, false>(GemmParams)", 50.0)]  # set-up launch, same name
+    ds += [("void jh::gemm_big<256, 9, false>(GemmParams)", 40.0)] * 3  # warm-up
+    ds += [("void jh::gemm_big<256, 9, false>(GemmParams)", 30.0 + i) for i in range(4)]
+    ds += [("jh::embed_kernel", 5.0)] * 9
+    ds += [("void jh::gemm_lat1<48, 20>(GemmParams)", 7.0)] * 2 + [("void jh::gemm_lat1<48, 20>(GemmParams)", 6.0)] * 4
+    labels = [{"label": "wo@4096", "kernel": "gemm_big<256, 9, false>", "warmup": 3, "timed": 4},
+              {"label": "qkv@293", "kernel": "gemm_lat1<48, 20>", "warmup": 2, "timed": 4}]
+    runs = kt.pair(ds, labels)
+    assert runs["wo@4096"]["launches"] == 4 and runs["wo@4096"]["avg_us"] == 31.5
+    assert runs["wo@4096"]["min_us"] == 30.0 and runs["wo@4096"]["max_us"] == 33.0
+    assert runs["qkv@293"]["avg_us"] == 6.0
+    with pytest.raises(SystemExit):
+        kt.pair(ds, labels + [{"label": "x", "kernel": "gemm_big", "warmup": 1, "timed": 1}])
