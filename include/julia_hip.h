@@ -268,6 +268,9 @@ typedef struct {
     float norm_eps, head_eps;
     uint64_t seed;
     size_t weight_bytes_f16, weight_bytes_f32;
+    /* persistent-kernel launches the runtime refused since the engine was loaded (another
+     * process held the GPU's cooperative-launch resource); those passes ran per-step */
+    size_t coop_refused;
 } julia_hip_engine_info;
 int julia_hip_engine_info_get(const Engine *e, julia_hip_engine_info *out);
 /* src/checkpoint.rs:27-62 `Checkpoint::open` (without a GPU): opens and checks a checkpoint

@@ -1129,6 +1129,7 @@ int julia_hip_engine_info_get(const Engine* e, julia_hip_engine_info* out) {
     out->max_positions = c.max_positions, out->max_length = e->max_length, out->cus = e->cus;
     out->norm_eps = c.norm_eps, out->head_eps = c.head_eps, out->seed = c.seed;
     out->weight_bytes_f16 = e->n16 * 2, out->weight_bytes_f32 = e->n32 * 4;
+    out->coop_refused = e->layer_kernel.refused();
     return 0;
 }
 

@@ -132,6 +132,7 @@ public:
         return a.xa + (size_t)(2 * (a.first + a.count - 1) + 1) * a.x_stride;
     }
     int per_cu() const { return per_cu_; }
+    size_t refused() const { return refused_; }  // cooperative launches the runtime refused
     bool available() const { return per_cu_ > 0; }
     // A plan for large batches: every GEMM on the 128 x 128 throughput tile and attention on the
     // 64-query tile, run by the kernel's large-batch instance (two blocks a CU).
@@ -152,6 +153,7 @@ private:
     // each block's bounded wait gives up (the non-co-resident case, forced from the host; every
     // block still runs to its end) and the host reports the error.
     uint32_t skew_ = 0;
+    size_t refused_ = 0;
 };
 
 }  // namespace jh

@@ -773,6 +773,7 @@ bool LayerKernel::launch(const LayerArgs& a, const LayerPlan& plan, const Scratc
             // Another process holds the cooperative-launch resource: nothing was launched, and
             // the caller runs this pass on the per-step kernels. The next pass tries again.
             (void)hipGetLastError();
+            refused_++;
             return false;
         }
     } else {

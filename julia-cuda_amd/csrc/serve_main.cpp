@@ -305,6 +305,10 @@ int serve(int argc, char** argv) {
         }
     }
     fflush(stdout);
+    julia_hip_engine_info info{};
+    if (fused && julia_hip_engine_info_get(eng.get(), &info) == 0 && info.coop_refused)
+        fprintf(stderr, "layer-fused: the runtime refused %zu cooperative launches (another process "
+                "holds the resource); those requests ran on the per-step kernels\n", info.coop_refused);
     report(tokens, wall, gpu);
     return 0;
 }

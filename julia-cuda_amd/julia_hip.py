@@ -72,7 +72,8 @@ class EngineInfo(ctypes.Structure):
         "d", "layers", "inter", "vocab", "head_layers", "head_ff", "n_qtypes", "window",
         "global_every", "max_positions", "max_length", "cus")] + [
         ("norm_eps", ctypes.c_float), ("head_eps", ctypes.c_float), ("seed", ctypes.c_uint64),
-        ("weight_bytes_f16", ctypes.c_size_t), ("weight_bytes_f32", ctypes.c_size_t)]
+        ("weight_bytes_f16", ctypes.c_size_t), ("weight_bytes_f32", ctypes.c_size_t),
+        ("coop_refused", ctypes.c_size_t)]
 
 
 # Every symbol include/julia_hip.h declares.

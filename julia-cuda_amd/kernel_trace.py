@@ -7,8 +7,8 @@ duration of exactly the same launches beside it.
         python3 bench.py --section kernels,fused_gemm --path per-step --trace-labels OUT/labels.json
     python julia-cuda_amd/kernel_trace.py OUT/bk OUT/labels.json --out profiles/bench_kernels_rocprof.json
 
-A label's run is the next stretch of consecutive dispatches of its kernel (name containing the
-label's instance) at least warm-up + timed long; its timed launches are the last `timed` of the
+A label's run is the next stretch of consecutive dispatches whose kernel names contain the
+label's instance, at least warm-up + timed long; its timed launches are the last `timed` of the
 stretch. Prints a table (label, kernel, launches, average / median / min / max us) and writes
 {"runs": {label: {...}}} for bench.py.
 """
@@ -34,32 +34,38 @@ def dispatches(path):
     return [(r["Kernel_Name"], (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3) for r in rows]
 
 
-def stretches(ds):
-    """[(name, [durations])] of consecutive dispatches of one kernel."""
-    out = []
-    for name, us in ds:
-        if out and out[-1][0] == name:
-            out[-1][1].append(us)
+def stretches(ds, part):
+    """[(first index, [names], [durations])] of maximal runs of consecutive dispatches whose
+    kernel names contain `part` (one instance, or several: the attention step alternates the
+    global and window layers' kernels)."""
+    out, cur = [], None
+    for i, (name, us) in enumerate(ds):
+        if part in name:
+            if cur is None:
+                cur = (i, [], [])
+                out.append(cur)
+            cur[1].append(name)
+            cur[2].append(us)
         else:
-            out.append((name, [us]))
+            cur = None
     return out
 
 
 def pair(ds, labels):
     runs, at = {}, 0
-    st = stretches(ds)
     for lab in labels:
         need = lab["warmup"] + lab["timed"]
-        while at < len(st) and not (lab["kernel"] in st[at][0] and len(st[at][1]) >= need):
-            at += 1
-        if at == len(st):
+        found = [s for s in stretches(ds, lab["kernel"]) if s[0] >= at and len(s[2]) >= need]
+        if not found:
             raise SystemExit(f"no run of {lab['kernel']} ({need} launches) for {lab['label']}")
-        us = st[at][1][-lab["timed"]:]
-        runs[lab["label"]] = {"kernel": lab["kernel"], "name": st[at][0], "launches": len(us),
+        i0, names, durs = found[0]
+        us = durs[-lab["timed"]:]
+        names = sorted(set(names[-lab["timed"]:]))
+        runs[lab["label"]] = {"kernel": lab["kernel"], "name": " + ".join(names), "launches": len(us),
                               "avg_us": round(statistics.mean(us), 3),
                               "median_us": round(statistics.median(us), 3),
                               "min_us": round(min(us), 3), "max_us": round(max(us), 3)}
-        at += 1
+        at = i0 + len(durs)
     return runs
 
 

@@ -12,6 +12,7 @@ tokenization of the reference's JSONL requests stays unpinned."""
 import json
 import math
 import os
+import re
 import subprocess
 
 import numpy as np
@@ -77,6 +78,10 @@ def test_serve_usage():
     assert r.returncode == 2 and "not a number" in r.stderr
 
 
+def say(*a):
+    print(*a, flush=True)
+
+
 SMALL = "synthetic:d=384,layers=4,inter=1152,vocab=1000,head_ff=768,max_positions=2048,seed=7"
 
 
@@ -102,8 +107,14 @@ def test_serve_results_match_julia_cuda_run(torch_cuda, tmp_path, fused):
     assert r.returncode == 0, r.stderr
     out = [json.loads(x) for x in r.stdout.splitlines()]
     assert len(out) == len(reqs)
+    # A child of this process, which holds the GPU's cooperative-launch resource, may have its
+    # persistent launches refused: it then reports it and runs those requests per-step.
+    refused = re.search(r"refused (\d+) cooperative launches", r.stderr)
+    per_step = fused and refused is not None
+    if per_step:
+        say(f"julia-serve: {refused.group(1)} cooperative launches refused, compared per-step")
     with jh.Engine(SMALL, max_length=512) as e:
-        want, _ = e.run(reqs, layer_fused=fused)
+        want, _ = e.run(reqs, layer_fused=fused and not per_step)
     for i, (res, (ids, markers, q), w) in enumerate(zip(out, reqs, want)):
         np.testing.assert_array_equal(np.array(res["logits"], np.float32), w)
         v, p = jh.answer(q, w)
