@@ -97,13 +97,20 @@ def row_bytes(step, m):
 
 def bandwidth_kernels(eng, m):
     """embed, norm_add and score (every row) on m rows: median us over back-to-back launches,
-    GB/s of algorithmic bytes and the fraction of the HBM peak."""
+    GB/s of algorithmic bytes and the fraction of the HBM peak; beside each, the library's plain
+    copy kernel moving the same bytes (half read, half written) in the same run: the rate this
+    transfer size reaches, and the kernel's fraction of it."""
     res = {}
     for step in ("embed", "norm_add", "score"):
         _, md = eng.time_step(step, m, warmup=10, batches=5, per_batch=40)
         b = row_bytes(step, m)
+        half = (b // 2 + 15) // 16 * 16
+        _, cp = jh.time_copy(half, warmup=10, batches=5, per_batch=40)
         res[step] = {"us": round(md, 3), "bytes": b, "GBps": round(b / (md * 1e-6) / 1e9, 1),
-                     "frac_hbm": round(b / (md * 1e-6) / PEAK_HBM, 4)}
+                     "frac_hbm": round(b / (md * 1e-6) / PEAK_HBM, 4),
+                     "copy_same_bytes_us": round(cp, 3),
+                     "copy_frac_hbm": round(2 * half / (cp * 1e-6) / PEAK_HBM, 4),
+                     "frac_of_copy": round(cp / md, 4)}
     return res
 
 

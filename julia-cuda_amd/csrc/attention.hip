@@ -77,22 +77,6 @@ bool attention_prepare() {
     return ok;
 }
 
-namespace {
-
-int device_cus() {  // (queried once per device)
-    static int cus[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cus[dev] == 0) {
-        int n = 0;
-        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cus[dev] = n;
-    }
-    return cus[dev];
-}
-
-}  // namespace
-
 // Waves per block of the LDS-resident kernel: eight when a slice takes more than four key steps
 // and the grid is at most a block a CU (measured: with two blocks on some CUs, eight-wave blocks
 // lose to four-wave ones, e.g. a +-64 window over 448 rows, 5.2 against 4.8 us).

@@ -833,13 +833,6 @@ static Gemm to_gemm(const julia_hip_gemm_args* g) {
     return x;
 }
 
-static int device_cus() {
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) == hipSuccess)
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    return cus > 0 ? cus : 256;
-}
-
 static Scratch scratch_of(const julia_hip_scratch* s) { return s ? s->s : Scratch{}; }
 
 int julia_hip_gemm(const julia_hip_gemm_args* g, julia_hip_gemm_config cfg,

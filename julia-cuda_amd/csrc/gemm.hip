@@ -78,7 +78,8 @@ std::string cfg_str(GemmConfig c) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Compute units of the current device (queried once per device).
+}  // namespace
+
 int device_cus() {
     static int cus[64] = {};
     int dev = 0;
@@ -90,8 +91,6 @@ int device_cus() {
     }
     return cus[dev];
 }
-
-}  // namespace
 
 // Split-K scratch: a tile's f32 partial per split, and an arrival counter per tile. A split
 // latency tile runs on four waves (gemm_lat, gemm_w_tile: 256 threads, 32 rows an epilogue pass),

@@ -138,6 +138,8 @@ void gemm_launch(const Gemm& g, GemmConfig cfg, const Scratch& s, hipStream_t st
 // (the throughput tiles only where they take the epilogue: LayerNorm up to k = GEMM_BIG_LN_MAX_K).
 GemmConfig gemm_choose(int m, int n, int k, int cus, int epi = 0);
 constexpr int GEMM_BIG_LN_MAX_K = 1024;
+// Compute units of the current device (queried once per device; 256 if the query fails).
+int device_cus();
 size_t gemm_ws_floats(int m, int n, GemmConfig cfg);
 size_t gemm_counters(int m, int n, GemmConfig cfg);
 // gemm_launch with the split-K partials and counters in the library's static device scratch

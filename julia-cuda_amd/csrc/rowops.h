@@ -49,13 +49,11 @@ __device__ __forceinline__ float2 ln_two_pass(const float (&v)[NC][4], int d, in
     return make_float2(mean, 1.0f / sqrtf(var + eps));
 }
 
-// x[row] = LN(table[ids[row]]) . gamma, rounded to f16 (kernels/src/main.rs:47-103).
+// x[row] = LN(v) . gamma, rounded to f16, for v = table row ids[row] loaded by load_row
+// (kernels/src/main.rs:47-103).
 template <int NC, bool XG>
-__device__ __forceinline__ void embed_row(const uint32_t* ids, int row, const f16* table, int vocab,
-                                          int d, const float* gamma, float eps, f16* x, int lane) {
-    const uint32_t id = min(ids[row], (uint32_t)(vocab - 1));  // the host checks ids < vocab
-    float v[NC][4];
-    load_row<NC>(table + (size_t)id * d, d, lane, v);
+__device__ __forceinline__ void embed_store(const float (&v)[NC][4], int row, int d,
+                                            const float* gamma, float eps, f16* x, int lane) {
     const float2 st = ln_two_pass<NC>(v, d, lane, eps);
 #pragma unroll
     for (int j = 0; j < NC; j++) {
@@ -71,16 +69,30 @@ __device__ __forceinline__ void embed_row(const uint32_t* ids, int row, const f1
     }
 }
 
-// out[row] = LN(x[row]) . gamma + add (+ row_type[row] * d when row_type is given);
-// stats[row][g] = (sum, sum of squares) of the stored f16 values of 64-column group g (chunks
-// 16 g .. 16 g + 15: lanes 16 (g % 4) .. + 15 of step g / 4) (kernels/src/main.rs:108-176).
+// The table row of token id (clamped: the host checks ids < vocab).
+__device__ __forceinline__ const f16* embed_src(const f16* table, uint32_t id, int vocab, int d) {
+    return table + (size_t)min(id, (uint32_t)(vocab - 1)) * d;
+}
+
+// x[row] = LN(table[ids[row]]) . gamma, rounded to f16 (kernels/src/main.rs:47-103).
 template <int NC, bool XG>
-__device__ __forceinline__ void norm_add_row(const f16* x, int row, int d, const float* gamma,
-                                             const float* add, const int32_t* row_type, float eps,
-                                             f16* out, float* stats, int lane) {
-    if (row_type) add += (size_t)row_type[row] * d;
+__device__ __forceinline__ void embed_row(const uint32_t* ids, int row, const f16* table, int vocab,
+                                          int d, const float* gamma, float eps, f16* x, int lane) {
     float v[NC][4];
-    load_row<NC>(x + (size_t)row * d, d, lane, v);
+    load_row<NC>(embed_src(table, ids[row], vocab, d), d, lane, v);
+    embed_store<NC, XG>(v, row, d, gamma, eps, x, lane);
+}
+
+// out[row] = LN(v) . gamma + add (+ row_type[row] * d when row_type is given), v = x[row] loaded
+// by load_row; stats[row][g] = (sum, sum of squares) of the stored f16 values of 64-column group
+// g (chunks 16 g .. 16 g + 15: lanes 16 (g % 4) .. + 15 of step g / 4)
+// (kernels/src/main.rs:108-176).
+template <int NC, bool XG>
+__device__ __forceinline__ void norm_add_store(const float (&v)[NC][4], int row, int d,
+                                               const float* gamma, const float* add,
+                                               const int32_t* row_type, float eps, f16* out,
+                                               float* stats, int lane) {
+    if (row_type) add += (size_t)row_type[row] * d;
     const float2 st = ln_two_pass<NC>(v, d, lane, eps);
 #pragma unroll
     for (int j = 0; j < NC; j++) {
@@ -107,6 +119,29 @@ __device__ __forceinline__ void norm_add_row(const f16* x, int row, int d, const
     }
 }
 
+// norm_add_store of row `row` of x.
+template <int NC, bool XG>
+__device__ __forceinline__ void norm_add_row(const f16* x, int row, int d, const float* gamma,
+                                             const float* add, const int32_t* row_type, float eps,
+                                             f16* out, float* stats, int lane) {
+    float v[NC][4];
+    load_row<NC>(x + (size_t)row * d, d, lane, v);
+    norm_add_store<NC, XG>(v, row, d, gamma, add, row_type, eps, out, stats, lane);
+}
+
+// logits[i] = v . u + b for a loaded row v and the loaded weights u (kernels/src/main.rs:180-200).
+template <int NC>
+__device__ __forceinline__ void score_dot(const float (&v)[NC][4], const float (&u)[NC][4], float b,
+                                          int i, float* logits, int lane) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NC; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) acc += v[j][e] * u[j][e];
+    acc = wave_sum(acc);
+    if (lane == 0) logits[i] = acc + b;
+}
+
 // logits[i] = y[markers[i]] . w + b (kernels/src/main.rs:180-200); markers null: row i.
 template <int NC>
 __device__ __forceinline__ void score_row(const f16* y, int n, int d, const f16* w, float b,
@@ -116,13 +151,7 @@ __device__ __forceinline__ void score_row(const f16* y, int n, int d, const f16*
     float v[NC][4], u[NC][4];
     load_row<NC>(y + (size_t)r * d, d, lane, v);
     load_row<NC>(w, d, lane, u);
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NC; j++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) acc += v[j][e] * u[j][e];
-    acc = wave_sum(acc);
-    if (lane == 0) logits[i] = acc + b;
+    score_dot<NC>(v, u, b, i, logits, lane);
 }
 
 }  // namespace jh
