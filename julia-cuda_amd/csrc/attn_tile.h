@@ -479,6 +479,78 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
 constexpr int ATT_STREAM_STAGES = 2;
 constexpr int ATT_STREAM_LDS = ATT_STREAM_STAGES * 16384;
 
+// One 64-key block of the streaming tile for a wave's 16 queries (lane l: query l % 16): S^T for
+// keys kb + 16 t + 4 g + e (t < 4) from the block's K fragments, one max and one rescale, P . V in
+// two K-32 halves. full: every score is valid; else key kb + 16 t + 4 g + e is valid iff
+// (uint32_t)(base + 16 t + e) < kspan, base = kb + 4 g - (the lane's first valid key).
+__device__ __forceinline__ void att_stream_block(const half8 (&kf)[4][2], const half4 (&vlo)[2][4],
+                                                 const half4 (&vhi)[2][4], const half8 (&qf)[2],
+                                                 bool full, int base, uint32_t kspan, float& mx,
+                                                 float& lsum, floatx4 (&oacc)[4]) {
+    const float scale = 1.4426950408889634f / 8.0f;  // log2(e) / sqrt(64)
+    floatx4 sc[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        sc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k2 = 0; k2 < 2; k2++) sc[t] = mfma16(kf[t][k2], qf[k2], sc[t]);
+    }
+    float bm = -INFINITY;
+    if (full) {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                bm = fmaxf(bm, sc[t][e]);
+            }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const bool ok = (uint32_t)(base + 16 * t + e) < kspan;
+                sc[t][e] = ok ? sc[t][e] : -INFINITY;
+                bm = fmaxf(bm, sc[t][e]);
+            }
+    }
+    bm = max_xor32(max_xor16(bm)) * scale;  // the scores stay unscaled until the exponent
+    const float mnew = fmaxf(mx, bm);
+    const float b0 = mnew == -INFINITY ? 0.0f : mnew;  // no valid key yet: exp2(-inf) = 0
+    const float alpha = fast_exp2(mx - b0);
+    // The output needs rescaling only where a lane's max rose (alpha < 1): skipped when no lane
+    // of the wave has (a wave-uniform test).
+    const bool rescale = __builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0;
+    mx = mnew;
+    float rs = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            sc[t][e] = fast_exp2(fmaf(sc[t][e], scale, -b0));
+            rs += sc[t][e];
+        }
+    lsum = lsum * alpha + rs;
+    if (rescale) {
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) oacc[dt] = oacc[dt] * alpha;
+    }
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+        half8 pf;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            pf[e] = (f16)sc[2 * hf][e];
+            pf[4 + e] = (f16)sc[2 * hf + 1][e];
+        }
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++) {
+            const half4 lo = vlo[hf][dt], hi = vhi[hf][dt];
+            const half8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            oacc[dt] = mfma16(vf, pf, oacc[dt]);
+        }
+    }
+}
+
 // Task `task` of (n + 16 NW - 1) / (16 NW) query blocks x heads (XCD-mapped); `lds`:
 // KS x ATT_STREAM_LDS bytes; 64 NW KS threads. XS: o is stored device-coherent (the persistent
 // kernel). Ends with a block barrier.
@@ -566,7 +638,6 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
         qf[1] = load16h<false>(qp + 32);
     }
 
-    const float scale = 1.4426950408889634f / 8.0f;  // log2(e) / sqrt(64)
     float mx = -INFINITY, lsum = 0.0f;
     floatx4 oacc[4];
 #pragma unroll
@@ -620,71 +691,9 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
         if (has(b + 1)) stage(kg + KS * (b + 1), (ST + 1) % NS);
         __builtin_amdgcn_sched_barrier(0);
         if (!act) return;
-        floatx4 sc[4];
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            sc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int k2 = 0; k2 < 2; k2++) sc[t] = mfma16(kf[t][k2], qf[k2], sc[t]);
-        }
         const bool full = one_seq && kb >= ulo && kb + 64 <= uhi &&
                           (p.window == 0 || (wql - kb <= p.window && kb + 63 - wq0 <= p.window));
-        float bm = -INFINITY;
-        if (full) {
-#pragma unroll
-            for (int t = 0; t < 4; t++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    bm = fmaxf(bm, sc[t][e]);
-                }
-        } else {
-            // key kb + 16 t + 4 g + e is valid iff it lies in [klo, khi)
-            const int base = kb + 4 * g - klo;
-#pragma unroll
-            for (int t = 0; t < 4; t++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const bool ok = (uint32_t)(base + 16 * t + e) < kspan;
-                    sc[t][e] = ok ? sc[t][e] : -INFINITY;
-                    bm = fmaxf(bm, sc[t][e]);
-                }
-        }
-        bm = max_xor32(max_xor16(bm)) * scale;  // the scores stay unscaled until the exponent
-        const float mnew = fmaxf(mx, bm);
-        const float base = mnew == -INFINITY ? 0.0f : mnew;  // no valid key yet: exp2(-inf) = 0
-        const float alpha = fast_exp2(mx - base);
-        // The output needs rescaling only where a lane's max rose (alpha < 1): skipped when no
-        // lane of the wave has (a wave-uniform test).
-        const bool rescale = __builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0;
-        mx = mnew;
-        float rs = 0.0f;
-#pragma unroll
-        for (int t = 0; t < 4; t++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                sc[t][e] = fast_exp2(fmaf(sc[t][e], scale, -base));
-                rs += sc[t][e];
-            }
-        lsum = lsum * alpha + rs;
-        if (rescale) {
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++) oacc[dt] = oacc[dt] * alpha;
-        }
-#pragma unroll
-        for (int hf = 0; hf < 2; hf++) {
-            half8 pf;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                pf[e] = (f16)sc[2 * hf][e];
-                pf[4 + e] = (f16)sc[2 * hf + 1][e];
-            }
-#pragma unroll
-            for (int dt = 0; dt < 4; dt++) {
-                const half4 lo = vlo[hf][dt], hi = vhi[hf][dt];
-                const half8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                oacc[dt] = mfma16(vf, pf, oacc[dt]);
-            }
-        }
+        att_stream_block(kf, vlo, vhi, qf, full, kb + 4 * g - klo, kspan, mx, lsum, oacc);
     };
 
     static_assert(NS == 2, "the loop below is unrolled by the stages");
