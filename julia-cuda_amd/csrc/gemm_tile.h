@@ -9,10 +9,18 @@
 
 namespace jh {
 
-// LDS floats gemm_lat_tile<BM> needs with NW waves: their partial BM x 64 tiles, rows padded
-// to 68.
+// The LDS slot (floats) of one wave of a BM-row latency tile: its partial BM x 64 tile (rows
+// padded to 68 floats); with eight waves also its staged activation lines first (lat_stage_lines
+// lines of 128 bytes a row: 32 floats each), when they fit the CU's 160 KB.
+template <int BM, int NW>
+constexpr int lat_stage_lines() { return NW != 8 ? 0 : (8 * BM * 96 * 4 <= 150 * 1024 ? 3 : 2); }
+template <int BM, int NW>
+constexpr int lat_slot_floats() {
+    return BM * 68 > BM * 32 * lat_stage_lines<BM, NW>() ? BM * 68 : BM * 32 * lat_stage_lines<BM, NW>();
+}
+// LDS floats gemm_lat_tile<BM> needs with NW waves.
 template <int BM, int NW = 4>
-constexpr int lat_lds_floats() { return NW * BM * 68; }
+constexpr int lat_lds_floats() { return NW * lat_slot_floats<BM, NW>(); }
 
 // Rows of one epilogue pass of a four-wave latency tile (256 threads, 8 a row): the unit in which
 // a K split's partial tile is stored (gemm_ws_floats sizes the scratch by it). Only four-wave
@@ -122,6 +130,7 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     constexpr int MI = BM / 16;
     constexpr int RPP = 8 * NW;                     // tile rows a pass of the epilogue
     constexpr int NPASS = (BM + RPP - 1) / RPP;
+    constexpr int SLOT = lat_slot_floats<BM, NW>();  // a wave's LDS floats
     static_assert(NW != 4 || RPP == LAT_SPLIT_PASS_ROWS, "split partials are sized by 32-row passes");
     const int T = p.tiles_n * p.tiles_m * p.splits;
     const int L = xcd_task(task, T);
@@ -233,9 +242,40 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
         }
     };
     // Every K step of the wave in one chunk (eight waves: three to five steps a wave).
-    auto kone = [&](auto uc_) {
+    //
+    // With LDS staging (STAGE: the wave's K range spans at most NL 128-byte lines a row, and its
+    // slot holds them), a is copied into the wave's own LDS slot as whole lines and the fragments
+    // are read from there. A fragment load straight from memory takes 16 rows x 64 bytes (the
+    // MFMA gives lane l row l % 16 and 8 K values of a 32-wide unit), half a 128-byte line a
+    // row, so the next unit's load asks for the same lines again; a CU's intake follows the
+    // number of line requests more than the bytes (measured at 293 rows: time ~ 2.2 us + 2 ns a
+    // line request over the tile heights, the same for 16 x 64 and 32 x 32 tiles of equal
+    // request counts). A direct copy here takes 8 rows x 128 bytes: half the requests for a.
+    // Copy q = line x (BM / 8) + rb holds rows 8 rb .. 8 rb + 7 of line L0 + line at slot bytes
+    // 1024 q + 128 (r % 8) + 16 (c ^ sw(r)), c the 16-byte chunk of the line, sw(r) = (r % 8) ^
+    // ((r / 8) % 2): the 16 rows one fragment read takes cover the 64 banks.
+    auto kone = [&](auto uc_, auto stage_) {
         constexpr int UC = decltype(uc_)::value;
+        constexpr bool STAGE = decltype(stage_)::value;
+        constexpr int NL = (UC + 2) / 2;  // lines a row a K range of UC units can touch
+        static_assert(!STAGE || NL * BM * 32 <= SLOT, "the staged lines fit the wave's slot");
         half8 fa[UC][MI], fw[UC][4];
+        char* const slot = (char*)(red + w * SLOT);
+        const int L0 = u0 >> 1, nline = (p.k >> 6);  // first line of the range, lines a row
+        auto swz = [](int r) { return (r & 7) ^ ((r >> 3) & 1); };
+        if (STAGE) {
+#pragma unroll
+            for (int li = 0; li < NL; li++)
+#pragma unroll
+                for (int rb = 0; rb < BM / 8; rb++) {
+                    const int r = 8 * rb + (l >> 3);
+                    const int row = min(by * BM + r, p.m - 1);  // rows past m: read, never stored
+                    const int line = min(L0 + li, nline - 1);
+                    const f16* src = (const f16*)p.a + (size_t)src_row<EPI>(p, row) * p.k + line * 64 +
+                                     ((l & 7) ^ swz(r)) * 8;
+                    lds_dma16<XG>(src, slot + (li * (BM / 8) + rb) * 1024);
+                }
+        }
         const auto wr = buffer_rsrc((const f16*)p.w + ((size_t)bx * U + u0) * 2048,
                                     (uint32_t)(u1 - u0) * 4096);
 #pragma unroll
@@ -243,14 +283,32 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
             const int uu = min(u0 + s, u1 - 1);
 #pragma unroll
             for (int j = 0; j < 4; j++) fw[s][j] = bload16<false>(wr, (uint32_t)s * 4096 + j * 1024 + l * 16);
+            if (!STAGE) {
 #pragma unroll
-            for (int i = 0; i < MI; i++) fa[s][i] = load16h<XG>(ap[i] + uu * 32);
+                for (int i = 0; i < MI; i++) fa[s][i] = load16h<XG>(ap[i] + uu * 32);
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, c0, er[ps]);
         __builtin_amdgcn_sched_barrier(0);
         if (late) __builtin_amdgcn_s_barrier();  // the halves' first barrier (see `two`)
+        __builtin_amdgcn_sched_barrier(0);
+        if (STAGE) {
+            // The copies are this wave's oldest loads in flight: w's fragments and the RoPE rows,
+            // issued after them, may still be.
+            wait_vmcnt<4 * UC + ((EPI & EPI_ROPE) ? 2 * NPASS : 0)>();
+#pragma unroll
+            for (int s = 0; s < UC; s++) {
+                const int uu = min(u0 + s, u1 - 1);
+#pragma unroll
+                for (int i = 0; i < MI; i++) {
+                    const int r = 16 * i + r16, c = 4 * (uu & 1) + g;
+                    const int q = ((uu >> 1) - L0) * (BM / 8) + (r >> 3);
+                    fa[s][i] = *(const half8*)(slot + q * 1024 + (r & 7) * 128 + 16 * (c ^ swz(r)));
+                }
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < UC; s++) {
@@ -263,10 +321,12 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
             }
         }
     };
+    using ST2 = std::integral_constant<bool, (lat_stage_lines<BM, NW>() >= 2)>;
+    using ST3 = std::integral_constant<bool, (lat_stage_lines<BM, NW>() >= 3)>;
     if (NW == 8 && u1 - u0 <= 3) {
-        kone(std::integral_constant<int, 3>{});
+        kone(std::integral_constant<int, 3>{}, ST2{});
     } else if (NW == 8 && u1 - u0 <= 5) {
-        kone(std::integral_constant<int, 5>{});
+        kone(std::integral_constant<int, 5>{}, ST3{});
     } else if (ONE && MI > 1) {
         if (u1 - u0 > 6)
             kloop(std::integral_constant<int, 5>{});
@@ -285,7 +345,7 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     for (int i = 0; i < MI; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            *(floatx4*)&red[(w * BM + 16 * i + r16) * 68 + 16 * j + 4 * g] = acc[i][j];
+            *(floatx4*)&red[w * SLOT + (16 * i + r16) * 68 + 16 * j + 4 * g] = acc[i][j];
     // The partials summed in wave order, from slot `from` on (0: all eight; two: the half sum in
     // slot 0, then waves 4-7).
     auto sum_slots = [&](float (&v)[NPASS][8], int from) {
@@ -298,8 +358,8 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
 #pragma unroll
                 for (int ww = 0; ww < NW; ww++) {
                     if (ww > 0 && ww < from) continue;
-                    const float4 lo = *(const float4*)&red[(ww * BM + r) * 68 + c0];
-                    const float4 hi = *(const float4*)&red[(ww * BM + r) * 68 + 32 + c0];
+                    const float4 lo = *(const float4*)&red[ww * SLOT + r * 68 + c0];
+                    const float4 hi = *(const float4*)&red[ww * SLOT + r * 68 + 32 + c0];
                     v[ps][0] += lo.x, v[ps][1] += lo.y, v[ps][2] += lo.z, v[ps][3] += lo.w;
                     v[ps][4] += hi.x, v[ps][5] += hi.y, v[ps][6] += hi.z, v[ps][7] += hi.w;
                 }
@@ -319,7 +379,7 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
                 float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
                 for (int ww = 0; ww < NW / 2; ww++) {
-                    const float4 b = *(const float4*)(e0 + ww * BM * 68);
+                    const float4 b = *(const float4*)(e0 + ww * SLOT);
                     a.x += b.x, a.y += b.y, a.z += b.z, a.w += b.w;
                 }
                 *(float4*)e0 = a;
