@@ -205,12 +205,16 @@ def path_ms(t):
     return {"mean": round(t[0], 4), "median": round(t[1], 4), "wall": round(t[2], 4)}
 
 
-def gemm_instance(m, n, bm, epi, cus):
-    """The kernel instance the engine launches for a GEMM on m rows with tile height bm."""
+def gemm_instance(m, n, k, bm, epi, cus):
+    """The kernel instance the engine launches for an m x n x k GEMM with tile height bm (one
+    K split)."""
     if bm >= 128:
         return f"gemm_big<{bm}, {jh.EPI[epi]}, false>"
-    one = (n // 64) * -(-m // bm) <= cus  # the eight-wave instance: at most a block a CU
-    return f"gemm_{'lat1' if one else 'lat'}<{bm}, {jh.EPI[epi]}>"
+    if (n // 64) * -(-m // bm) <= cus and k >= 256:  # the eight-wave instance: a block a CU at most
+        most = (k // 32 + 7) // 8  # K steps of the busiest wave: its K path
+        path = 3 if most <= 3 else 5 if most <= 5 else 1
+        return f"gemm_lat1<{bm}, {jh.EPI[epi]}, {path}>"
+    return f"gemm_lat<{bm}, {jh.EPI[epi]}>"
 
 
 def roofline(kern, steps, kname):
@@ -347,7 +351,7 @@ def main():
         kern = {}
         for step, (n, k, epi, cnt) in STEP_SHAPES.items():
             cfg = list(jh.gemm_choose(293, n, k, info.cus, epi))
-            kname = gemm_instance(293, n, cfg[0], epi, info.cus)
+            kname = gemm_instance(293, n, k, cfg[0], epi, info.cus)
             mn, md = time_step(eng, step, 293, f"{step}@293", kname)
             kern[step] = dict(us=round(md, 3), us_min=round(mn, 3), per_forward=cnt, kernel=kname,
                               bytes=gemm_bytes(293, n, k, epi), flops=2 * 293 * n * k, config=cfg)
@@ -446,7 +450,7 @@ def main():
         for m in (4096, 8192, 18752):
             for step, (n, k, epi, _) in STEP_SHAPES.items():
                 cfg = list(jh.gemm_choose(m, n, k, info.cus, epi))
-                kname = gemm_instance(m, n, cfg[0], epi, info.cus)
+                kname = gemm_instance(m, n, k, cfg[0], epi, info.cus)
                 mn, md = time_step(eng_big, step, m, f"{step}@{m}", kname, warmup=5, batches=5,
                                    per_batch=8)
                 fl = 2 * m * n * k

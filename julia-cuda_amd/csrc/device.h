@@ -344,8 +344,8 @@ template <int EPI>
 __device__ __forceinline__ int src_row(const GemmParams& p, int r) {
     return (EPI & EPI_GATHER) ? (int)min(p.rows[r], (uint32_t)(p.src_m - 1)) : r;
 }
-struct EpiRow {  // per row: statistics slots, position, RoPE (cos, sin) pairs, residual lo, hi
-    float2 st[EPI_PRE_SLOTS];
+struct EpiRow {  // per row: statistics slots, position (as loaded), RoPE (cos, sin) pairs,
+    float2 st[EPI_PRE_SLOTS];  // residual lo, hi
     int pos;
     float4 rt[2];
     half4 rl, rh;
@@ -383,8 +383,8 @@ __device__ __forceinline__ void epi_load_row(const GemmParams& p, int row, int g
         // An unconditional load (from the table itself when there are no positions): a load
         // under a branch leaves the compiler unsure where it is in the load order, and the
         // table loads that wait for it would then wait for every load issued before them.
-        const int v = *(const int*)(p.pos ? (const void*)(p.pos + r) : (const void*)p.rope);
-        e.pos = p.pos ? v : r;
+        // The choice between it and the row waits for the load: epi_load_rope makes it.
+        e.pos = *(const int*)(p.pos ? (const void*)(p.pos + r) : (const void*)p.rope);
     }
     if ((EPI & EPI_RES) && !(EPI & EPI_GEGLU)) {
         const f16* x = (const f16*)(p.res ? p.res : p.c) + (size_t)(p.res ? rs : r) * p.n + grp * 64 + c0;
@@ -393,12 +393,13 @@ __device__ __forceinline__ void epi_load_row(const GemmParams& p, int row, int g
     }
 }
 
-// The RoPE table row of e.pos (set by epi_load_row): a separate step, so that a tile issues every
-// row's position load before any table load (which waits for its position).
+// The RoPE table row of output row `row`'s position (e.pos, loaded by epi_load_row): a separate
+// step, so that a tile issues every row's position load before any table load (which waits for
+// its position).
 template <int EPI>
-__device__ __forceinline__ void epi_load_rope(const GemmParams& p, int c0, EpiRow& e) {
+__device__ __forceinline__ void epi_load_rope(const GemmParams& p, int row, int c0, EpiRow& e) {
     if (EPI & EPI_ROPE) {
-        const int pos = min(max(e.pos, 0), p.rope_rows - 1);
+        const int pos = min(max(p.pos ? e.pos : min(row, p.m - 1), 0), p.rope_rows - 1);
         const float4* t = (const float4*)(p.rope + ((size_t)pos * 32 + c0) * 2);
         e.rt[0] = t[0];
         e.rt[1] = t[1];

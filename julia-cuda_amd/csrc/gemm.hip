@@ -40,14 +40,16 @@ __global__ __launch_bounds__(256, 2) void gemm_lat(GemmParams p) {
 }
 
 // gemm_lat for grids of at most one block a CU (one request's GEMMs up to ~300 tokens): eight
-// waves split the tile's K steps, each issuing all of its three to five steps' loads at once. A CU takes in its operands from L2 faster with eight waves loading than
-// with four (measured on MI355X: ~86-94 against ~55-79 GB/s), for twice the partial tiles to sum
-// through LDS. Dynamic LDS: lat_lds_floats<BM, 8>() floats.
-template <int BM, int EPI>
+// waves split the tile's K steps, each issuing all of its three to five steps' loads at once. A
+// CU takes in its operands from L2 faster with eight waves loading than with four (measured on
+// MI355X: ~86-94 against ~55-79 GB/s), for twice the partial tiles to sum through LDS. KP: the
+// waves' K path (LAT_KONE3 / LAT_KONE5 / LAT_KLOOP), chosen by the host from K. Dynamic LDS:
+// lat_lds_floats<BM, 8>() floats.
+template <int BM, int EPI, int KP>
 __global__ __launch_bounds__(512, 1) void gemm_lat1(GemmParams p) {
     extern __shared__ __attribute__((aligned(16))) float red_dyn[];
     __shared__ uint32_t s_last;
-    gemm_lat_tile<BM, EPI, false, false, 8>(p, blockIdx.x, red_dyn, &s_last);
+    gemm_lat_tile<BM, EPI, false, false, 8, KP>(p, blockIdx.x, red_dyn, &s_last);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -173,6 +175,8 @@ void gemm_check(const Gemm& g, GemmConfig cfg, const Scratch& s) {
     if (tput && ((size_t)g.m * g.n * 2 > 0xFFFFFF00ull || (size_t)g.m * g.k * 2 > 0xFFFFFFFFull ||
                  (size_t)g.n * g.k * 2 > 0xFFFFFFFFull))  // buffer offsets: copies, epilogue
         fail("the throughput tiles take a, w and outputs up to 4 GB");
+    if (!tput && (size_t)(gather ? g.src_m : g.m) * g.k * 2 > 0xFFFFFFFFull)  // the a copies' offsets
+        fail("the latency tiles take a up to 4 GB");
     if (!tput && ksteps / cfg.splits < 4)  // each of the four waves takes a K step of every split
         fail(std::to_string(cfg.splits) + " splits leave a wave no K step of " + std::to_string(ksteps));
     if (tput && ksteps / cfg.splits < 2)  // the stage pipeline's first wait covers two stages
@@ -192,16 +196,33 @@ static void launch_big(const GemmParams& p, hipStream_t st) {
     hipLaunchKernelGGL((gemm_big<B, EPI, SPLIT>), dim3(grid), dim3(C::THREADS), (C::LDS_BYTES), st, p);
 }
 
+template <int BM, int EPI, int KP>
+static void launch_lat1(const GemmParams& p, int blocks, hipStream_t st) {
+    constexpr int LDS = lat_lds_floats<BM, 8>() * 4;
+    static const bool lds_ok =  // once per instantiation, before its first launch
+        hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_lat1<BM, EPI, KP>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, LDS) == hipSuccess;
+    if (!lds_ok) throw std::runtime_error("gemm: the one-block latency kernel cannot have its LDS");
+    hipLaunchKernelGGL((gemm_lat1<BM, EPI, KP>), dim3(blocks), dim3(512), LDS, st, p);
+}
+
+// The eight-wave kernel's K path for K: wave w of 8 takes K steps [w U / 8, (w + 1) U / 8) of
+// U = K / 32, at most ceil(U / 8).
+static int gemm_lat1_path(int k) {
+    const int most = (k / 32 + 7) / 8;
+    return most <= 3 ? LAT_KONE3 : most <= 5 ? LAT_KONE5 : LAT_KLOOP;
+}
+
 template <int BM, int EPI>
 static void launch_lat(const GemmParams& p, hipStream_t st) {
     const int blocks = p.tiles_n * p.tiles_m * p.splits;
-    if (p.splits == 1 && blocks <= device_cus()) {
-        constexpr int LDS = lat_lds_floats<BM, 8>() * 4;
-        static const bool lds_ok =  // once per instantiation, before its first launch
-            hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_lat1<BM, EPI>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, LDS) == hipSuccess;
-        if (!lds_ok) throw std::runtime_error("gemm: the one-block latency kernel cannot have its LDS");
-        hipLaunchKernelGGL((gemm_lat1<BM, EPI>), dim3(blocks), dim3(512), LDS, st, p);
+    // (Eight waves with a K step each: K >= 256.)
+    if (p.splits == 1 && blocks <= device_cus() && p.k >= 256) {
+        switch (gemm_lat1_path(p.k)) {
+            case LAT_KONE3: launch_lat1<BM, EPI, LAT_KONE3>(p, blocks, st); break;
+            case LAT_KONE5: launch_lat1<BM, EPI, LAT_KONE5>(p, blocks, st); break;
+            default: launch_lat1<BM, EPI, LAT_KLOOP>(p, blocks, st); break;
+        }
     } else {
         hipLaunchKernelGGL((gemm_lat<BM, EPI>), dim3(blocks), dim3(256), 0, st, p);
     }

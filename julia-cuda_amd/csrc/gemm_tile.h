@@ -22,6 +22,14 @@ constexpr int lat_slot_floats() {
 template <int BM, int NW = 4>
 constexpr int lat_lds_floats() { return NW * lat_slot_floats<BM, NW>(); }
 
+// The K path of an eight-wave latency tile's waves, when the kernel fixes it: every wave in one
+// chunk of three or five K steps (LAT_KONE3, LAT_KONE5) or in the chunked loop (LAT_KLOOP);
+// LAT_KANY chooses per wave at run time. One path per kernel keeps the waits exact: the compiler
+// joins run-time alternatives into one flow, and each alternative then waits for the loads the
+// others might have left in flight (measured in the generated code: a full wait ahead of the
+// three-step chunk's weight loads, for the other paths' RoPE table loads).
+enum { LAT_KANY = 0, LAT_KLOOP = 1, LAT_KONE3 = 3, LAT_KONE5 = 5 };
+
 // Rows of one epilogue pass of a four-wave latency tile (256 threads, 8 a row): the unit in which
 // a K split's partial tile is stored (gemm_ws_floats sizes the scratch by it). Only four-wave
 // tiles take a K split.
@@ -120,7 +128,7 @@ __device__ __forceinline__ void finish(const GemmParams& p, float (&v)[NPASS][8]
 // `red` right after. ONE: the block has its CU to itself (four waves: 512 registers a lane),
 // so that the 48- and 64-row tiles hold every K step of a wave in flight at once. Eight waves
 // (NW = 8) take a CU's operand loads at a higher rate than four.
-template <int BM, int EPI, bool XG = false, bool ONE = false, int NW = 4>
+template <int BM, int EPI, bool XG = false, bool ONE = false, int NW = 4, int KP = LAT_KANY>
 __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, float* red,
                                               uint32_t* s_last, uint64_t* sub = nullptr) {
     auto mark = [&](int i) {  // profiling: thread 0's view of the task's stages
@@ -159,6 +167,50 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
         const int row = min(by * BM + 16 * i + r16, p.m - 1);  // rows past m: read, never stored
         ap[i] = (const f16*)p.a + (size_t)src_row<EPI>(p, row) * p.k + 8 * g;
     }
+    // Eight waves with K ranges of up to three or five units: a goes through the wave's LDS slot
+    // as whole 128-byte lines (see kone), copied first, before any other load of the tile. The
+    // copies go through a buffer descriptor over a (the host checks that it spans at most 4 GB):
+    // the compiler counts buffer copies in order with the other loads, so the waits that follow
+    // are partial. (With global-address copies in flight it waits for every load instead.)
+    constexpr int NLS = lat_stage_lines<BM, NW>();
+    static_assert(NLS == 0 || NLS * BM * 32 <= SLOT, "the staged lines fit the wave's slot");
+    char* const slot = (char*)(red + w * SLOT);
+    const int L0 = u0 >> 1;  // the first line of the wave's K range
+    auto swz = [](int r) { return (r & 7) ^ ((r >> 3) & 1); };
+    // Lane l copies 16 bytes of row 8 rb + l / 8 a copy: one lane offset a row block (aoff,
+    // kept live until the fragment loads have gone out: the compiler would otherwise give their
+    // registers to w's fragments and wait for the copies first), the line as a scalar offset.
+    uint32_t aoff[NLS ? BM / 8 : 1];
+    auto stage_a = [&](auto nl_) {
+        constexpr int NL = decltype(nl_)::value;  // lines a row the wave's K range touches
+        const int a_rows = (EPI & EPI_GATHER) ? p.src_m : p.m;
+        const auto ar = buffer_rsrc(p.a, (uint32_t)((size_t)a_rows * p.k * 2));
+#pragma unroll
+        for (int rb = 0; rb < BM / 8; rb++) {
+            const int r = 8 * rb + (l >> 3);
+            const int row = min(by * BM + r, p.m - 1);  // rows past m: read, never stored
+            aoff[rb] = ((uint32_t)src_row<EPI>(p, row) * (uint32_t)p.k +
+                        (uint32_t)(L0 * 64 + ((l & 7) ^ swz(r)) * 8)) * 2u;
+        }
+#pragma unroll
+        for (int li = 0; li < NL; li++) {
+            const uint32_t soff = (uint32_t)(min(L0 + li, (p.k >> 6) - 1) - L0) * 128u;  // wave-uniform
+#pragma unroll
+            for (int rb = 0; rb < BM / 8; rb++)
+                lds_bdma16<XG>(ar, aoff[rb], slot + (li * (BM / 8) + rb) * 1024, soff);
+        }
+    };
+    static_assert(KP == LAT_KANY || NW == 8, "a fixed K path is an eight-wave tile's");
+    if constexpr (KP == LAT_KONE3) {
+        stage_a(std::integral_constant<int, 2>{});
+    } else if constexpr (KP == LAT_KONE5) {
+        if constexpr (NLS >= 3) stage_a(std::integral_constant<int, 3>{});
+    } else if constexpr (KP == LAT_KANY) {
+        const int nuw = u1 - u0;
+        if (NW == 8 && nuw <= 3 && NLS >= 2) stage_a(std::integral_constant<int, 2>{});
+        else if (NW == 8 && nuw > 3 && nuw <= 5 && NLS >= 3) stage_a(std::integral_constant<int, 3>{});
+    }
+
     // The epilogue's other inputs, in flight with the first operand loads.
     const int c0 = (tid & 7) * 4;
     EpiCol ec;
@@ -229,7 +281,7 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
         // first that wait would hold back the operand loads by a round trip.
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, c0, er[ps]);
+        for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, by * BM + ps * RPP + (tid >> 3), c0, er[ps]);
         for (int u = u0; u < u1; u += 2 * UC) {
             __builtin_amdgcn_sched_barrier(0);
             compute(fa0, fw0, u);
@@ -257,25 +309,7 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     auto kone = [&](auto uc_, auto stage_) {
         constexpr int UC = decltype(uc_)::value;
         constexpr bool STAGE = decltype(stage_)::value;
-        constexpr int NL = (UC + 2) / 2;  // lines a row a K range of UC units can touch
-        static_assert(!STAGE || NL * BM * 32 <= SLOT, "the staged lines fit the wave's slot");
         half8 fa[UC][MI], fw[UC][4];
-        char* const slot = (char*)(red + w * SLOT);
-        const int L0 = u0 >> 1, nline = (p.k >> 6);  // first line of the range, lines a row
-        auto swz = [](int r) { return (r & 7) ^ ((r >> 3) & 1); };
-        if (STAGE) {
-#pragma unroll
-            for (int li = 0; li < NL; li++)
-#pragma unroll
-                for (int rb = 0; rb < BM / 8; rb++) {
-                    const int r = 8 * rb + (l >> 3);
-                    const int row = min(by * BM + r, p.m - 1);  // rows past m: read, never stored
-                    const int line = min(L0 + li, nline - 1);
-                    const f16* src = (const f16*)p.a + (size_t)src_row<EPI>(p, row) * p.k + line * 64 +
-                                     ((l & 7) ^ swz(r)) * 8;
-                    lds_dma16<XG>(src, slot + (li * (BM / 8) + rb) * 1024);
-                }
-        }
         const auto wr = buffer_rsrc((const f16*)p.w + ((size_t)bx * U + u0) * 2048,
                                     (uint32_t)(u1 - u0) * 4096);
 #pragma unroll
@@ -288,16 +322,27 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
                 for (int i = 0; i < MI; i++) fa[s][i] = load16h<XG>(ap[i] + uu * 32);
             }
         }
-        __builtin_amdgcn_sched_barrier(0);
+        if (STAGE) {
 #pragma unroll
-        for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, c0, er[ps]);
+            for (int rb = 0; rb < BM / 8; rb++) asm volatile("" ::"v"(aoff[rb]));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // The RoPE table loads wait for the positions. While copies into LDS are in flight the
+        // compiler takes any such wait as one for every load (it does not count the copies in
+        // order with the other loads), so with STAGE they follow the explicit wait below.
+        if (!STAGE) {
+#pragma unroll
+            for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, by * BM + ps * RPP + (tid >> 3), c0, er[ps]);
+        }
         __builtin_amdgcn_sched_barrier(0);
         if (late) __builtin_amdgcn_s_barrier();  // the halves' first barrier (see `two`)
         __builtin_amdgcn_sched_barrier(0);
         if (STAGE) {
-            // The copies are this wave's oldest loads in flight: w's fragments and the RoPE rows,
-            // issued after them, may still be.
-            wait_vmcnt<4 * UC + ((EPI & EPI_ROPE) ? 2 * NPASS : 0)>();
+            // The copies went out before every other load of the tile (stage_a): waiting until
+            // at most w's 4 UC fragment loads are in flight covers them.
+            wait_vmcnt<4 * UC>();
+#pragma unroll
+            for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, by * BM + ps * RPP + (tid >> 3), c0, er[ps]);
 #pragma unroll
             for (int s = 0; s < UC; s++) {
                 const int uu = min(u0 + s, u1 - 1);
@@ -323,9 +368,13 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     };
     using ST2 = std::integral_constant<bool, (lat_stage_lines<BM, NW>() >= 2)>;
     using ST3 = std::integral_constant<bool, (lat_stage_lines<BM, NW>() >= 3)>;
-    if (NW == 8 && u1 - u0 <= 3) {
+    if constexpr (KP == LAT_KONE3) {
         kone(std::integral_constant<int, 3>{}, ST2{});
-    } else if (NW == 8 && u1 - u0 <= 5) {
+    } else if constexpr (KP == LAT_KONE5) {
+        kone(std::integral_constant<int, 5>{}, ST3{});
+    } else if (KP == LAT_KANY && NW == 8 && u1 - u0 <= 3) {
+        kone(std::integral_constant<int, 3>{}, ST2{});
+    } else if (KP == LAT_KANY && NW == 8 && u1 - u0 <= 5) {
         kone(std::integral_constant<int, 5>{}, ST3{});
     } else if (ONE && MI > 1) {
         if (u1 - u0 > 6)
@@ -473,7 +522,7 @@ __device__ __forceinline__ void gemm_w_tile(const GemmParams& p, int task, char*
 #pragma unroll
     for (int ps = 0; ps < NPASS; ps++) epi_load_row<EPI, true, false>(p, by * BM + ps * 32 + (tid >> 3), bx, c0, er[ps]);
 #pragma unroll
-    for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, c0, er[ps]);
+    for (int ps = 0; ps < NPASS; ps++) epi_load_rope<EPI>(p, by * BM + ps * 32 + (tid >> 3), c0, er[ps]);
 
     const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(p.a, (uint32_t)p.m * (uint32_t)p.k * 2u);
     uint32_t aoff[MI];
