@@ -375,7 +375,7 @@ def main():
         out["kernels_293"] = kern
         out["bandwidth_kernels"] = {"293_rows": bandwidth_kernels(eng, 293)}
         # The roofline: the kernel instance with the largest share of the forward's GPU time
-        # (wo and wo_mlp share one instance), and config 1's qkv GEMM beside it.
+        # (steps that share an instance count together), and config 1's qkv GEMM beside it.
         by_inst = {}
         for step in STEP_SHAPES:
             by_inst.setdefault(kern[step]["kernel"], []).append(step)

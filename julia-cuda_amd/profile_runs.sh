@@ -24,7 +24,7 @@ if has trace; then
         --out $NEW/bench_kernels_rocprof.json > $NEW/bench_kernels_rocprof.table || exit $?
 fi
 if has traffic; then
-    for step in qkv wo wo_mlp; do
+    for step in qkv wo wi wo_mlp; do
         for c in FETCH_SIZE WRITE_SIZE; do
             echo "profile: $c of $step at 293 tokens" >&2
             timeout -s KILL 120 rocprofv3 --pmc $c -f csv -d $OUT/pmc_${step}_$c -o pmc -- \
