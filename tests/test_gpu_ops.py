@@ -168,6 +168,28 @@ def test_head_gemms(torch_cuda, scratch, kind, n, k):
     check_gemm(P, out, st, f"{kind} n={n} k={k}")
 
 
+# ---- the eight-wave latency kernel's K paths ----------------------------------------------
+# gemm_lat1 (grids of at most a block a CU) fixes its waves' K path per instance from K: wave w
+# of 8 takes K units [w U / 8, (w + 1) U / 8) of U = K / 32, all in one chunk when the busiest
+# wave has at most three (K <= 768) or five (K <= 1280) units, with a's lines staged through the
+# wave's LDS slot, else in the chunked loop. K at and around each boundary (320 and 832: waves
+# whose range starts in the middle of a 128-byte line; 1344: the first loop case), every tile
+# height, M = 293 (rows past m in the last tile). Grids: 12 or 36 column tiles x 5-19 row tiles,
+# at most 252 blocks, so the eight-wave kernel runs on a 256-CU MI355X.
+LAT1_KS = [256, 320, 768, 832, 1152, 1280, 1344, 1536, 3072]
+
+
+@pytest.mark.parametrize("k", LAT1_KS)
+@pytest.mark.parametrize("kind,n,bm", [("resstats", 768, 16), ("resstats", 768, 32),
+                                       ("lngeglu", 2304, 48), ("lnrope", 2304, 48),
+                                       ("resstats", 768, 64)])
+def test_eight_wave_latency_tile_k_paths(torch_cuda, scratch, kind, n, bm, k):
+    say(f"eight-wave latency tile {kind} M=293 N={n} K={k} bm={bm}")
+    P = gemm_problem(kind, 293, n, k, seed=71 + k + bm)
+    out, st = run_gemm(torch_cuda, P, bm, 1, scratch)
+    check_gemm(P, out, st, f"{kind} n={n} k={k} bm={bm}")
+
+
 # ---- MFMA-bound sizes ---------------------------------------------------------------------
 # Every epilogue on the throughput tiles (128 x 128 and 256 x 256), M not a multiple of either.
 BIG_EPIS = [("lnrope", 2304, 768), ("rope", 2304, 768), ("lngeglu", 2304, 768),
