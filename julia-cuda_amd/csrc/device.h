@@ -319,8 +319,15 @@ __device__ __forceinline__ int xcd_task(int b, int T) {
 //
 // Order as the reference's gemm_tile (kernels/src/main.rs:931-1038): LayerNorm from the input
 // statistics, bias, ReLU, GELU, RoPE, then GeGLU or the store with the residual and the output
-// statistics of the stored f16 values. XG: the outputs are read by other blocks of the same
-// kernel (the persistent layer kernel's next phase), so they are stored device-coherent.
+// statistics of the stored f16 values. XG: the input statistics are read device-coherent (the
+// persistent layer kernel, where other blocks of the same kernel wrote them).
+//
+// The outputs (and output statistics) are stored device-coherent on every path, written through
+// the XCD's L2. In the persistent kernel other blocks read them in the same launch; between
+// per-step kernels, a kernel's end has to write back the dirty lines its stores leave in its
+// XCD's L2 before the next kernel, on all eight XCDs, may read them. Measured on the 293-token
+// forward (same box, interleaved runs): 0.675 -> 0.655 ms a request. (The same for the attention
+// and row kernels' outputs gained nothing more.)
 //
 // Everything the epilogue reads besides the accumulator (statistics, colsum, bias, the RoPE
 // table, the residual) is loaded by epi_load_* when the tile starts, so those loads overlap the
@@ -464,7 +471,7 @@ __device__ __forceinline__ void epi_apply(const GemmParams& p, int row, int grp,
             half4 o;
 #pragma unroll
             for (int e = 0; e < 4; e++) o[e] = (f16)(gelu(v[e]) * v[4 + e]);
-            store8<XG>((f16*)p.c + (size_t)row * (p.n >> 1) + grp * 32 + c0, o);
+            store8<true>((f16*)p.c + (size_t)row * (p.n >> 1) + grp * 32 + c0, o);
         }
     } else {
         half4 lo, hi;
@@ -489,8 +496,8 @@ __device__ __forceinline__ void epi_apply(const GemmParams& p, int row, int grp,
             s = group_sum<8>(s);
             if (valid && (threadIdx.x & 7) == 0) xstore32(p.ws + (size_t)row * p.tiles_n + grp, s);
         } else if (valid) {
-            store8<XG>(out, lo);
-            store8<XG>(out + 32, hi);
+            store8<true>(out, lo);
+            store8<true>(out + 32, hi);
         }
         if (EPI & EPI_STATS) {
             float s = 0.0f, q = 0.0f;
@@ -503,7 +510,7 @@ __device__ __forceinline__ void epi_apply(const GemmParams& p, int row, int grp,
             s = group_sum<8>(s);
             q = group_sum<8>(q);
             if (valid && (threadIdx.x & 7) == 0) {
-                store8<XG>(p.stats_out + ((size_t)row * (p.n >> 6) + grp) * 2, make_float2(s, q));
+                store8<true>(p.stats_out + ((size_t)row * (p.n >> 6) + grp) * 2, make_float2(s, q));
             }
         }
     }
