@@ -386,8 +386,11 @@ void gemm_launch_static(const Gemm& g, GemmConfig cfg, hipStream_t st) {
 //    for one round, 48.7-55 for two, 82 for three).
 //  - 192 x 256 tiles (one a CU): ~2 us plus ~21.7 us per round (0.82 of the 256-row round:
 //    23.3-24.4, 42.5-45.9, 66.1, 89.5 us for one to four rounds).
+// The throughput tiles enter from 640 rows (below, the latency tiles win by the model and by
+// measurement: qkv at 448 rows 6.7 us on 64-row tiles against 10.5 on 128 x 128; at 600 level).
 // Measured winners it reproduces: 48-row tiles for qkv and wi at 293 tokens, 16-row for wo and
-// wo_mlp; 128 x 128 for qkv at 1024-3072 and 8192 rows and for wo and wo_mlp from 2048 to 8192;
+// wo_mlp; 64-row for qkv and wi at 448; 128 x 128 for qkv and wi at 800 rows (10.7 us against
+// 12.3 for 64-row latency tiles) and 1024-3072 and 8192, and for wo and wo_mlp from 2048 to 8192;
 // 192 x 256 for qkv and wi at 4096; 256 x 256 at 6144 and 12288 (qkv, wi) and everything at
 // 18752.
 GemmConfig gemm_choose(int m, int n, int k, int cus, int epi) {
@@ -401,7 +404,7 @@ GemmConfig gemm_choose(int m, int n, int k, int cus, int epi) {
         const double cost = 4.0 + (double)per_cu * (bm + 64) * k * 2 / 55e3;
         if (cost < best_cost - 0.05) best_cost = cost, best = GemmConfig{bm, 1};
     }
-    if (m >= 1024 && n % 128 == 0 && k % 64 == 0 && !((epi & EPI_LN) && k > GEMM_BIG_LN_MAX_K)) {
+    if (m >= 640 && n % 128 == 0 && k % 64 == 0 && !((epi & EPI_LN) && k > GEMM_BIG_LN_MAX_K)) {
         const double ks = (double)k / 768.0;
         const long l128 = ((long)(n / 128) * ((m + 127) / 128) + cus - 1) / cus;
         const double c128 = 2.0 + 8.5 * ks * (double)l128;

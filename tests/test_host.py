@@ -324,6 +324,14 @@ def test_chooser_matches_the_measured_winners():
     assert jh.gemm_choose(293, 768, 768, 256)[0] == 16
     assert jh.gemm_choose(293, 768, 1152, 256)[0] == 16
     assert jh.gemm_choose(448, 768, 768, 256)[0] == 32
+    # 448 tokens: 64-row tiles for qkv (252 tiles, the eight-wave kernel: 6.7 us against 10.4-12.0
+    # for 16/32/48 and 10.5 for 128 x 128); 800: 128 x 128 for qkv (10.7 us against 12.3 for the
+    # 64-row latency tiles), latency tiles for wo and wo_mlp (5.6 and 6.8 us on 48 rows against
+    # 9.5 and 12.0 on 128 x 128)
+    assert jh.gemm_choose(448, 2304, 768, 256)[0] == 64
+    assert jh.gemm_choose(800, 2304, 768, 256) == (128, 1)
+    assert jh.gemm_choose(800, 768, 768, 256)[0] == 48
+    assert jh.gemm_choose(800, 768, 1152, 256)[0] == 48
     assert jh.gemm_choose(18752, 2304, 768, 256) == (256, 1)
     assert jh.gemm_choose(4096, 768, 768, 256) == (128, 1)
     assert jh.gemm_choose(18752, 768, 768, 256) == (256, 1)
