@@ -212,7 +212,7 @@ def gemm_instance(m, n, k, bm, epi, cus):
         return f"gemm_big<{bm}, {jh.EPI[epi]}, false>"
     if (n // 64) * -(-m // bm) <= cus and k >= 256:  # the eight-wave instance: a block a CU at most
         most = (k // 32 + 7) // 8  # K steps of the busiest wave: its K path
-        path = 3 if most <= 3 else 5 if most <= 5 else 1
+        path = 3 if most <= 3 else 5 if most <= 5 else 6 if most <= 6 and bm <= 32 else 1
         return f"gemm_lat1<{bm}, {jh.EPI[epi]}, {path}>"
     return f"gemm_lat<{bm}, {jh.EPI[epi]}>"
 

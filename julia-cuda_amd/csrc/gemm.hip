@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256, 2) void gemm_lat(GemmParams p) {
 // waves split the tile's K steps, each issuing all of its three to five steps' loads at once. A
 // CU takes in its operands from L2 faster with eight waves loading than with four (measured on
 // MI355X: ~86-94 against ~55-79 GB/s), for twice the partial tiles to sum through LDS. KP: the
-// waves' K path (LAT_KONE3 / LAT_KONE5 / LAT_KLOOP), chosen by the host from K. Dynamic LDS:
+// waves' K path (LAT_KONE3 / 5 / 6, LAT_KLOOP), chosen by the host from K and BM. Dynamic LDS:
 // lat_lds_floats<BM, 8>() floats.
 template <int BM, int EPI, int KP>
 __global__ __launch_bounds__(512, 1) void gemm_lat1(GemmParams p) {
@@ -206,11 +206,12 @@ static void launch_lat1(const GemmParams& p, int blocks, hipStream_t st) {
     hipLaunchKernelGGL((gemm_lat1<BM, EPI, KP>), dim3(blocks), dim3(512), LDS, st, p);
 }
 
-// The eight-wave kernel's K path for K: wave w of 8 takes K steps [w U / 8, (w + 1) U / 8) of
-// U = K / 32, at most ceil(U / 8).
-static int gemm_lat1_path(int k) {
+// The eight-wave kernel's K path for K and the tile height: wave w of 8 takes K steps
+// [w U / 8, (w + 1) U / 8) of U = K / 32, at most ceil(U / 8); six in one chunk for tiles of up
+// to 32 rows (K = 1536: the head's linear2, 6.8 us on the chunked loop).
+static int gemm_lat1_path(int k, int bm) {
     const int most = (k / 32 + 7) / 8;
-    return most <= 3 ? LAT_KONE3 : most <= 5 ? LAT_KONE5 : LAT_KLOOP;
+    return most <= 3 ? LAT_KONE3 : most <= 5 ? LAT_KONE5 : most <= 6 && bm <= 32 ? LAT_KONE6 : LAT_KLOOP;
 }
 
 template <int BM, int EPI>
@@ -218,9 +219,12 @@ static void launch_lat(const GemmParams& p, hipStream_t st) {
     const int blocks = p.tiles_n * p.tiles_m * p.splits;
     // (Eight waves with a K step each: K >= 256.)
     if (p.splits == 1 && blocks <= device_cus() && p.k >= 256) {
-        switch (gemm_lat1_path(p.k)) {
+        switch (gemm_lat1_path(p.k, BM)) {
             case LAT_KONE3: launch_lat1<BM, EPI, LAT_KONE3>(p, blocks, st); break;
             case LAT_KONE5: launch_lat1<BM, EPI, LAT_KONE5>(p, blocks, st); break;
+            case LAT_KONE6:
+                if constexpr (BM <= 32) launch_lat1<BM, EPI, LAT_KONE6>(p, blocks, st);
+                break;
             default: launch_lat1<BM, EPI, LAT_KLOOP>(p, blocks, st); break;
         }
     } else {

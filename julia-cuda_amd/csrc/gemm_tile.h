@@ -11,9 +11,11 @@ namespace jh {
 
 // The LDS slot (floats) of one wave of a BM-row latency tile: its partial BM x 64 tile (rows
 // padded to 68 floats); with eight waves also its staged activation lines first (lat_stage_lines
-// lines of 128 bytes a row: 32 floats each), when they fit the CU's 160 KB.
+// lines of 128 bytes a row: 32 floats each), as many of four, three or two as fit the CU's 160 KB.
 template <int BM, int NW>
-constexpr int lat_stage_lines() { return NW != 8 ? 0 : (8 * BM * 96 * 4 <= 150 * 1024 ? 3 : 2); }
+constexpr int lat_stage_lines() {
+    return NW != 8 ? 0 : 8 * BM * 128 * 4 <= 150 * 1024 ? 4 : 8 * BM * 96 * 4 <= 150 * 1024 ? 3 : 2;
+}
 template <int BM, int NW>
 constexpr int lat_slot_floats() {
     return BM * 68 > BM * 32 * lat_stage_lines<BM, NW>() ? BM * 68 : BM * 32 * lat_stage_lines<BM, NW>();
@@ -23,12 +25,13 @@ template <int BM, int NW = 4>
 constexpr int lat_lds_floats() { return NW * lat_slot_floats<BM, NW>(); }
 
 // The K path of an eight-wave latency tile's waves, when the kernel fixes it: every wave in one
-// chunk of three or five K steps (LAT_KONE3, LAT_KONE5) or in the chunked loop (LAT_KLOOP);
+// chunk of three, five or six K steps (LAT_KONE3, LAT_KONE5, LAT_KONE6: tiles of up to 32 rows,
+// whose six steps' four lines of a a row fit the LDS) or in the chunked loop (LAT_KLOOP);
 // LAT_KANY chooses per wave at run time. One path per kernel keeps the waits exact: the compiler
 // joins run-time alternatives into one flow, and each alternative then waits for the loads the
 // others might have left in flight (measured in the generated code: a full wait ahead of the
 // three-step chunk's weight loads, for the other paths' RoPE table loads).
-enum { LAT_KANY = 0, LAT_KLOOP = 1, LAT_KONE3 = 3, LAT_KONE5 = 5 };
+enum { LAT_KANY = 0, LAT_KLOOP = 1, LAT_KONE3 = 3, LAT_KONE5 = 5, LAT_KONE6 = 6 };
 
 // Rows of one epilogue pass of a four-wave latency tile (256 threads, 8 a row): the unit in which
 // a K split's partial tile is stored (gemm_ws_floats sizes the scratch by it). Only four-wave
@@ -151,14 +154,16 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
     const int U = p.k >> 5;
     const int ub = z * U / p.splits, ue = (z + 1) * U / p.splits, nu = ue - ub;
     const int u0 = ub + w * nu / NW, u1 = ub + (w + 1) * nu / NW;
-    // Eight waves, each with its K steps in one chunk (up to 40 steps a split): the waves'
+    // Eight waves, each with its K steps in one chunk (up to 40 steps a split; 48 on the six-step
+    // path): the waves'
     // partials are summed in two halves. The operands reach the CU in the order the waves issued
     // their loads, so waves 4-7 (each the second wave of its SIMD) finish ~1.5 us after waves
     // 0-3 (293 rows, K = 768), and waves 0-3 sum their four partials in that time; after the
     // last wave only the half sum and four partials remain. The late waves pass the first barrier
     // right after issuing their loads. The sums run in wave order either way (the values do not
     // depend on which half finishes first).
-    const bool two = NW == 8 && (nu + NW - 1) / NW <= 5;  // block-uniform: every wave takes kone
+    // (block-uniform: every wave takes kone)
+    const bool two = NW == 8 && (KP == LAT_KONE6 || (nu + NW - 1) / NW <= 5);
     const bool late = two && w >= NW / 2;
 
     const f16* ap[MI];
@@ -205,6 +210,9 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
         stage_a(std::integral_constant<int, 2>{});
     } else if constexpr (KP == LAT_KONE5) {
         if constexpr (NLS >= 3) stage_a(std::integral_constant<int, 3>{});
+    } else if constexpr (KP == LAT_KONE6) {
+        static_assert(NLS >= 4, "six K steps' lines staged");
+        stage_a(std::integral_constant<int, 4>{});
     } else if constexpr (KP == LAT_KANY) {
         const int nuw = u1 - u0;
         if (NW == 8 && nuw <= 3 && NLS >= 2) stage_a(std::integral_constant<int, 2>{});
@@ -372,6 +380,8 @@ __device__ __forceinline__ void gemm_lat_tile(const GemmParams& p, int task, flo
         kone(std::integral_constant<int, 3>{}, ST2{});
     } else if constexpr (KP == LAT_KONE5) {
         kone(std::integral_constant<int, 5>{}, ST3{});
+    } else if constexpr (KP == LAT_KONE6) {
+        kone(std::integral_constant<int, 6>{}, std::true_type{});
     } else if (KP == LAT_KANY && NW == 8 && u1 - u0 <= 3) {
         kone(std::integral_constant<int, 3>{}, ST2{});
     } else if (KP == LAT_KANY && NW == 8 && u1 - u0 <= 5) {

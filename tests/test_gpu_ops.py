@@ -171,10 +171,11 @@ def test_head_gemms(torch_cuda, scratch, kind, n, k):
 # ---- the eight-wave latency kernel's K paths ----------------------------------------------
 # gemm_lat1 (grids of at most a block a CU) fixes its waves' K path per instance from K: wave w
 # of 8 takes K units [w U / 8, (w + 1) U / 8) of U = K / 32, all in one chunk when the busiest
-# wave has at most three (K <= 768) or five (K <= 1280) units, with a's lines staged through the
-# wave's LDS slot, else in the chunked loop. K at and around each boundary (320 and 832: waves
-# whose range starts in the middle of a 128-byte line; 1344: the first loop case), every tile
-# height, M = 293 (rows past m in the last tile). Grids: 12 or 36 column tiles x 5-19 row tiles,
+# wave has at most three (K <= 768), five (K <= 1280) or, on tiles of up to 32 rows, six
+# (K <= 1536) units, with a's lines staged through the wave's LDS slot, else in the chunked
+# loop. K at and around each boundary (320, 832 and 1344: waves whose range starts in the middle
+# of a 128-byte line; 1344 and 1536 on 48 and 64 rows, and 3072: the loop), every tile height,
+# M = 293 (rows past m in the last tile). Grids: 12 or 36 column tiles x 5-19 row tiles,
 # at most 252 blocks, so the eight-wave kernel runs on a 256-CU MI355X.
 LAT1_KS = [256, 320, 768, 832, 1152, 1280, 1344, 1536, 3072]
 
