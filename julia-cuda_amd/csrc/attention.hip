@@ -68,8 +68,10 @@ bool attention_prepare() {
                             hipFuncAttributeMaxDynamicSharedMemorySize, att_lds_bytes(512, 4)) == hipSuccess &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(attention_lds_kernel<8>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, att_lds_bytes(512, 8)) == hipSuccess &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(attention_streamk_kernel<2, 2>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, 2 * ATT_STREAM_LDS) == hipSuccess &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(attention_streamk_kernel<1, 4>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 4 * ATT_STREAM_LDS) == hipSuccess &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(attention_streamk_kernel<2, 4>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, 4 * ATT_STREAM_LDS) == hipSuccess &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(attention_streamk_kernel<4, 2>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, 2 * ATT_STREAM_LDS) == hipSuccess &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(attention_streamk_kernel<4, 4>),
@@ -77,13 +79,18 @@ bool attention_prepare() {
     return ok;
 }
 
+// 32-key steps a 16-query slice takes over the keys it reaches (from a 32-aligned start; up to
+// 512 keys at once).
+int attention_slice_steps(int n, int window) {
+    const int reach = window > 0 ? std::min(n, 16 + 2 * window) + 31 : n;
+    return (std::min(reach, attention_gkeys(n, window)) + 31) / 32;
+}
+
 // Waves per block of the LDS-resident kernel: eight when a slice takes more than four key steps
 // and the grid is at most a block a CU (measured: with two blocks on some CUs, eight-wave blocks
 // lose to four-wave ones, e.g. a +-64 window over 448 rows, 5.2 against 4.8 us).
 int attention_slice_waves(int n, int d, int window) {
-    const int gkeys = attention_gkeys(n, window);
-    const int reach = window > 0 ? std::min(n, 16 + 2 * window) + 31 : n;
-    if ((std::min(reach, gkeys) + 31) / 32 <= 4) return 4;
+    if (attention_slice_steps(n, window) <= 4) return 4;
     const long blocks = (long)(n + 15) / 16 * (d / 64);
     return blocks <= device_cus() ? 8 : 4;
 }
@@ -125,24 +132,39 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
     if (seg && chunks != 1) fail("concatenated sequences take one key range");
     if (seg && ((uintptr_t)seg % 8)) fail("seg must be 8-byte aligned");
     AttnParams p{qkv, o, n, d, window, chunks, s.ws, s.counters, seg};
-    // One key range: the tile by measured crossovers (MI355X, one sequence, us; slice tile
-    // with 4 / 8 waves, streaming tile with waves x key groups 2 x 2 / 4 x 2 / 4 x 1):
-    //   global   293 rows  5.5 / 5.1 | 5.0 / 5.9 / 6.0      1024 rows 28.3 / 21.2 | 10.7 / 10.8 / 12.7
-    //            2048 rows 98 / 68   | 30.1 / 27.5 / 28.8   4096 rows (4 x 2 / 4 x 1) 85.4 / 82.5
+    // One key range: the tile by measured crossovers (MI355X, one sequence, us). The slice
+    // tile with 4 / 8 waves against the streaming tile with waves x key groups 1 x 4 / 2 x 2 /
+    // 2 x 4 (d = 768 unless noted):
+    //   global   72 rows  3.6 / 3.8 | 3.7 / 3.7 / 4.0     150 rows  4.3 / 4.1 | 3.9 / 4.3 / 4.5
+    //            293 rows 5.5 / 5.1 | 4.7 / 5.1 / 5.2     336 rows  5.8 / 5.1 | 4.9 / 5.3 / 5.4
+    //            352 rows 8.2 / 8.2 | 8.1 / 5.3 / 5.4     400 rows  9.5 / 8.8 | 8.5 / 5.9 / 5.7
+    //            600 rows 2 x 2 / 2 x 4: 7.0 / 6.7        d = 384, 672 rows 8.5 / 6.7 | 6.2 / 7.4 / 6.8
+    //   +-64     150 rows 4.2 / 4.1 | 3.9 / 4.3 / 4.5     293 rows  4.3 / 4.2 | 3.9 / 4.4 / 4.5
+    //            400 rows 4.5 / 5.2 | 6.3 / 4.4 / 4.6     d = 384, 672 rows 4.3 / 4.2 | 3.9 / 4.4 / 4.5
+    // so one wave of 16 queries a key group, four groups (a task per 16-query slice and head,
+    // each group a quarter of the key blocks), wherever that grid fits the CUs and a slice takes
+    // more than four 32-key steps. Past that grid (and from earlier measurements, slice tile
+    // against the streaming tile's 2 x 2 / 4 x 2 / 4 x 1):
+    //   global   1024 rows 28.3 / 21.2 | 10.7 / 10.8 / 12.7   2048 rows 98 / 68 | 30.1 / 27.5 / 28.8
+    //            4096 rows (4 x 2 / 4 x 1) 85.4 / 82.5
     //   +-64     700 rows  4.9 / 6.6 | 5.0 / 5.1 / 5.0      1024 rows 5.3 / 7.1 | 5.3 / 5.3 / 5.0
     //            1536 rows 7.9 / 10.4 | 7.9 / 6.8 / 6.1
     // and four key groups of four waves (one 1024-thread block a CU) against 2 x 2 / 4 x 2:
     //   global   448 rows 6.9 against 5.6 / 6.7     768 rows 8.8 against 8.9 / 9.0
     //            1024 rows 10.5 against 11.1 / 11.0  1536 rows 25.4 against 24.1 / 22.4
-    // so the slice tile below 293 rows (global) or 768 (window), else the streaming tile: two
-    // key groups of two waves while that grid fits the CUs, then four groups of four while
-    // their grid does, two of four while the four-wave grid is at most two blocks a CU
-    // (global), one group of four otherwise (config 5's batch: 4 x 1 48 us a global layer
-    // against 59 for 4 x 2).
+    // so the slice tile for the shortest inputs (global) and up to 768 rows (window), else the
+    // streaming tile: four key groups of two waves while that grid fits the CUs, then four
+    // groups of four while their grid does, two of four while the four-wave grid is at most two
+    // blocks a CU (global), one group of four otherwise (config 5's batch: 4 x 1 48 us a global
+    // layer against 59 for 4 x 2).
     const int cus = device_cus();
     const long grid64 = (long)(n + 63) / 64 * (d / 64), grid32 = (long)(n + 31) / 32 * (d / 64);
+    const long grid16 = (long)(n + 15) / 16 * (d / 64);
     const bool slice = chunks == 1 && (window == 0 ? n < 293 : n <= 768);
-    if (slice) {
+    if (chunks == 1 && grid16 <= cus && attention_slice_steps(n, window) > 4) {
+        if (!attention_prepare()) fail("the multi-group streaming kernels cannot have their LDS");
+        hipLaunchKernelGGL((attention_streamk_kernel<1, 4>), dim3(grid16), dim3(256), 4 * ATT_STREAM_LDS, st, p);
+    } else if (slice) {
         if (!attention_prepare()) fail("the LDS-resident kernel cannot have its LDS");
         const int gkeys = attention_gkeys(n, window);
         const dim3 grid((n + 15) / 16 * (d / 64));
@@ -153,7 +175,7 @@ void attention_launch(const jh_half* qkv, jh_half* o, int n, int d, int window, 
     } else if (chunks == 1) {
         if (!attention_prepare()) fail("the multi-group streaming kernels cannot have their LDS");
         if (window == 0 && grid32 <= cus)
-            hipLaunchKernelGGL((attention_streamk_kernel<2, 2>), dim3(grid32), dim3(256), 2 * ATT_STREAM_LDS, st, p);
+            hipLaunchKernelGGL((attention_streamk_kernel<2, 4>), dim3(grid32), dim3(512), 4 * ATT_STREAM_LDS, st, p);
         else if (window == 0 && grid64 <= cus)
             hipLaunchKernelGGL((attention_streamk_kernel<4, 4>), dim3(grid64), dim3(1024), 4 * ATT_STREAM_LDS, st, p);
         else if (window == 0 && grid64 <= 2 * cus)

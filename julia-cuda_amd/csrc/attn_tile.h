@@ -475,7 +475,9 @@ __device__ __forceinline__ void attention_slice_tile(const AttnParams& p, int ta
 // block barrier a step for all); groups 1 .. KS - 1 then pass their running max, sum and
 // output through LDS and group 0 merges them (in group order: deterministic). Two or four
 // waves a SIMD instead of one hide each other's step latencies where the grid leaves the CUs
-// a block each, and the chain of steps is KS times shorter.
+// a block each, and the chain of steps is KS times shorter. NW = 1, KS = 4 (short inputs: a
+// task per 16-query slice and head, the grid about a block a CU): four single-wave groups, each
+// issuing all 16 copies of its stages, so a slice's few key blocks are spread over four waves.
 constexpr int ATT_STREAM_STAGES = 2;
 constexpr int ATT_STREAM_LDS = ATT_STREAM_STAGES * 16384;
 
@@ -559,7 +561,7 @@ __device__ __forceinline__ void attention_stream_tile(const AttnParams& p, int t
     static_assert(KS == 1 || KS == 2 || KS == 4, "key groups");
     constexpr int NS = ATT_STREAM_STAGES, QB = 16 * NW;
     constexpr int LOADS = 16 / NW;  // 1 KB copies a wave per stage
-    static_assert(NW == 2 || NW == 4 || NW == 8, "waves");
+    static_assert(NW == 1 || NW == 2 || NW == 4 || NW == 8, "waves");
     const int n = p.n, d = p.d, ld = 3 * d, heads = d >> 6;
     const int tiles = (n + QB - 1) / QB;
     const int L = xcd_task(task, tiles * heads);

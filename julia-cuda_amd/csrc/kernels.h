@@ -156,6 +156,7 @@ int attention_chunks(int n, int d, int window, int cus);
 int attention_gkeys(int n, int window);
 bool attention_prepare();
 int attention_slice_waves(int n, int d, int window);  // 4 or 8 (needs the device)
+int attention_slice_steps(int n, int window);
 
 void embed_launch(const uint32_t* ids, int n, const jh_half* table, int vocab, int d,
                   const float* gamma, float eps, jh_half* x, hipStream_t stream);

@@ -266,12 +266,13 @@ def test_config3_attention(torch_cuda, scratch, n, window, chunks):
     say(f"  vs f64 {rel:.2e} (max {mrel:.2e}), vs emulation {erel:.2e}")
 
 
-@pytest.mark.parametrize("lens", [[300, 1024, 17, 700, 1, 513], [70, 130, 45, 200, 64]])
+@pytest.mark.parametrize("lens", [[300, 1024, 17, 700, 1, 513], [70, 130, 45, 200, 64], [70, 130, 45, 64]])
 @pytest.mark.parametrize("window", [0, 64])
 def test_attention_over_concatenated_sequences(torch_cuda, scratch, lens, window):
     """Config 5's batched attention: sequences concatenated into one set of rows, each query
-    seeing only its own sequence's keys (past 2048 rows the streaming 64-query tile, below it the
-    slice tile), against the f64 attention of each sequence alone."""
+    seeing only its own sequence's keys (past 2048 rows the streaming 64-query tile; 509 rows the
+    slice tile or, global, 2 x 4 streaming waves; 309 rows four single-wave key groups), against
+    the f64 attention of each sequence alone."""
     say(f"attention over {len(lens)} sequences ({sum(lens)} rows) window={window}")
     torch = torch_cuda
     n = sum(lens)
@@ -312,12 +313,14 @@ def test_attention_d384_and_tail(torch_cuda, scratch):
 @pytest.mark.parametrize("window", [0, 64])
 def test_attention_at_the_routing_edges(torch_cuda, scratch, window):
     """One sequence at d=768 on both sides of every size where attention_launch changes tile
-    (global: the slice tile below 293 rows, then the streaming tile with 2 x 2 waves up to 682
-    rows, 4 x 4 up to 1365, 4 x 2 up to 2730, 4 x 1 past it; window: the slice tile up to 768
-    rows, then the streaming tile), and at lengths around the 16-, 32- and 64-row block edges,
-    against the f64 attention."""
+    (global: the slice tile up to 128 rows, the streaming tile with four single-wave key groups
+    up to 336 rows, then 2 x 4 waves up to 682 rows, 4 x 4 up to 1365, 4 x 2 up to 2730, 4 x 1
+    past it; window: the slice tile up to 97 rows, four single-wave key groups up to 336, the
+    slice tile up to 768 rows, then the streaming tile), and at lengths around the 16-, 32- and
+    64-row block edges, against the f64 attention."""
     torch = torch_cuda
-    for n in (2, 17, 63, 64, 65, 129, 292, 293, 400, 682, 683, 768, 769, 1365, 1366, 2730, 2731):
+    for n in (2, 17, 63, 64, 65, 97, 98, 128, 129, 292, 293, 336, 337, 400, 682, 683, 768, 769,
+              1365, 1366, 2730, 2731):
         rng = np.random.default_rng(900 + n + window)
         qkv16 = rand16(rng, (n, 3 * 768))
         ref = O.attention(f32(qkv16), window)
