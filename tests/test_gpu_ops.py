@@ -295,9 +295,11 @@ def test_attention_over_concatenated_sequences(torch_cuda, scratch, lens, window
 
 def test_attention_d384_and_tail(torch_cuda, scratch):
     """The real Julia-1 width (6 heads) and a length that is not a multiple of 64 (2048 rows:
-    the streaming tile with four key groups)."""
+    the streaming tile with four key groups); 672 / 673 rows are the two sides of the largest
+    grid of single-wave key groups that fits 256 CUs at this width."""
     torch = torch_cuda
-    for n, window in [(363, 64), (363, 0), (450, 0), (1, 0), (65, 64), (2048, 0)]:
+    for n, window in [(363, 64), (363, 0), (450, 0), (1, 0), (65, 64), (2048, 0), (672, 0),
+                      (673, 0), (672, 64), (673, 64)]:
         say(f"attention d=384 n={n} window={window}")
         rng = np.random.default_rng(7 + n)
         qkv16 = rand16(rng, (n, 3 * 384))
