@@ -13,12 +13,16 @@
 // With `chunks` > 1 the key blocks of each (query block, head) tile are split into ranges, one
 // block each; every range writes its unnormalised output, max and sum to the scratch and the
 // last one of the tile to arrive merges them in range order (kernels/src/attn.rs:92-204).
-// With one range, short key ranges take the LDS-resident query-slice tile (attn_tile.h: 16
-// queries per block, the key range staged at once and split between the waves, V^T fragments
-// from the transposing LDS read): the latency shape for one request of a few hundred tokens.
-// Long ones (global attention from ~400 rows, windows past ~1500 rows, config 5's concatenated
-// requests) take the streaming tile, which loads each key once per 64 queries instead of once
-// per 16 (att_use_stream).
+// With one range, attention_launch picks the tile by measured crossovers (the table there):
+// - one request of a few hundred tokens (a 16-query grid of at most a block a CU): the
+//   streaming tile (attn_tile.h) with a task per 16-query slice and head and four single-wave
+//   key groups, each taking every fourth 64-key block;
+// - the shortest inputs, and windows up to 768 rows past that grid: the LDS-resident slice tile
+//   (16 queries per block, the key range staged at once and split between the waves);
+// - longer ones (config 5's concatenated requests among them): the streaming tile with 16 NW
+//   queries a task and KS key groups, which loads each key once per 16 NW queries.
+// (The persistent kernel chooses between the slice and the streaming tile itself:
+// att_use_stream.)
 #include <algorithm>
 #include <stdexcept>
 #include <string>
