@@ -3,12 +3,15 @@
 // kernels/src/main.rs:886-1041) walks K through shared tiles with 4-8 warps each owning a
 // piece of the output; here two kernels cover the two regimes of a 256-CU GPU:
 //
-//  - gemm_lat (BM = 16/32/64 rows x 64 columns): the small-M, latency-bound regime of one
-//    request (M = 72-1024). Its four waves split K between them (each streams its own a and w
-//    fragments straight from L2 into registers, two K steps in flight, no LDS staging) and
-//    reduce their partial tiles through LDS, so a tile's serial K loop is a quarter as long and
-//    there are more tiles to spread over 256 CUs. Grid split-K on top is deterministic: the
-//    last block of a tile to arrive sums every split's partial in split order.
+//  - gemm_lat / gemm_lat1 (BM = 16/32/48/64 rows x 64 columns): the small-M, latency-bound
+//    regime of one request (M = 72-1024). The block's waves split K between them and reduce
+//    their partial tiles through LDS, so a tile's serial K loop is short and there are more
+//    tiles to spread over 256 CUs. gemm_lat1, for grids of at most a block a CU (every latency
+//    GEMM of a 293-token request), runs eight waves, copies each wave's range of a into LDS as
+//    whole 128-byte lines and fixes the waves' K path per kernel instance (gemm_tile.h);
+//    gemm_lat runs four waves streaming a and w fragments from L2 into registers, two blocks a
+//    CU. Grid split-K on top is deterministic: the last block of a tile to arrive sums every
+//    split's partial in split order.
 //  - gemm_big (128 x 128, 192 x 256 or 256 x 256 tiles): the MFMA-bound regime (M >= 2048): a
 //    and w tiles copied into four LDS stages by direct buffer -> LDS loads (gemm_big.h), four or
 //    eight waves each owning a 64 x 64 (96 x 64, 128 x 64) output block on 32 x 32 x 16 MFMA, the
