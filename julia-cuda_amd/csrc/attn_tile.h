@@ -16,11 +16,11 @@ constexpr int ATT_SLICE_ROWS = 2048;
 
 // Which tile one key range takes in the persistent kernel, which compiles these two (the
 // per-step kernels choose in attention_launch; measured on MI355X, one sequence, heads of 64):
-// the slice tile while a query's keys are few (global attention under ~400 rows: 293 rows 5.2 us against
-// 7.4; a +-64 window up to ~1500 rows: 1024 rows 5.4 against 6.0), the streaming tile past
-// that (global 448 rows 9.0 us against 9.3, 1024 rows 17.1 against 21.3; window 2048 rows 7.2
-// against 9.2), where the slice tile's per-slice restaging of every key costs more than it
-// saves in latency.
+// the slice tile while a query's keys are few (global attention under ~400 rows: 293 rows
+// 5.2 us against 7.4; a +-64 window up to ~1500 rows: 1024 rows 5.4 against 6.0), the
+// streaming tile past that (global 448 rows 9.0 us against 9.3, 1024 rows 17.1 against 21.3;
+// window 2048 rows 7.2 against 9.2), where the slice tile's per-slice restaging of every key
+// costs more than it saves in latency.
 __host__ __device__ constexpr bool att_use_stream(int n, int window) {
     return n > ATT_SLICE_ROWS || (window == 0 ? n >= 400 : n > 1536);
 }
